@@ -1,0 +1,225 @@
+/*
+ * coli_hip.h - C ABI of libcoli_hip.so, the MI355X (gfx950) replacement for the
+ * Vulkan backend of zhaohb/qwen3.c.
+ *
+ * Part 1 declares every entry point of the reference's c/backend_vulkan.h with the same
+ * name, signature and return convention, so c/qwen.c builds and links against this
+ * library unchanged (backend_vulkan.h in this directory forwards here).  Each comment
+ * cites the reference declaration it replaces.  Conventions kept from the reference:
+ *   - int 1 = success, 0 = unavailable / failed -> the caller computes on the CPU
+ *     (c/backend_vulkan.h:55-57, c/qwen.c:296-308);
+ *   - a device failure is sticky: every later call returns 0 (c/backend_vulkan.c:1280);
+ *   - tensors are created lazily through the in/out ColiVkTensor** handle and own a
+ *     device copy of the caller's host weights (c/backend_vulkan.c:1055-1085);
+ *   - one host thread; at most one expert group in flight (c/backend_vulkan.c:1648).
+ * Entry points for the GLM (MLA absorb) paths, which c/qwen.c never calls, return 0.
+ *
+ * Part 2 (coli_hip_*) has no counterpart in the reference: device-pointer forms of the
+ * hot path for callers whose inputs already live in HBM (the benchmark, the parity
+ * tests, a device-resident engine), plus the device synthetic-data generator.
+ *
+ * Plain pointers and sizes only.  `void *stream` is a hipStream_t (NULL = the
+ * library's own stream); work issued on it is stream-ordered and not synchronised.
+ */
+#ifndef COLI_HIP_H
+#define COLI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* c/backend_vulkan.h:33 - opaque device copy of one quantized tensor.  fmt 6 (grouped
+ * asymmetric int4, [scale, zero] f32 per group) and fmt 1 (int8, f32 per-row scale) as
+ * in the reference; fmt 0 (plain f32 rows, scales NULL) is an addition used for the f32
+ * MoE router. */
+typedef struct ColiVkTensor ColiVkTensor;
+
+/* ======================= Part 1: the drop-in ABI ======================= */
+
+/* c/backend_vulkan.h:37-40 */
+int  coli_vk_init(const char *spv_path);            /* spv_path ignored (kernels are built in) */
+void coli_vk_shutdown(void);
+int  coli_vk_available(void);
+void coli_vk_mem_info(size_t *used_bytes, size_t *tensor_count);
+/* c/backend_vulkan.h:49-50 (no eviction classes on HBM: alloc_priority is a no-op) */
+void coli_vk_alloc_priority(float p);
+int  coli_vk_mem_budget(double *used_gb, double *budget_gb);
+
+/* c/backend_vulkan.h:56-59: y[S,O] = x[S,I] @ dequant(W)^T */
+int  coli_vk_matmul(ColiVkTensor **tensor, float *y, const float *x,
+                    const void *weights, const float *scales,
+                    int fmt, int S, int I, int O, int gs);
+/* c/backend_vulkan.h:66-68: lm_head GEMV + device argmax, ties -> lowest index */
+int  coli_vk_matmul_argmax(ColiVkTensor **tensor, const void *weights, const float *scales,
+                           int fmt, int I, int O, int gs,
+                           const float *x, int *idx, float *val);
+/* c/backend_vulkan.h:75-79: hidden[s,o] = silu(gate(x)) * up(x) */
+int  coli_vk_gate_up(ColiVkTensor **gate, ColiVkTensor **up, float *hidden, const float *x,
+                     const void *gw, const float *gs, const void *uw, const float *us,
+                     int fmt, int S, int D, int I, int grp);
+/* c/backend_vulkan.h:85-101: batched expert MLP y_c = down_c(silu(gate_c x_c) * up_c x_c) */
+int  coli_vk_expert_group(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                          ColiVkTensor *const *downs, const int *rows, int count,
+                          float *y, const float *x);
+int  coli_vk_expert_group_issue(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                ColiVkTensor *const *downs, const int *rows, int count,
+                                const float *x);
+int  coli_vk_expert_group_take(float *y);
+int  coli_vk_eg_gather_available(void);
+int  coli_vk_eg_xs_bind(const float *xs, int S, int D);
+int  coli_vk_expert_group_issue_id(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                   ColiVkTensor *const *downs, const int *rows, int count,
+                                   const int *tok_ids);
+/* c/backend_vulkan.h:105 */
+int  coli_vk_tensor_ensure(ColiVkTensor **tensor, const void *weights, const float *scales,
+                           int fmt, int I, int O, int grp);
+/* c/backend_vulkan.h:114-122, 125-131, 138-141: GLM MLA paths (unused by c/qwen.c): return 0 */
+int  coli_vk_kv_ensure(int layer, int max_rows, int K, int Rd);
+int  coli_vk_kv_row(int layer, int pos, const float *L, const float *R);
+void coli_vk_kv_reset(void);
+int  coli_vk_attention_absorb(ColiVkTensor **kvb, const void *w, const float *sc, int fmt, int grp,
+                              float *ctx, const float *q, int layer, int S, int H,
+                              int Q, int R, int V, int K, int st0, int T, float scale);
+int  coli_vk_attn_qprep(int layer,
+                        ColiVkTensor **qa,  const void *wqa,  const float *sqa,  int Oqa,
+                        ColiVkTensor **kva, const void *wkva, const float *skva, int Okva,
+                        ColiVkTensor **qb,  const void *wqb,  const float *sqb,  int Oqb,
+                        int fmt, int grp, const float *lnw, float eps,
+                        const float *x, int S, int I, float *q_out, float *kv_out,
+                        float *lat_out);
+/* c/backend_vulkan.h:132-134: two GEMVs sharing x, one synchronisation */
+int  coli_vk_matmul_pair(ColiVkTensor **t1p, float *y1, const void *w1, const float *s1, int O1,
+                         ColiVkTensor **t2p, float *y2, const void *w2, const float *s2, int O2,
+                         int fmt, const float *x, int S, int I, int grp);
+int  coli_vk_attention_absorb_project(ColiVkTensor **kvb, const void *w, const float *sc, int fmt, int grp,
+                              ColiVkTensor **ot, const void *ow, const float *osc, int ofmt, int ogrp,
+                              float *out, const float *q, int layer, int S, int H,
+                              int Q, int R, int V, int K, int st0, int T, float scale, int Dout);
+/* c/backend_vulkan.h:143-144 (arena slices are not reclaimed, as in the reference) */
+void   coli_vk_tensor_free(ColiVkTensor *t);
+size_t coli_vk_tensor_bytes(const ColiVkTensor *t);
+
+/* c/backend_vulkan.h:151-157: GatedDeltaNet recurrence */
+int  coli_vk_gdn_available(void);
+int  coli_vk_gdn_state_ensure(int layer, int VH, int KD, int VD);
+void coli_vk_gdn_reset(void);
+int  coli_vk_gdn(int layer, const float *qn, const float *kn, const float *v, const float *z,
+                 const float *decay, const float *beta, const float *gnorm, float *y,
+                 int KH, int KD, int VH, int VD, float eps);
+/* c/backend_vulkan.h:162-180: GQA decode attention */
+int  coli_vk_gqa_available(void);
+int  coli_vk_gqa(int layer, const float *q, float *ctx, int S, int H, int KH, int hd,
+                 int max_t, int st0, int T, float scale);
+int  coli_vk_gqa_project(int layer, const float *q, ColiVkTensor *ot, float *out,
+                         int S, int H, int KH, int hd, int max_t, int st0, int T,
+                         float scale, int Dout);
+int  coli_vk_gqa_full_available(void);
+int  coli_vk_gqa_norm_weight(int layer, const float *qnw, const float *knw, int hd);
+int  coli_vk_gqa_full(int layer, const float *x, int D, ColiVkTensor *gq_t, ColiVkTensor *gk_t,
+                      ColiVkTensor *gv_t, ColiVkTensor *out_t, float *out, int S, int H, int KH,
+                      int hd, int rot, int pos_base, int max_t, float eps, float theta, int Dout);
+/* c/backend_vulkan.h:185-198: MoE route prep fused after the attention/GDN block */
+int  coli_vk_moe_route_available(void);
+int  coli_vk_layer_norm_weight(int layer, const float *in_ln, const float *post_ln, int D);
+int  coli_vk_gqa_full_route(int layer, const float *resid, int D,
+                            ColiVkTensor *gq_t, ColiVkTensor *gk_t, ColiVkTensor *gv_t, ColiVkTensor *out_t,
+                            ColiVkTensor *router, int ln_layer,
+                            float *resid_out, float *nrm_out, float *pr_out,
+                            int S, int H, int KH, int hd, int rot, int pos_base, int max_t,
+                            float eps, float theta, int Dout, int E);
+int  coli_vk_gdn_full_route(int layer, const float *x_in, const float *resid, int D,
+                            ColiVkTensor *gqkv_t, ColiVkTensor *gz_t, const float *params,
+                            ColiVkTensor *out_t, ColiVkTensor *router, int ln_layer,
+                            float *resid_out, float *nrm_out, float *pr_out,
+                            int KH, int KD, int VH, int VD, int conv_dim, int conv_k,
+                            float eps, int Dout, int E);
+/* c/backend_vulkan.h:206-221: device-resident residual stream */
+int  coli_vk_stream_available(void);
+int  coli_vk_stream_begin(const float *x, int D);
+int  coli_vk_stream_end(float *x, int D);
+int  coli_vk_stream_add(const float *y, int D);
+const float *coli_vk_stream_nrm(void);
+int  coli_vk_final_norm_weight(const float *w, int D);
+int  coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weights, const float *scales,
+                                int fmt, int I, int O, int gs, float eps, int *idx, float *val);
+int  coli_vk_stream_copy_resid(float *x, int D);
+void coli_vk_route_cache_stats(void);
+void coli_vk_decode_prof(double decode_ms, int tokens);
+/* c/backend_vulkan.h:222-241: layer blocks with device routing (stream path) */
+int  coli_vk_gdn_ba_weight(int layer, const float *alog, const float *dtb,
+                           const float *gnorm, int VH, int VD);
+int  coli_vk_gqa_full_route_pipe(int layer, int D,
+                                 ColiVkTensor *gq_t, ColiVkTensor *gk_t, ColiVkTensor *gv_t, ColiVkTensor *out_t,
+                                 ColiVkTensor *router, int ln_layer,
+                                 int *idx_out, float *val_out, int topk,
+                                 int H, int KH, int hd, int rot, int pos_base, int max_t,
+                                 float eps, float theta, int Dout, int E);
+int  coli_vk_gdn_full_route_pipe(int layer, int D,
+                                 ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                                 ColiVkTensor *gba_t, ColiVkTensor *gbb_t,
+                                 ColiVkTensor *out_t, ColiVkTensor *router, int ln_layer,
+                                 int *idx_out, float *val_out, int topk,
+                                 int KH, int KD, int VH, int VD, int conv_dim, int conv_k,
+                                 float eps, int Dout, int E);
+int  coli_vk_expert_group_issue_pipe(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                     ColiVkTensor *const *downs, const int *rows,
+                                     const float *weights, int count, int D);
+int  coli_vk_expert_group_take_pipe(void);
+/* c/backend_vulkan.h:243-252: device-indexed MoE over a per-layer expert table */
+int  coli_vk_moe_ix_available(void);
+int  coli_vk_eg_table_init(int n_layers, int E, int D, int I, int gs);
+int  coli_vk_eg_table_set(int layer, int eid, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d);
+int  coli_vk_eg_table_set_shared(int layer, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d,
+                                 const float *sh_gate, int D);
+int  coli_vk_stream_moe_fused(void);
+int  coli_vk_stream_ix_pending(void);
+int  coli_vk_stream_ix_hist(int layer, int *idx_out, int K);
+/* c/backend_vulkan.h:258-279: GDN block forms */
+int  coli_vk_gdn_project(int layer, const float *qn, const float *kn, const float *v, const float *z,
+                         const float *decay, const float *beta, const float *gnorm,
+                         ColiVkTensor *ot, float *out, int KH, int KD, int VH, int VD,
+                         float eps, int Dout);
+int  coli_vk_gdn_full_available(void);
+int  coli_vk_gdn_conv_ensure(int layer, int conv_k, int conv_dim);
+int  coli_vk_gdn_conv_weight(int layer, const float *cw, int conv_k, int conv_dim);
+int  coli_vk_gdn_full(int layer, const float *x, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                      const float *params, ColiVkTensor *out_t, float *out,
+                      int KH, int KD, int VH, int VD, int conv_dim, int conv_k, float eps, int Dout);
+int  coli_vk_gdn_full_seq(int layer, const float *x, int S, int D,
+                          ColiVkTensor *gqkv_t, ColiVkTensor *gz_t, const float *params,
+                          ColiVkTensor *out_t, float *out,
+                          int KH, int KD, int VH, int VD, int conv_dim, int conv_k,
+                          float eps, int Dout);
+
+/* ============ Part 2: device-pointer extensions (no reference counterpart) ============ */
+
+/* Device view of a tensor: weights d_w [O, row_bytes] (row_bytes a multiple of 16,
+ * zero padded), d_sz as uploaded.  Returns 0 for NULL. */
+int   coli_hip_tensor_info(const ColiVkTensor *t, int *fmt, int *I, int *O, int *gs,
+                           int *row_bytes, void **d_w, void **d_sz);
+/* The library's stream (hipStream_t); wait for a stream; blocking copy between any
+ * host / device addresses. */
+void *coli_hip_stream(void);
+int   coli_hip_sync(void *stream);
+int   coli_hip_memcpy(void *dst, const void *src, size_t bytes);
+/* y[S,O] = x[S,I] @ dequant(W)^T on device pointers. */
+int   coli_hip_gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, void *stream);
+/* GEMV fused with the k best outputs (k <= 8; value desc, index asc); d_y may be NULL. */
+int   coli_hip_gemv_topk(const ColiVkTensor *t, const float *d_x, float *d_y, int k,
+                         int *d_idx, float *d_val, void *stream);
+/* Create a tensor whose contents are generated on the device with the synthetic-data
+ * spec (fmt 6: bytes = stream(seed,1), [scale,zero] = stream(seed,2) with scale sigma;
+ * fmt 0: rows = sigma * normal(stream(seed,3))); equal to uploading the host-generated
+ * buffers.  Returns 0 on failure. */
+int   coli_hip_tensor_synth(ColiVkTensor **t, int fmt, int I, int O, int gs,
+                            uint64_t seed, double sigma);
+/* d_dst[i] = (float)(sigma * normal(seed, i)) for i < n. */
+int   coli_hip_synth_normal(float *d_dst, size_t n, uint64_t seed, double sigma, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,351 @@
+// fmt6_device.h - device building blocks of the fmt=6 int4 matvec, shared by the GEMV
+// and MoE kernels (gfx950, wave64).
+//
+// Arithmetic (c/qwen.c:211-229):  y[o] = sum_g s_g * (sum_{i in g} x_i n_i - z_g sum_{i in g} x_i)
+//
+// x is converted once per workgroup into block fixed point per group g: e_g is the
+// smallest exponent with max|x_g| < 2^e_g, q_i = rint(x_i * 2^(22-e_g)) (|q_i| <= 2^22,
+// i.e. 23 significant bits relative to the group maximum), and q_i = sum_{l<6} d_l 16^l
+// with balanced digits d_l in [-8, 7].  Digit l of 8 consecutive columns is packed into
+// one 32-bit "limb word"; the weights are stored XOR 0x88 (signed nibbles n - 8, see
+// kLayoutLanes), so sum_i q_i (n_i - 8) over 8 columns is six v_dot8_i32_i4.  Integer
+// sums are exact; one "unit" of chunks sharing a group is scaled back in fp32:
+//   partial = s_g * (2^(e_g-22) * T  -  (z_g - 8) * sum_unit(x~)).
+// The only rounding not present in exact arithmetic on the reference's inputs is x to 23
+// bits relative to its group maximum, so results stay within fp32-accumulation accuracy.
+#pragma once
+
+#include "internal.h"
+
+#include <limits.h>
+
+namespace coli {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kLimbs = 6;
+constexpr int kTopK = 8;                           // largest fused top-k
+constexpr int kLaneWords = kLaneChunks * 4;        // 32-bit weight words per lane and row
+
+// ---------------------------------------------------------------- wave helpers
+#define COLI_DPP_ADD(v, ctrl, rmask)                                                                  \
+    ((v) + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), \
+                                                                 (ctrl), (rmask), 0xF, false)))
+
+// Sum over aligned segments of LPR lanes; the full sum is valid in the LAST lane of each
+// segment (row_bcast15/31 only feed the upper DPP rows).
+template <int LPR>
+__device__ __forceinline__ float seg_sum(float v) {
+    if constexpr (LPR >= 2) v = COLI_DPP_ADD(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    if constexpr (LPR >= 4) v = COLI_DPP_ADD(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 8) v = COLI_DPP_ADD(v, 0x141, 0xF);   // row_half_mirror
+    if constexpr (LPR >= 16) v = COLI_DPP_ADD(v, 0x140, 0xF);  // row_mirror
+    if constexpr (LPR >= 32) v = COLI_DPP_ADD(v, 0x142, 0xA);  // row_bcast15 -> rows 1,3
+    if constexpr (LPR >= 64) v = COLI_DPP_ADD(v, 0x143, 0xC);  // row_bcast31 -> rows 2,3
+    return v;
+}
+
+// (value desc, index asc): the order of c/shaders/argmax.comp:28,41 and of the host scan
+// c/qwen.c:1471-1472 (ties resolve to the lowest index).
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+    return a > b || (a == b && ia < ib);
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert(float (&tv)[K], int (&ti)[K], float v, int i) {
+    if (!better(v, i, tv[K - 1], ti[K - 1])) return;
+#pragma unroll
+    for (int j = 0; j < K; j++) {
+        if (better(v, i, tv[j], ti[j])) {
+            const float t = tv[j];
+            const int u = ti[j];
+            tv[j] = v;
+            ti[j] = i;
+            v = t;
+            i = u;
+        }
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void topk_clear(float (&tv)[K], int (&ti)[K]) {
+#pragma unroll
+    for (int j = 0; j < K; j++) {
+        tv[j] = -INFINITY;
+        ti[j] = INT_MAX;
+    }
+}
+
+// a := best K of (a U b), both sorted by `better`.  The elementwise best of a and
+// reversed b is a bitonic sequence holding the top K; a bitonic merge sorts it.
+template <int K>
+__device__ __forceinline__ void topk_merge2(float (&av)[K], int (&ai)[K], const float (&bv)[K], const int (&bi)[K]) {
+#pragma unroll
+    for (int i = 0; i < K; i++)
+        if (better(bv[K - 1 - i], bi[K - 1 - i], av[i], ai[i])) {
+            av[i] = bv[K - 1 - i];
+            ai[i] = bi[K - 1 - i];
+        }
+#pragma unroll
+    for (int s = K / 2; s > 0; s >>= 1)
+#pragma unroll
+        for (int i = 0; i < K; i++)
+            if ((i & s) == 0 && better(av[i + s], ai[i + s], av[i], ai[i])) {
+                const float t = av[i];
+                const int u = ai[i];
+                av[i] = av[i + s];
+                ai[i] = ai[i + s];
+                av[i + s] = t;
+                ai[i + s] = u;
+            }
+}
+
+// merge the sorted lists of lanes l and l ^ off, for off = 1 .. LANES/2
+template <int K, int LANES>
+__device__ __forceinline__ void wave_topk_merge(float (&tv)[K], int (&ti)[K]) {
+#pragma unroll
+    for (int off = 1; off < LANES; off <<= 1) {
+        float ov[K];
+        int oi[K];
+#pragma unroll
+        for (int j = 0; j < K; j++) {
+            ov[j] = __shfl_xor(tv[j], off);
+            oi[j] = __shfl_xor(ti[j], off);
+        }
+        topk_merge2<K>(tv, ti, ov, oi);
+    }
+}
+
+// Rank selection over n candidates in LDS (value, index-as-bits): each candidate counts
+// the candidates that beat it; rank < k is its output position.  All comparisons are
+// independent (no merge chain) and every thread reads the same LDS word (broadcast).
+// Equal candidates (only the padding (-inf, INT_MAX)) share a rank and write the same.
+__device__ __forceinline__ void rank_select(const float2 *cand, int n, int k, float *out_v, int *out_i,
+                                            int nthreads) {
+    for (int c = threadIdx.x; c < n; c += nthreads) {
+        const float2 me = cand[c];
+        const int mi = __float_as_int(me.y);
+        int r = 0;
+        for (int j = 0; j < n; j++) {
+            const float2 o = cand[j];
+            r += better(o.x, __float_as_int(o.y), me.x, mi) ? 1 : 0;
+        }
+        if (r < k) {
+            out_v[r] = me.x;
+            out_i[r] = mi;
+        }
+    }
+}
+
+// Block-wide best-k (k <= K) over per-thread sorted lists; result to out_v/out_i
+// (written by thread 0).  All kThreads threads call.
+template <int K>
+__device__ void block_topk_merge(float (&tv)[K], int (&ti)[K], int k, float *out_v, int *out_i) {
+    __shared__ float s_v[kWaves][K];
+    __shared__ int s_i[kWaves][K];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    wave_topk_merge<K, 64>(tv, ti);
+    if (lane == 0)
+#pragma unroll
+        for (int j = 0; j < K; j++) {
+            s_v[wave][j] = tv[j];
+            s_i[wave][j] = ti[j];
+        }
+    __syncthreads();
+    if (wave == 0) {
+        const int w = lane < kWaves ? lane : 0;
+#pragma unroll
+        for (int j = 0; j < K; j++) {
+            tv[j] = lane < kWaves ? s_v[w][j] : -INFINITY;
+            ti[j] = lane < kWaves ? s_i[w][j] : INT_MAX;
+        }
+        wave_topk_merge<K, kWaves>(tv, ti);
+        if (lane == 0)
+            for (int j = 0; j < k; j++) {
+                out_v[j] = tv[j];
+                out_i[j] = ti[j];
+            }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------- x -> digit planes
+struct XPrep {
+    uint32_t limb[kLaneMaxI / 8][kLimbs];   // [word][digit]
+    int qsum[kLaneMaxI / 32];               // per 32-column chunk: sum of q
+    unsigned gmax[kLaneMaxI / 32];          // per group (gs >= 32): bits of max |x|
+};
+
+// ncols: columns to prepare (a multiple of 32 covering every lane's chunks, <= kLaneMaxI);
+// columns at or past I are zero.  Each thread owns whole 8-column words: it loads its
+// x values once (all loads in flight together), publishes one max per word, then turns
+// them into digit planes.  Ends with __syncthreads().
+constexpr int kPrepWords = kLaneMaxI / 8 / kThreads;   // words per thread
+struct XRegs {
+    float v[kPrepWords][8];
+};
+// Issue the x loads (split from prep_x so that they can go out before other loads).
+__device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, int ncols, XRegs &xr) {
+    const int tid = threadIdx.x, nwords = ncols / 8;
+#pragma unroll
+    for (int k = 0; k < kPrepWords; k++) {
+        const int w = tid + k * kThreads;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int i = w * 8 + c;
+            xr.v[k][c] = (w < nwords && i < I) ? x[i] : 0.f;
+        }
+    }
+}
+
+__device__ inline void prep_x(const XRegs &xr, int gs, int ncols, XPrep &P) {
+    const int tid = threadIdx.x;
+    const int nwords = ncols / 8, nch = ncols / 32, ngrp = (ncols + gs - 1) / gs;
+    const auto &xv = xr.v;
+    for (int g = tid; g < ngrp; g += kThreads) P.gmax[g] = 0u;
+    for (int c = tid; c < nch; c += kThreads) P.qsum[c] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPrepWords; k++) {
+        const int w = tid + k * kThreads;
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(xv[k][c]));
+        if (w < nwords) atomicMax(&P.gmax[(w * 8) / gs], __float_as_uint(m));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPrepWords; k++) {
+        const int w = tid + k * kThreads;
+        if (w >= nwords) continue;
+        const float m = __uint_as_float(P.gmax[(w * 8) / gs]);
+        const int e = m > 0.f ? ilogbf(m) + 1 : 0;    // m < 2^e
+        uint32_t u[8];
+        int qs = 0;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int q = (int)rintf(ldexpf(xv[k][c], 22 - e));
+            qs += q;
+            u[c] = (uint32_t)(q + 0x888888);   // balanced digits d -> unsigned nibbles d + 8
+        }
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) {
+            uint32_t lw = 0;
+#pragma unroll
+            for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
+            P.limb[w][l] = lw ^ 0x88888888u;   // (d + 8) ^ 8 == d mod 16
+        }
+        atomicAdd(&P.qsum[w >> 2], qs);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int group_exp22(const XPrep &P, int g) {
+    const float m = __uint_as_float(P.gmax[g]);
+    return (m > 0.f ? ilogbf(m) + 1 : 0) - 22;
+}
+
+// ---------------------------------------------------------------- per-lane state
+// Buffer loads: out-of-range offsets read 0 (no predication), 32-bit offsets.
+typedef int coli_v4i __attribute__((ext_vector_type(4)));
+typedef int coli_v2i __attribute__((ext_vector_type(2)));
+constexpr uint32_t kOOB = 0x80000000u;     // added to an offset <= 2^31: always out of range
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+__device__ __forceinline__ float2 buf_load8f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const coli_v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return make_float2(__int_as_float(v.x), __int_as_float(v.y));
+}
+
+// One lane's share of a row: kLaneChunks host chunks, split into NU units of CU chunks
+// that share a group (CU = min(gs/32, kLaneChunks)).
+template <int CU>
+struct LaneX {
+    static constexpr int NU = kLaneChunks / CU;
+    // geometry (independent of x)
+    uint32_t woff[kLaneChunks];   // byte offset of the lane's chunk c within a row (or kOOB)
+    uint32_t soff[NU];            // byte offset of the unit's [scale, zero] within a row (or kOOB)
+    int ch0;                      // first host chunk of the lane
+    bool on;                      // lane holds data (j < nl)
+    // x digits of the lane's columns
+    uint32_t lm[kLaneWords][kLimbs];
+    int ue[NU];      // e_g - 22
+    float ucs[NU];   // sum of x~ over the unit
+};
+
+template <int CU>
+__device__ __forceinline__ void lane_geo(int j, int nl, int I, int gs, LaneX<CU> &L) {
+    L.on = j < nl;
+    L.ch0 = (L.on ? j : 0) * kLaneChunks;
+#pragma unroll
+    for (int c = 0; c < kLaneChunks; c++) L.woff[c] = L.on ? (uint32_t)((c * nl + j) * 16) : kOOB;
+#pragma unroll
+    for (int q = 0; q < LaneX<CU>::NU; q++) {
+        const int col0 = (L.ch0 + q * CU) * 32;
+        L.soff[q] = (L.on && col0 < I) ? (uint32_t)((col0 / gs) * 8) : kOOB;
+    }
+}
+
+template <int CU>
+__device__ __forceinline__ void lane_x(const XPrep &P, int gs, LaneX<CU> &L) {
+#pragma unroll
+    for (int w = 0; w < kLaneWords; w++)
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) L.lm[w][l] = P.limb[L.ch0 * 4 + w][l];
+#pragma unroll
+    for (int q = 0; q < LaneX<CU>::NU; q++) {
+        const int ch = L.ch0 + q * CU;
+        L.ue[q] = group_exp22(P, (ch * 32) / gs);
+        int qs = 0;
+#pragma unroll
+        for (int c = 0; c < CU; c++) qs += P.qsum[ch + c];
+        L.ucs[q] = ldexpf((float)qs, L.ue[q]);
+    }
+}
+
+// Lane partial of one row: wq = the lane's kLaneChunks chunks (device words), sv = the
+// units' [scale, zero] (scale 0 for units without data).
+template <int CU>
+__device__ __forceinline__ float lane_row(const uint4 (&wq)[kLaneChunks], const float2 (&sv)[LaneX<CU>::NU],
+                                          const LaneX<CU> &L) {
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < LaneX<CU>::NU; q++) {
+        int t[kLimbs] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int c = q * CU; c < (q + 1) * CU; c++) {
+            const uint32_t wv[4] = {wq[c].x, wq[c].y, wq[c].z, wq[c].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+#pragma unroll
+                for (int l = 0; l < kLimbs; l++)
+                    t[l] = __builtin_amdgcn_sdot8((int)wv[w], (int)L.lm[c * 4 + w][l], t[l], false);
+        }
+        const int lo = t[0] + 16 * t[1] + 256 * t[2];
+        const int hi = t[3] + 16 * t[4] + 256 * t[5];
+        const float T = fmaf((float)hi, 4096.f, (float)lo);
+        const float v = fmaf(-(sv[q].y - 8.f), L.ucs[q], ldexpf(T, L.ue[q]));
+        acc = fmaf(sv[q].x, v, acc);
+    }
+    return acc;
+}
+
+// Load the lane's chunks and unit scales of the row at byte offsets (wrow, srow), which
+// are clamped by the caller to at most the buffer sizes: rows past the end, lanes without
+// data and units without columns all read 0 and contribute 0.
+template <int CU>
+__device__ __forceinline__ void lane_load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, uint32_t wrow,
+                                          uint32_t srow, const LaneX<CU> &L, uint4 (&wq)[kLaneChunks],
+                                          float2 (&sv)[LaneX<CU>::NU]) {
+#pragma unroll
+    for (int c = 0; c < kLaneChunks; c++) wq[c] = buf_load16(rw, wrow + L.woff[c]);
+#pragma unroll
+    for (int q = 0; q < LaneX<CU>::NU; q++) sv[q] = buf_load8f(rs, srow + L.soff[q]);
+}
+
+}  // namespace coli

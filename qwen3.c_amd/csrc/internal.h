@@ -1,0 +1,79 @@
+// internal.h - shared declarations of libcoli_hip (MI355X / gfx950 only).
+//
+// One process, one GPU, one host thread (the reference engine is single-threaded
+// and keeps a global singleton too: c/backend_vulkan.c:69-278).  All device work is
+// issued on one non-blocking HIP stream at default priority.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define COLI_API extern "C" __attribute__((visibility("default")))
+
+// Opaque handle of the drop-in ABI (c/backend_vulkan.h:33).  Device layouts:
+//   kLayoutRows  (fmt 0/1, and fmt 6 outside the fast path): row o of the host copy,
+//                zero-padded to row_bytes (a 16-byte multiple).  fmt 6: U8 nibbles,
+//                fmt 1: I8, fmt 0: F32.
+//   kLayoutLanes (fmt 6 with gs % 32 == 0 and I <= kLaneMaxI): each row is cut into
+//                16-byte chunks (32 nibbles); lane j of a row owns host chunks 2j, 2j+1,
+//                and host chunk h = 2j + c is stored at chunk slot c * nl + j (nl = lanes
+//                with data = ceil(nchunks / 2)), so one load instruction per c reads nl
+//                consecutive 16-byte chunks.  Every byte is stored XOR 0x88, which turns
+//                the unsigned nibble n into the signed nibble n - 8 for v_dot8_i32_i4.
+//                Bytes past the host row read as 0 (stored as 0x88).
+//   sz: fmt 6 f32 [O, ng, 2] verbatim, fmt 1 f32 [O], fmt 0 none.
+enum { kLayoutRows = 0, kLayoutLanes = 1 };
+struct ColiVkTensor {
+    int fmt, I, O, gs, ng;
+    int layout;
+    int nchunks;       // 16-byte host chunks per row: ceil(host row bytes / 16)
+    int nl;            // kLayoutLanes: lanes with data per row
+    int row_bytes;     // device row stride
+    uint8_t *w;        // device weights
+    float *sz;         // device scales (+zeros)
+    size_t bytes;      // device bytes held
+};
+
+namespace coli {
+
+struct Runtime;
+extern Runtime G;
+
+// sticky failure: print and disable the device for the rest of the process
+bool fail(const char *what, hipError_t e);
+bool ok();                               // device usable (init done, no sticky failure)
+hipStream_t stream();
+int n_cu();
+
+// device memory
+void *arena_alloc(size_t bytes);          // weights: 256-byte aligned slices, never freed
+bool scratch(void **p, size_t *cap, size_t need);   // grow-only device scratch
+bool host_scratch(void **p, size_t *cap, size_t need);  // grow-only pinned host scratch
+bool sync_stream(const char *who);
+
+// tensors
+constexpr int kLaneMaxI = 4096;          // fmt 6 lanes layout / fast GEMV path: nl <= 64
+constexpr int kLaneChunks = 2;           // 16-byte chunks owned by one lane of a row
+ColiVkTensor *tensor_alloc(int fmt, int I, int O, int gs);   // not yet filled or counted
+size_t tensor_host_row_bytes(const ColiVkTensor *t);
+void tensor_register(ColiVkTensor *t);                       // count it in mem_info
+// Fill t->w from `rows` host-layout rows [r0, r0+rows) already in device memory
+// (d_src, stride tensor_host_row_bytes), converting to t's device layout.
+bool tensor_fill_rows(ColiVkTensor *t, const uint8_t *d_src, int r0, int rows, hipStream_t st);
+// Shared device staging buffer for host-layout rows: *cap_rows rows of host_rb bytes.
+bool stage_buffer(void **p, size_t *cap_rows, size_t host_rb);
+
+// GEMV launchers on device pointers (stream-ordered, no sync)
+struct TopkOut {       // fused top-k over the GEMV outputs (rows of one launch)
+    int k;             // 1..8 (0 = none)
+    int *idx;          // device [k]
+    float *val;        // device [k]
+};
+bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_t st,
+          const TopkOut *tk = nullptr);
+// k best (value desc, index asc) of d_v[0, n), k <= 8
+bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t st);
+bool rmsnorm_zc(const float *d_x, const float *d_w, float *d_y, int D, float eps, hipStream_t st);
+
+}  // namespace coli
