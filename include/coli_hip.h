@@ -218,6 +218,17 @@ int   coli_hip_tensor_synth(ColiVkTensor **t, int fmt, int I, int O, int gs,
                             uint64_t seed, double sigma);
 /* d_dst[i] = (float)(sigma * normal(seed, i)) for i < n. */
 int   coli_hip_synth_normal(float *d_dst, size_t n, uint64_t seed, double sigma, void *stream);
+/* One layer's MoE block (router -> softmax/top-K -> K routed + shared expert -> weighted
+ * combine, c/qwen.c:804-920) in one launch over the expert table of coli_vk_eg_table_*.
+ * K <= 8; router fmt 0 (f32) or 1 (int8), [E, D].  d_out[D] = the block output
+ * (accumulate != 0: d_out += it).  d_idx[K] (rank order) and d_val[K + 1] (renormed
+ * weights, then the shared gate) may be NULL.  Launches share one scratch area: issue
+ * them on one stream. */
+int   coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x,
+                          float *d_out, int accumulate, int *d_idx, float *d_val, void *stream);
+/* Error flag of the MoE launches since the last call (synchronizes the device): 0 none,
+ * 1 a bounded wait gave up, 2 an out-of-range expert id, -1 runtime error. */
+int   coli_hip_moe_error(void);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,18 @@ _SIGS = {
     "coli_hip_gemv_topk": (_I, [_P, _P, _P, _I, _P, _P, _P]),
     "coli_hip_tensor_synth": (_I, [_P, _I, _I, _I, _I, C.c_uint64, C.c_double]),
     "coli_hip_synth_normal": (_I, [_P, C.c_size_t, C.c_uint64, C.c_double, _P]),
+    "coli_vk_gate_up": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "coli_vk_expert_group": (_I, [_P, _P, _P, _P, _I, _P, _P]),
+    "coli_vk_expert_group_issue": (_I, [_P, _P, _P, _P, _I, _P]),
+    "coli_vk_expert_group_take": (_I, [_P]),
+    "coli_vk_eg_xs_bind": (_I, [_P, _I, _I]),
+    "coli_vk_expert_group_issue_id": (_I, [_P, _P, _P, _P, _I, _P]),
+    "coli_vk_moe_ix_available": (_I, []),
+    "coli_vk_eg_table_init": (_I, [_I, _I, _I, _I, _I]),
+    "coli_vk_eg_table_set": (_I, [_I, _I, _P, _P, _P]),
+    "coli_vk_eg_table_set_shared": (_I, [_I, _P, _P, _P, _P, _I]),
+    "coli_hip_moe_decode": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
+    "coli_hip_moe_error": (_I, []),
 }
 
 
@@ -165,3 +177,71 @@ class Lib:
     def synth_normal_dev(self, d_dst, n, seed, sigma, stream=None):
         if not self.L.coli_hip_synth_normal(d_dst, n, C.c_uint64(seed), sigma, stream):
             raise RuntimeError("coli_hip_synth_normal failed")
+
+    # ---- MoE: expert MLPs on host buffers (c/backend_vulkan.h:75-101) ---------------
+    def gate_up(self, g, u, x, S=1):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        h = np.empty(S * g.O, np.float32)
+        if not self.L.coli_vk_gate_up(g.ref, u.ref, _ptr(h), _ptr(x), None, None, None, None, g.fmt, S, g.I,
+                                      g.O, g.gs):
+            raise RuntimeError("coli_vk_gate_up failed")
+        return h
+
+    @staticmethod
+    def _group(gates, ups, downs, rows):
+        n = len(gates)
+        arr = lambda ts: (C.c_void_p * n)(*[t.handle.value for t in ts])
+        return arr(gates), arr(ups), arr(downs), (C.c_int * n)(*rows)
+
+    def expert_group(self, gates, ups, downs, rows, x):
+        """y[sum(rows), D]: row block c = down_c(silu(gate_c x) * up_c x)."""
+        g, u, d, r = self._group(gates, ups, downs, rows)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(sum(rows) * gates[0].I, np.float32)
+        if not self.L.coli_vk_expert_group(g, u, d, r, len(gates), _ptr(y), _ptr(x)):
+            raise RuntimeError("coli_vk_expert_group failed")
+        return y
+
+    def expert_group_issue(self, gates, ups, downs, rows, x):
+        g, u, d, r = self._group(gates, ups, downs, rows)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        return bool(self.L.coli_vk_expert_group_issue(g, u, d, r, len(gates), _ptr(x)))
+
+    def expert_group_take(self, n_rows, D):
+        y = np.empty(n_rows * D, np.float32)
+        if not self.L.coli_vk_expert_group_take(_ptr(y)):
+            raise RuntimeError("coli_vk_expert_group_take failed")
+        return y
+
+    def eg_xs_bind(self, xs, S, D):
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        if not self.L.coli_vk_eg_xs_bind(_ptr(xs), S, D):
+            raise RuntimeError("coli_vk_eg_xs_bind failed")
+
+    def expert_group_issue_id(self, gates, ups, downs, rows, tok_ids):
+        g, u, d, r = self._group(gates, ups, downs, rows)
+        ids = np.ascontiguousarray(tok_ids, dtype=np.int32)
+        return bool(self.L.coli_vk_expert_group_issue_id(g, u, d, r, len(gates), _ptr(ids)))
+
+    # ---- MoE: device expert table + one-launch block (c/backend_vulkan.h:243-252) ----
+    def eg_table_init(self, n_layers, E, D, I, gs):
+        if not self.L.coli_vk_eg_table_init(n_layers, E, D, I, gs):
+            raise RuntimeError("coli_vk_eg_table_init failed")
+
+    def eg_table_set(self, layer, eid, g, u, d):
+        if not self.L.coli_vk_eg_table_set(layer, eid, g.handle, u.handle, d.handle):
+            raise RuntimeError(f"coli_vk_eg_table_set({layer}, {eid}) failed")
+
+    def eg_table_set_shared(self, layer, g, u, d, sh_gate):
+        sg = np.ascontiguousarray(sh_gate, dtype=np.float32)
+        if not self.L.coli_vk_eg_table_set_shared(layer, g.handle, u.handle, d.handle, _ptr(sg), sg.size):
+            raise RuntimeError("coli_vk_eg_table_set_shared failed")
+
+    def moe_decode_dev(self, layer, router, K, d_x, d_out, accumulate=False, d_idx=None, d_val=None,
+                       stream=None):
+        if not self.L.coli_hip_moe_decode(layer, router.handle, K, d_x, d_out, int(accumulate), d_idx, d_val,
+                                          stream):
+            raise RuntimeError("coli_hip_moe_decode failed")
+
+    def moe_error(self):
+        return int(self.L.coli_hip_moe_error())

@@ -1,38 +1,1097 @@
-// moe.hip - expert group, device-indexed MoE and residual stream entry points.
-// (first cut: unavailable; filled in by the MoE kernels)
-#include "internal.h"
+// moe.hip - the device-indexed top-k MoE block, the expert-group entry points, the expert
+// table and the device residual stream of the drop-in ABI.
+//
+// Semantics (c/qwen.c:804-928, the --no-vulkan path):
+//   logits = router @ x                                  (f32 router, c/qwen.c:178-189)
+//   p = softmax(logits); idx/val = K greedy picks of p (ties -> lower index), val /= sum(val)
+//   shgt = sigmoid(sh_gate . x)
+//   out[d] = sum_k val_k * down_k(silu(gate_k x) * up_k x)[d]   (rank order), then
+//   out[d] += shgt * down_sh(silu(gate_sh x) * up_sh x)[d]
+//
+// One persistent launch (moe_block_kernel) over a list of tiles in dependency order:
+//   R  router rows          -> logits (tagged)
+//   Gs shared gate/up rows  -> h[K]   (independent of routing: overlaps R and T)
+//   T  softmax / top-k / renorm / shared gate -> route (tagged)
+//   Gk routed gate/up rows  -> h[k]   (wait for route)
+//   D  down rows of all K+1 experts + weighted combine -> out   (wait for route, then h)
+// Block b runs tile b; when the grid is smaller than the tile list, finished blocks take
+// further tiles from an atomic counter.  A tile only waits for tiles of smaller index,
+// which blocks of smaller index hold (workgroups are dispatched in index order).
+//
+// Cross-block data are 64-bit words {epoch, value} written and read with agent-scope
+// atomics (single-copy atomic, coherent across the XCDs' L2s): a consumer polls until the
+// tag equals the launch epoch.  No counters need ordering, so no device-scope fences (an
+// L2 write-back each on gfx950) are issued.  Polls are bounded: past the limit they set an
+// error flag and give up, so every wave always exits.
+#include "fmt6_device.h"
 
-COLI_API int coli_vk_gate_up(ColiVkTensor **, ColiVkTensor **, float *, const float *, const void *,
-                             const float *, const void *, const float *, int, int, int, int, int) { return 0; }
-COLI_API int coli_vk_expert_group(ColiVkTensor *const *, ColiVkTensor *const *, ColiVkTensor *const *,
-                                  const int *, int, float *, const float *) { return 0; }
-COLI_API int coli_vk_expert_group_issue(ColiVkTensor *const *, ColiVkTensor *const *, ColiVkTensor *const *,
-                                        const int *, int, const float *) { return 0; }
-COLI_API int coli_vk_expert_group_take(float *) { return 0; }
-COLI_API int coli_vk_eg_gather_available(void) { return 0; }
-COLI_API int coli_vk_eg_xs_bind(const float *, int, int) { return 0; }
-COLI_API int coli_vk_expert_group_issue_id(ColiVkTensor *const *, ColiVkTensor *const *, ColiVkTensor *const *,
-                                           const int *, int, const int *) { return 0; }
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+namespace coli {
+
+struct ExpertRec {
+    const uint8_t *wg, *wu, *wd;
+    const float *sg, *su, *sd;
+};
+
+// geometry shared by every expert of a table (fmt 6, lanes layout)
+struct MoeGeom {
+    int D, I, gs;
+    int ngD, ngI;   // groups per gate/up row (over D) and per down row (over I)
+    int nlG, nlD;   // lanes with data per gate/up row and per down row
+    int rbG, rbD;   // device row bytes of gate/up and of down
+};
+
+constexpr int kMaxK = 64;                 // c/backend_vulkan.c:3298 (topk <= 64)
+constexpr int kMaxE = 1024;
+constexpr int kMaxSlots = kTopK + 1;      // fused kernel: K <= 8 routed + the shared expert
+constexpr int kMoeMaxI = 512;             // expert intermediate size (h staged in LDS)
+constexpr int kRRows = 8;                 // router rows per tile
+constexpr int kGSteps = 2;                // gate/up row steps per tile
+constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.5-2 us)
+
+struct MoeArgs {
+    const float *x;                       // [D] expert input (post-attention RMSNorm)
+    const uint8_t *rw;                    // router rows (fmt 0 f32 or fmt 1 int8)
+    const float *rs;                      // fmt 1: per-row scales
+    int rfmt, rrb, E;
+    const ExpertRec *rec;                 // [E + 1], shared expert at E
+    const float *sh_gate;                 // [D]
+    int K;
+    float *out;                           // [D]
+    int accumulate;                       // out += (residual stream) instead of out =
+    int *idx_out;                         // optional [K]
+    float *val_out;                       // optional [K + 1] (renormed weights, then shgt)
+    unsigned long long *tagv;             // logits [E] | idx [K] | w [K + 1] | h [(K + 1) * I]
+    unsigned *tickets;                    // [2]
+    int *err;
+    uint32_t epoch;
+    int gRows, nG;                        // gate/up rows per tile, tiles per expert
+    int dRows, nD;                        // down rows per tile, tiles
+    MoeGeom g;
+};
+
+// ---------------------------------------------------------------- tagged words
+__device__ __forceinline__ unsigned long long aload(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tag_put(unsigned long long *p, uint32_t epoch, float v) {
+    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool poll_give_up(int *err, int polls) {
+    if (polls > kPollLimit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    return false;
+}
+__device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t epoch, int *err) {
+    for (int polls = 0;; polls++) {
+        const unsigned long long v = aload(p);
+        if ((uint32_t)(v >> 32) == epoch) return __uint_as_float((uint32_t)v);
+        if (poll_give_up(err, polls)) return 0.f;
+    }
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+// ---------------------------------------------------------------- h -> digit planes
+// The down projection uses the same integer-dot arithmetic as the GEMV (fmt6_device.h)
+// with h in place of x: per slot s, limb[s * I/8 + word][digit], qsum[s * I/32 + chunk],
+// gmax[s * ngI + group].
+struct HPrep {
+    uint32_t limb[kMaxSlots * kMoeMaxI / 8][kLimbs];
+    int qsum[kMaxSlots * kMoeMaxI / 32];
+    unsigned gmax[kMaxSlots * kMoeMaxI / 64];
+};
+constexpr int kHWords = (kMaxSlots * kMoeMaxI / 8 + kThreads - 1) / kThreads;
+
+// v: the thread's words q = tid + k * kThreads (8 columns each) of the NS x I values.
+// Ends with __syncthreads().
+__device__ void prep_h(const float (&v)[kHWords][8], int NS, int I, int gs, int ngI, HPrep &H) {
+    const int tid = threadIdx.x, wpr = I / 8, nw = NS * wpr;
+    for (int i = tid; i < NS * ngI; i += kThreads) H.gmax[i] = 0u;
+    for (int i = tid; i < NS * (I / 32); i += kThreads) H.qsum[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kHWords; k++) {
+        const int q = tid + k * kThreads;
+        if (q >= nw) continue;
+        const int s = q / wpr, w = q - s * wpr;
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(v[k][c]));
+        atomicMax(&H.gmax[s * ngI + (w * 8) / gs], __float_as_uint(m));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kHWords; k++) {
+        const int q = tid + k * kThreads;
+        if (q >= nw) continue;
+        const int s = q / wpr, w = q - s * wpr;
+        const float m = __uint_as_float(H.gmax[s * ngI + (w * 8) / gs]);
+        const int e = m > 0.f ? ilogbf(m) + 1 : 0;
+        uint32_t u[8];
+        int qs = 0;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int qv = (int)rintf(ldexpf(v[k][c], 22 - e));
+            qs += qv;
+            u[c] = (uint32_t)(qv + 0x888888);
+        }
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) {
+            uint32_t lw = 0;
+#pragma unroll
+            for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
+            H.limb[q][l] = lw ^ 0x88888888u;
+        }
+        atomicAdd(&H.qsum[s * (I / 32) + w / 4], qs);
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------- down rows
+// One thread per 16-byte chunk of a down row: TPR = 2 * (lanes of the lanes layout,
+// rounded up to a power of two); thread t < TPR/2 reads chunk slot 0 of lane t, thread
+// TPR/2 + t chunk slot 1 of lane t, so one load instruction covers whole rows.  The
+// thread's host chunk is h = 2 * lane + slot (columns 32h .. 32h + 31, one group).
+struct DownThread {
+    uint32_t woff, soff;   // byte offsets within a row (kOOB: no data)
+    int h;                 // host chunk
+};
+
+template <int TPR>
+__device__ __forceinline__ DownThread down_thread(const MoeGeom &g) {
+    const int t = (threadIdx.x & 63) % TPR, c = t >= TPR / 2 ? 1 : 0, jj = t - c * (TPR / 2);
+    const bool on = jj < g.nlD && 2 * jj + c < g.I / 32;
+    DownThread d;
+    d.h = on ? 2 * jj + c : 0;
+    d.woff = on ? (uint32_t)((c * g.nlD + jj) * 16) : kOOB;
+    d.soff = on ? (uint32_t)(((d.h * 32) / g.gs) * 8) : kOOB;
+    return d;
+}
+
+// partial of one chunk: s * (2^(e-22) T - (z - 8) sum(h~)) over its 32 columns of slot s
+__device__ __forceinline__ float down_chunk(const HPrep &H, int s, int I, int gs, int ngI, const DownThread &d,
+                                            const uint4 &w, const float2 &sz) {
+    const uint32_t *lb = H.limb[s * (I / 8) + d.h * 4];
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    int t[kLimbs] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int l = 0; l < kLimbs; l++) t[l] = __builtin_amdgcn_sdot8((int)wv[q], (int)lb[q * kLimbs + l], t[l], false);
+    const int lo = t[0] + 16 * t[1] + 256 * t[2];
+    const int hi = t[3] + 16 * t[4] + 256 * t[5];
+    const float T = fmaf((float)hi, 4096.f, (float)lo);
+    const float m = __uint_as_float(H.gmax[s * ngI + (d.h * 32) / gs]);
+    const int ue = (m > 0.f ? ilogbf(m) + 1 : 0) - 22;
+    const float ucs = ldexpf((float)H.qsum[s * (I / 32) + d.h], ue);
+    return sz.x * fmaf(-(sz.y - 8.f), ucs, ldexpf(T, ue));
+}
+
+// Rows r0 + wave * RPW + seg of the down projections of NS slots (recs in LDS), combined
+// as out[r] = ((0 + w_0 y_0) + w_1 y_1) + ... (accumulate: out[r] + that).  gather(hv)
+// fills the thread's h words (see prep_h); weight loads are issued before it.
+template <int TPR, typename Gather>
+__device__ __forceinline__ void down_rows(const MoeGeom &g, int NS, const ExpertRec *recs, const float *wts,
+                                          HPrep &H, int r0, int rows, float *out, int accumulate, Gather gather) {
+    constexpr int RPW = 64 / TPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = lane % TPR, seg = lane / TPR;
+    const DownThread d = down_thread<TPR>(g);
+    const uint32_t wtot = (uint32_t)g.D * g.rbD, stot = (uint32_t)g.D * g.ngI * 8;
+    const int r = r0 + wave * RPW + seg;
+    const uint32_t rc = (uint32_t)(r < g.D ? r : g.D);   // row D reads 0 (past the end)
+    uint4 wq[kMaxSlots];
+    float2 sv[kMaxSlots];
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; s++) {
+        if (s < NS) {
+            wq[s] = buf_load16(buf_rsrc(recs[s].wd, wtot), rc * g.rbD + d.woff);
+            sv[s] = buf_load8f(buf_rsrc(recs[s].sd, stot), rc * g.ngI * 8 + d.soff);
+        }
+    }
+    float hv[kHWords][8];
+    gather(hv);
+    prep_h(hv, NS, g.I, g.gs, g.ngI, H);
+    float accum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; s++) {
+        if (s < NS) {
+            const float y = seg_sum<TPR>(down_chunk(H, s, g.I, g.gs, g.ngI, d, wq[s], sv[s]));
+            accum = accum + wts[s] * y;
+        }
+    }
+    if (t == TPR - 1 && r < g.D && r < r0 + rows) out[r] = accumulate ? out[r] + accum : accum;
+}
+
+// ---------------------------------------------------------------- gate/up rows
+// h[r] = silu(gate r . x) * (up r . x) for the tile's rows (c/qwen.c:780-786, silu :173).
+// All of the tile's weight loads are issued before the first row is reduced.
+template <int LPR, int CU, typename Emit>
+__device__ __forceinline__ void gateup_rows(const LaneX<CU> &L, const ExpertRec &rec, const MoeGeom &g, int r0,
+                                            Emit emit) {
+    constexpr int RPW = 64 / LPR, NU = LaneX<CU>::NU;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane % LPR, seg = lane / LPR;
+    const uint32_t wtot = (uint32_t)g.I * g.rbG, stot = (uint32_t)g.I * g.ngD * 8;
+    const __amdgpu_buffer_rsrc_t rgw = buf_rsrc(rec.wg, wtot), rgs = buf_rsrc(rec.sg, stot);
+    const __amdgpu_buffer_rsrc_t ruw = buf_rsrc(rec.wu, wtot), rus = buf_rsrc(rec.su, stot);
+    uint4 wg[kGSteps][kLaneChunks], wu[kGSteps][kLaneChunks];
+    float2 sg[kGSteps][NU], su[kGSteps][NU];
+#pragma unroll
+    for (int st = 0; st < kGSteps; st++) {
+        const int r = r0 + (st * kWaves + wave) * RPW + seg;
+        const uint32_t rc = (uint32_t)(r < g.I ? r : g.I);   // row I reads 0 (past the end)
+        lane_load<CU>(rgw, rgs, rc * g.rbG, rc * g.ngD * 8, L, wg[st], sg[st]);
+        lane_load<CU>(ruw, rus, rc * g.rbG, rc * g.ngD * 8, L, wu[st], su[st]);
+    }
+#pragma unroll
+    for (int st = 0; st < kGSteps; st++) {
+        const int r = r0 + (st * kWaves + wave) * RPW + seg;
+        const float gv = seg_sum<LPR>(lane_row<CU>(wg[st], sg[st], L));
+        const float uv = seg_sum<LPR>(lane_row<CU>(wu[st], su[st], L));
+        if (j == LPR - 1 && r < g.I) emit(r, gv / (1.f + expf(-gv)) * uv);
+    }
+}
+
+// ---------------------------------------------------------------- R: router rows
+// Dot products accumulate in fp64 from exact fp64 products, so each logit is the correctly
+// rounded value of the exact sum (the reference sums sequentially in fp32).
+__device__ void tile_router(const MoeArgs &a, int r0) {
+    constexpr int kRC = 8;   // float4 per lane and pass: 2048 columns
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.g.D;
+    for (int rr = wave; rr < kRRows; rr += kWaves) {
+        const int r = r0 + rr;
+        if (r >= a.E) break;
+        const uint8_t *row = a.rw + (size_t)r * a.rrb;
+        double acc = 0.0;
+        for (int c0 = 0; c0 < D; c0 += kRC * 256) {
+            float4 xv[kRC];
+            float4 w[kRC];
+#pragma unroll
+            for (int c = 0; c < kRC; c++) {
+                const int col = c0 + (lane + c * 64) * 4;
+                const bool in = col < D;
+                xv[c] = in ? *(const float4 *)(a.x + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (a.rfmt == 0) {
+                    w[c] = in ? *(const float4 *)(row + (size_t)col * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {   // fmt 1: int8 rows
+                    const uint32_t q = in ? *(const uint32_t *)(row + col) : 0u;
+                    w[c] = make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16),
+                                       (float)(int8_t)(q >> 24));
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < kRC; c++) {
+                acc = fma((double)xv[c].x, (double)w[c].x, acc);
+                acc = fma((double)xv[c].y, (double)w[c].y, acc);
+                acc = fma((double)xv[c].z, (double)w[c].z, acc);
+                acc = fma((double)xv[c].w, (double)w[c].w, acc);
+            }
+        }
+        acc = wave_sum_d(acc);
+        if (lane == 0) {
+            float l = (float)acc;
+            if (a.rfmt == 1) l *= a.rs[r];   // c/qwen.c:237: acc * scale[o]
+            tag_put(&a.tagv[r], a.epoch, l);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- T: route
+// c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate.
+struct RouteLds {
+    float p[kMaxE];
+    float red[kWaves];
+    double redd[kWaves];
+    float sum;
+    int idx[kMaxK];
+    float val[kMaxK];
+};
+
+__device__ void tile_route(const MoeArgs &a, RouteLds &R) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.E, K = a.K;
+    float m = -1e30f;   // the reference's initial max
+    for (int e = tid; e < E; e += kThreads) {
+        const float l = tag_get(&a.tagv[e], a.epoch, a.err);
+        R.p[e] = l;
+        m = fmaxf(m, l);
+    }
+    m = wave_max_f(m);
+    if (lane == 0) R.red[wave] = m;
+    // shared expert gate: fp64 dot, rounded once
+    double sg = 0.0;
+    for (int d = tid; d < a.g.D; d += kThreads) sg = fma((double)a.sh_gate[d], (double)a.x[d], sg);
+    sg = wave_sum_d(sg);
+    if (lane == 0) R.redd[wave] = sg;
+    __syncthreads();
+    m = R.red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, R.red[w]);
+    for (int e = tid; e < E; e += kThreads) R.p[e] = expf(R.p[e] - m);
+    __syncthreads();
+    if (tid == 0) {   // sequential sum in index order, as the reference
+        float s = 0.f;
+        for (int e = 0; e < E; e++) s += R.p[e];
+        R.sum = s;
+    }
+    __syncthreads();
+    const float s = R.sum;
+    for (int e = tid; e < E; e += kThreads) R.p[e] = R.p[e] / s;
+    __syncthreads();
+    // rank(e) = #{f better than e}, better = (p desc, index asc): the reference's strict
+    // '>' scan from the lowest index picks exactly this order
+    for (int e = tid; e < E; e += kThreads) {
+        const float pe = R.p[e];
+        int rank = 0;
+        for (int f = 0; f < E; f++) {
+            const float pf = R.p[f];
+            rank += (pf > pe || (pf == pe && f < e)) ? 1 : 0;
+        }
+        if (rank < K) {
+            R.idx[rank] = e;
+            R.val[rank] = pe;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double t = 0.0;
+        for (int w = 0; w < kWaves; w++) t += R.redd[w];
+        const float shgt = 1.f / (1.f + expf(-(float)t));
+        float sm = 0.f;
+        for (int k = 0; k < K; k++) sm += R.val[k];
+        unsigned long long *route = a.tagv + E;
+        for (int k = 0; k < K; k++) {
+            const float v = R.val[k] / sm;
+            tag_put(&route[k], a.epoch, __int_as_float(R.idx[k]));
+            tag_put(&route[K + k], a.epoch, v);
+            if (a.idx_out) a.idx_out[k] = R.idx[k];
+            if (a.val_out) a.val_out[k] = v;
+        }
+        tag_put(&route[2 * K], a.epoch, shgt);
+        if (a.val_out) a.val_out[K] = shgt;
+    }
+}
+
+// ---------------------------------------------------------------- LDS of the kernel
+union MoeLds {
+    XPrep x;       // G tiles
+    HPrep h;       // D tiles
+    RouteLds r;    // T tile
+};
+
+// ---------------------------------------------------------------- G tile
+template <int LPR, int CU>
+__device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, int *s_e) {
+    const MoeGeom &g = a.g;
+    if (threadIdx.x == 0) {
+        int e = a.E;
+        if (slot < a.K) e = __float_as_int(tag_get(&a.tagv[a.E + slot], a.epoch, a.err));
+        if (e < 0 || e > a.E) {
+            __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            e = a.E;
+        }
+        *s_e = e;
+    }
+    __syncthreads();
+    const ExpertRec rec = a.rec[*s_e];
+    const int j = (threadIdx.x & 63) % LPR;
+    LaneX<CU> L;
+    lane_geo<CU>(j, g.nlG, g.D, g.gs, L);
+    lane_x<CU>(P, g.gs, L);
+    unsigned long long *hs = a.tagv + a.E + 2 * a.K + 1 + (size_t)slot * g.I;
+    const uint32_t ep = a.epoch;
+    gateup_rows<LPR, CU>(L, rec, g, r0, [&](int r, float h) { tag_put(&hs[r], ep, h); });
+}
+
+// ---------------------------------------------------------------- D tile
+// y_s[r] = down_s row r . h_s for the K routed slots and the shared one, then
+// out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt y_sh, the reference's order
+// (c/qwen.c:870-877, :917).  Weight loads go out as soon as the route is known.
+template <int TPR>
+__device__ void tile_down(const MoeArgs &a, HPrep &H, int r0, ExpertRec *s_rec, float *s_w) {
+    const int tid = threadIdx.x;
+    const int K = a.K, NS = K + 1;
+    const unsigned long long *route = a.tagv + a.E;
+    if (tid < NS) {
+        int e = a.E;
+        if (tid < K) e = __float_as_int(tag_get(&route[tid], a.epoch, a.err));
+        if (e < 0 || e > a.E) {
+            __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            e = a.E;
+        }
+        s_rec[tid] = a.rec[e];
+        s_w[tid] = tag_get(&route[K + tid], a.epoch, a.err);   // val[0..K), then shgt at K
+    }
+    __syncthreads();
+    // h of every slot: each thread polls its words until all carry this launch's tag
+    const unsigned long long *hall = a.tagv + a.E + 2 * K + 1;
+    const int nw = NS * (a.g.I / 8);
+    const uint32_t ep = a.epoch;
+    int *err = a.err;
+    down_rows<TPR>(a.g, NS, s_rec, s_w, H, r0, a.dRows, a.out, a.accumulate, [&](float (&hv)[kHWords][8]) {
+        for (int polls = 0;; polls++) {
+            bool all = true;
+#pragma unroll
+            for (int k = 0; k < kHWords; k++) {
+                const int q = tid + k * kThreads;
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const unsigned long long v = q < nw ? aload(hall + (size_t)q * 8 + c) : 0ull;
+                    all &= q >= nw || (uint32_t)(v >> 32) == ep;
+                    hv[k][c] = __uint_as_float((uint32_t)v);
+                }
+            }
+            if (all || poll_give_up(err, polls)) break;
+        }
+    });
+}
+
+// ---------------------------------------------------------------- the persistent kernel
+template <int LPRG, int TPRD>
+__global__ __launch_bounds__(kThreads) void moe_block_kernel(MoeArgs a) {
+    __shared__ MoeLds S;
+    __shared__ int s_ticket, s_xvalid;
+    __shared__ int s_e[1];
+    __shared__ ExpertRec s_rec[kMaxSlots];
+    __shared__ float s_w[kMaxSlots];
+    const MoeGeom &g = a.g;
+    const int K = a.K;
+    const int nR = (a.E + kRRows - 1) / kRRows;
+    const int tGs = nR, tT = nR + a.nG, tGk = tT + 1, tD = tGk + K * a.nG, total = tD + a.nD;
+    if (blockIdx.x == 0 && threadIdx.x == 0)   // the previous launch's counter is free now
+        __hip_atomic_store(&a.tickets[(a.epoch + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) s_xvalid = 0;
+    __syncthreads();
+    int t = blockIdx.x;
+    while (t < total) {
+        const bool gtile = t >= tGs && t < tD && t != tT;
+        if (gtile && !s_xvalid) {   // x digits for the G tiles of this block
+            XRegs xr;
+            prep_load(a.x, g.D, g.nlG * kLaneChunks * 32, xr);
+            prep_x(xr, g.gs, g.nlG * kLaneChunks * 32, S.x);
+            if (threadIdx.x == 0) s_xvalid = 1;
+        }
+        if (t < tGs) tile_router(a, t * kRRows);
+        else if (t < tT) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
+        else if (t == tT) tile_route(a, S.r);
+        else if (t < tD) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
+        else tile_down<TPRD>(a, S.h, (t - tD) * a.dRows, s_rec, s_w);
+        if ((int)gridDim.x >= total) break;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            s_ticket = (int)gridDim.x + (int)atomicAdd(&a.tickets[a.epoch & 1], 1u);
+            if (!gtile) s_xvalid = 0;   // the LDS union was reused
+        }
+        __syncthreads();
+        t = s_ticket;
+    }
+}
+
+// ---------------------------------------------------------------- expert table
+struct EgTable {
+    int n_layers = 0, E = 0, D = 0, I = 0, gs = 0;
+    ExpertRec *d_rec = nullptr;   // device [n_layers][E + 1]
+    ExpertRec *h_rec = nullptr;   // host mirror
+    uint8_t *valid = nullptr;     // host [n_layers][E + 1]
+    float *d_shgate = nullptr;    // device [n_layers][D]
+    size_t rec_cap = 0, sg_cap = 0;
+    MoeGeom geom;
+    int geom_set = 0;
+};
+static EgTable g_eg;
+
+struct MoeScratch {
+    void *tag = nullptr;
+    size_t tag_cap = 0;
+    void *misc = nullptr;         // tickets [2] at 0, err at 64
+    size_t misc_cap = 0;
+    uint32_t epoch = 0;
+};
+static MoeScratch g_ms;
+
+static bool geom_of(const ColiVkTensor *gt, const ColiVkTensor *dt, MoeGeom &m) {
+    if (!gt || !dt || gt->fmt != 6 || dt->fmt != 6 || gt->layout != kLayoutLanes || dt->layout != kLayoutLanes)
+        return false;
+    memset(&m, 0, sizeof(m));
+    m.D = gt->I;
+    m.I = gt->O;
+    m.gs = gt->gs;
+    m.ngD = gt->ng;
+    m.ngI = dt->ng;
+    m.nlG = gt->nl;
+    m.nlD = dt->nl;
+    m.rbG = gt->row_bytes;
+    m.rbD = dt->row_bytes;
+    return dt->I == m.I && dt->O == m.D && dt->gs == m.gs;
+}
+
+static bool same_geom(const MoeGeom &a, const MoeGeom &b) { return memcmp(&a, &b, sizeof(a)) == 0; }
+
+// every lane's 64 columns of a down row lie in one group; h fits the kernel's LDS
+static bool geom_supported(const MoeGeom &m) {
+    return m.gs % 64 == 0 && m.I % 64 == 0 && m.I >= 128 && m.I <= kMoeMaxI && m.D >= 192 && m.D <= kLaneMaxI &&
+           m.D % 64 == 0;
+}
+
+static int pow2_ceil(int n) {
+    int l = 1;
+    while (l < n) l <<= 1;
+    return l;
+}
+
+// Dispatch over the compiled shapes: LPRG = lanes per gate/up row (D / 64 rounded up to a
+// power of two, 4..64), TPRD = threads per down row (2 x I / 64 likewise, 4..16).
+template <template <int, int> class F, typename A>
+static bool dispatch_shape(const MoeGeom &m, A &arg, hipStream_t st) {
+    const int lg = pow2_ceil(m.nlG), td = 2 * pow2_ceil(m.nlD);
+#define COLI_MOE_CASE(LG, TD) \
+    if (lg == LG && td == TD) return F<LG, TD>::run(arg, st);
+#define COLI_MOE_ROW(LG) COLI_MOE_CASE(LG, 4) COLI_MOE_CASE(LG, 8) COLI_MOE_CASE(LG, 16)
+    COLI_MOE_ROW(4) COLI_MOE_ROW(8) COLI_MOE_ROW(16) COLI_MOE_ROW(32) COLI_MOE_ROW(64)
+#undef COLI_MOE_ROW
+#undef COLI_MOE_CASE
+    return false;
+}
+
+template <int LPRG, int TPRD>
+struct LaunchMoe {
+    static bool run(MoeArgs &a, hipStream_t st) {
+        auto kern = moe_block_kernel<LPRG, TPRD>;
+        a.gRows = kGSteps * kWaves * (64 / LPRG);
+        a.nG = (a.g.I + a.gRows - 1) / a.gRows;
+        a.dRows = kWaves * (64 / TPRD);
+        a.nD = (a.g.D + a.dRows - 1) / a.dRows;
+        static int per = 0;
+        if (!per) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, kThreads, 0) != hipSuccess || per < 1)
+                per = 1;
+        }
+        const int nR = (a.E + kRRows - 1) / kRRows;
+        const long tiles = nR + a.nG + 1 + (long)a.K * a.nG + a.nD;
+        long nb = (long)n_cu() * per;
+        if (nb > tiles) nb = tiles;
+        hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail("moe launch", e);
+        return true;
+    }
+};
+
+// A refused call returns false with one line on stderr (once per reason).
+static bool reject(const char *why) {
+    static const char *last = nullptr;
+    if (why != last) fprintf(stderr, "[HIP] moe block refused: %s\n", why);
+    last = why;
+    return false;
+}
+
+// The layer's MoE block on device pointers (stream-ordered, no sync).  Launches share one
+// scratch area: issue them on one stream.
+bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
+                int *d_idx, float *d_val, hipStream_t st) {
+    EgTable &T = g_eg;
+    if (!ok()) return false;
+    if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return reject("no expert table for the layer");
+    if (!router || !d_x || !d_out) return reject("NULL argument");
+    if (K < 1 || K > kTopK || K > T.E || T.E > kMaxE) return reject("K outside 1..8 or E above 1024");
+    if (router->I != T.D || router->O != T.E || (router->fmt != 0 && router->fmt != 1) ||
+        router->layout != kLayoutRows)
+        return reject("router is not [E, D] fmt 0 or 1");
+    for (int e = 0; e <= T.E; e++)
+        if (!T.valid[(size_t)layer * (T.E + 1) + e]) return reject("expert table slot not set");
+    const MoeGeom &m = T.geom;
+    const size_t ntag = (size_t)T.E + 2 * K + 1 + (size_t)(K + 1) * m.I;
+    if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, 256)) return false;
+    if (++g_ms.epoch == 0) g_ms.epoch = 1;   // 0 is what fresh scratch holds
+    MoeArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = d_x;
+    a.rw = router->w;
+    a.rs = router->sz;
+    a.rfmt = router->fmt;
+    a.rrb = router->row_bytes;
+    a.E = T.E;
+    a.rec = T.d_rec + (size_t)layer * (T.E + 1);
+    a.sh_gate = T.d_shgate + (size_t)layer * T.D;
+    a.K = K;
+    a.out = d_out;
+    a.accumulate = accumulate;
+    a.idx_out = d_idx;
+    a.val_out = d_val;
+    a.tagv = (unsigned long long *)g_ms.tag;
+    a.tickets = (unsigned *)g_ms.misc;
+    a.err = (int *)((uint8_t *)g_ms.misc + 64);
+    a.epoch = g_ms.epoch;
+    a.g = m;
+    return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
+}
+
+// 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id
+int moe_error() {
+    if (!g_ms.misc) return 0;
+    int e = 0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (hipMemcpy(&e, (uint8_t *)g_ms.misc + 64, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (e) {
+        const int z = 0;
+        if (hipMemcpy((uint8_t *)g_ms.misc + 64, &z, 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return e;
+}
+
+// ---------------------------------------------------------------- expert group kernels
+// Items (expert record, input row) of the host-routed ABI path: h = silu(g x) * (u x),
+// then y = d h, one launch each; nothing is combined (the caller weighs and accumulates).
+struct EgItems {
+    const ExpertRec *rec;     // [n] per item
+    const float *x;           // rows [n_x, D]
+    const int *xrow;          // [n] row of x per item
+    float *h;                 // [n, I]
+    float *y;                 // [n, D]
+    int n;
+    int gRows, nG, dRows, nD;
+    MoeGeom g;
+};
+
+template <int LPR>
+__global__ __launch_bounds__(kThreads) void eg_gateup_kernel(EgItems it) {
+    __shared__ XPrep P;
+    const MoeGeom &g = it.g;
+    const int item = blockIdx.x / it.nG, r0 = (blockIdx.x % it.nG) * it.gRows;
+    const int j = (threadIdx.x & 63) % LPR;
+    XRegs xr;
+    prep_load(it.x + (size_t)it.xrow[item] * g.D, g.D, g.nlG * kLaneChunks * 32, xr);
+    prep_x(xr, g.gs, g.nlG * kLaneChunks * 32, P);
+    LaneX<kLaneChunks> L;
+    lane_geo<kLaneChunks>(j, g.nlG, g.D, g.gs, L);
+    lane_x<kLaneChunks>(P, g.gs, L);
+    float *h = it.h + (size_t)item * g.I;
+    gateup_rows<LPR, kLaneChunks>(L, it.rec[item], g, r0, [&](int r, float v) { h[r] = v; });
+}
+
+template <int TPR>
+__global__ __launch_bounds__(kThreads) void eg_down_kernel(EgItems it) {
+    __shared__ HPrep H;
+    __shared__ ExpertRec s_rec[1];
+    const int item = blockIdx.x / it.nD, r0 = (blockIdx.x % it.nD) * it.dRows;
+    if (threadIdx.x == 0) s_rec[0] = it.rec[item];
+    __syncthreads();
+    const float one = 1.f;
+    const float *hsrc = it.h + (size_t)item * it.g.I;
+    const int nw = it.g.I / 8;
+    down_rows<TPR>(it.g, 1, s_rec, &one, H, r0, it.dRows, it.y + (size_t)item * it.g.D, 0,
+                   [&](float (&hv)[kHWords][8]) {
+#pragma unroll
+                       for (int k = 0; k < kHWords; k++) {
+                           const int q = threadIdx.x + k * kThreads;
+#pragma unroll
+                           for (int c = 0; c < 8; c++) hv[k][c] = q < nw ? hsrc[q * 8 + c] : 0.f;
+                       }
+                   });
+}
+
+template <int LPRG, int TPRD>
+struct LaunchEg {
+    static bool run(EgItems &it, hipStream_t st) {
+        it.gRows = kGSteps * kWaves * (64 / LPRG);
+        it.nG = (it.g.I + it.gRows - 1) / it.gRows;
+        it.dRows = kWaves * (64 / TPRD);
+        it.nD = (it.g.D + it.dRows - 1) / it.dRows;
+        hipLaunchKernelGGL(eg_gateup_kernel<LPRG>, dim3(it.n * it.nG), dim3(kThreads), 0, st, it);
+        hipLaunchKernelGGL(eg_down_kernel<TPRD>, dim3(it.n * it.nD), dim3(kThreads), 0, st, it);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail("expert group launch", e);
+        return true;
+    }
+};
+
+// ---------------------------------------------------------------- expert group state
+// One group in flight (c/backend_vulkan.c:1648).  Pinned staging holds rec | xrow | x | y.
+struct EgGroup {
+    int inflight = 0;
+    size_t y_off = 0, y_bytes = 0;
+    void *d_buf = nullptr;
+    size_t d_cap = 0;
+    void *h_buf = nullptr;
+    size_t h_cap = 0;
+    void *d_xs = nullptr;     // bound prefill rows (coli_vk_eg_xs_bind)
+    size_t d_xs_cap = 0;
+    int xs_S = 0, xs_D = 0;
+    hipEvent_t done = nullptr;
+};
+static EgGroup g_grp;
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Validate a group (c/backend_vulkan.c:1418-1440) and issue it.  tok_ids != NULL: rows
+// come from the bound xs; otherwise x is packed [sum(rows), D].
+static bool eg_submit(ColiVkTensor *const *gates, ColiVkTensor *const *ups, ColiVkTensor *const *downs,
+                      const int *rows, int count, const float *x, const int *tok_ids) {
+    if (!ok() || count < 1 || count > 64 || !gates || !ups || !downs || !rows) return false;
+    MoeGeom m;
+    if (!geom_of(gates[0], downs[0], m) || !geom_supported(m)) return false;
+    int total = 0;
+    for (int c = 0; c < count; c++) {
+        MoeGeom mc, mu;
+        if (rows[c] < 1 || !geom_of(gates[c], downs[c], mc) || !same_geom(mc, m) || !ups[c] ||
+            !geom_of(ups[c], downs[c], mu) || !same_geom(mu, m))
+            return false;
+        total += rows[c];
+    }
+    if (tok_ids && (!g_grp.d_xs || g_grp.xs_D != m.D)) return false;
+    const size_t rec_b = al256((size_t)total * sizeof(ExpertRec)), xrow_b = al256((size_t)total * 4);
+    const size_t x_b = tok_ids ? 0 : al256((size_t)total * m.D * 4);
+    const size_t h_b = al256((size_t)total * m.I * 4), y_b = (size_t)total * m.D * 4;
+    if (!scratch(&g_grp.d_buf, &g_grp.d_cap, rec_b + xrow_b + x_b + h_b + al256(y_b))) return false;
+    if (!host_scratch(&g_grp.h_buf, &g_grp.h_cap, rec_b + xrow_b + x_b + y_b)) return false;
+    uint8_t *hb = (uint8_t *)g_grp.h_buf;
+    ExpertRec *hrec = (ExpertRec *)hb;
+    int *hrow = (int *)(hb + rec_b);
+    for (int c = 0, p = 0; c < count; c++)
+        for (int r = 0; r < rows[c]; r++, p++) {
+            hrec[p] = {gates[c]->w, ups[c]->w, downs[c]->w, gates[c]->sz, ups[c]->sz, downs[c]->sz};
+            hrow[p] = tok_ids ? tok_ids[p] : p;
+            if (hrow[p] < 0 || (tok_ids && hrow[p] >= g_grp.xs_S)) return false;
+        }
+    if (!tok_ids) memcpy(hb + rec_b + xrow_b, x, (size_t)total * m.D * 4);
+    uint8_t *db = (uint8_t *)g_grp.d_buf;
+    EgItems it;
+    memset(&it, 0, sizeof(it));
+    it.rec = (const ExpertRec *)db;
+    it.xrow = (const int *)(db + rec_b);
+    it.x = tok_ids ? (const float *)g_grp.d_xs : (const float *)(db + rec_b + xrow_b);
+    it.h = (float *)(db + rec_b + xrow_b + x_b);
+    it.y = (float *)(db + rec_b + xrow_b + x_b + h_b);
+    it.n = total;
+    it.g = m;
+    hipError_t e = hipMemcpyAsync(db, hb, rec_b + xrow_b + x_b, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("expert group upload", e);
+    if (!dispatch_shape<LaunchEg>(m, it, stream())) return false;
+    g_grp.y_off = rec_b + xrow_b + x_b;
+    g_grp.y_bytes = y_b;
+    e = hipMemcpyAsync(hb + g_grp.y_off, it.y, y_b, hipMemcpyDeviceToHost, stream());
+    if (e == hipSuccess && !g_grp.done) e = hipEventCreateWithFlags(&g_grp.done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(g_grp.done, stream());
+    if (e != hipSuccess) return fail("expert group issue", e);
+    g_grp.inflight = 1;
+    return true;
+}
+
+static bool eg_take(float *y) {
+    if (!g_grp.inflight) return false;
+    g_grp.inflight = 0;
+    const hipError_t e = hipEventSynchronize(g_grp.done);
+    if (e != hipSuccess) return fail("expert group take", e);
+    memcpy(y, (uint8_t *)g_grp.h_buf + g_grp.y_off, g_grp.y_bytes);
+    return true;
+}
+
+// ---------------------------------------------------------------- residual stream
+struct StreamState {
+    float *d_resid = nullptr;
+    size_t resid_cap = 0;
+    float *h_y = nullptr;         // pinned staging of stream_add
+    size_t hy_cap = 0;
+    float *d_y = nullptr;
+    size_t dy_cap = 0;
+    float *d_fnw = nullptr;       // final norm weight
+    size_t fnw_cap = 0;
+    int fn_D = 0;
+    float *d_xn = nullptr;        // normed row + argmax result
+    size_t xn_cap = 0;
+    int D = 0, live = 0;
+};
+static StreamState g_str;
+
+__global__ void silu_mul_kernel(const float *g, const float *u, float *h, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float gv = g[i];
+        h[i] = gv / (1.f + expf(-gv)) * u[i];
+    }
+}
+
+__global__ void vec_add_kernel(float *r, const float *y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) r[i] = r[i] + y[i];
+}
+
+static void *g_gu_d = nullptr, *g_gu_h = nullptr;
+static size_t g_gu_dc = 0, g_gu_hc = 0;
+
+}  // namespace coli
+
+using namespace coli;
+
+extern "C" int coli_vk_tensor_ensure(ColiVkTensor **, const void *, const float *, int, int, int, int);
+
+// ---------------------------------------------------------------- ABI: expert group
+// c/backend_vulkan.h:85-101, c/backend_vulkan.c:1645-1697.  Gate/up/down must be fmt 6
+// in the lanes layout (D <= 4096, I <= 1024, gs % 64 == 0); otherwise 0 (the caller
+// computes on the CPU, as it does when the reference rejects a group).
+COLI_API int coli_vk_expert_group_issue(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                        ColiVkTensor *const *downs, const int *rows, int count, const float *x) {
+    if (g_grp.inflight || !x) return 0;
+    return eg_submit(gates, ups, downs, rows, count, x, nullptr) ? 1 : 0;
+}
+
+COLI_API int coli_vk_expert_group_take(float *y) { return y && eg_take(y) ? 1 : 0; }
+
+COLI_API int coli_vk_expert_group(ColiVkTensor *const *gates, ColiVkTensor *const *ups, ColiVkTensor *const *downs,
+                                  const int *rows, int count, float *y, const float *x) {
+    if (g_grp.inflight || !x || !y) return 0;
+    if (!eg_submit(gates, ups, downs, rows, count, x, nullptr)) return 0;
+    return eg_take(y) ? 1 : 0;
+}
+
+COLI_API int coli_vk_eg_gather_available(void) { return ok() ? 1 : 0; }
+
+// c/backend_vulkan.c:1656-1666: bind the prefill rows once; issue_id then names rows
+COLI_API int coli_vk_eg_xs_bind(const float *xs, int S, int D) {
+    if (!ok() || !xs || S < 1 || D < 1 || g_grp.inflight) return 0;
+    const size_t xb = (size_t)S * D * 4;
+    if (!scratch(&g_grp.d_xs, &g_grp.d_xs_cap, xb)) return 0;
+    const hipError_t e = hipMemcpy(g_grp.d_xs, xs, xb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail("xs bind", e) ? 1 : 0;
+    g_grp.xs_S = S;
+    g_grp.xs_D = D;
+    return 1;
+}
+
+COLI_API int coli_vk_expert_group_issue_id(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                           ColiVkTensor *const *downs, const int *rows, int count,
+                                           const int *tok_ids) {
+    if (g_grp.inflight || !tok_ids) return 0;
+    return eg_submit(gates, ups, downs, rows, count, nullptr, tok_ids) ? 1 : 0;
+}
+
+// c/backend_vulkan.h:75-79, c/backend_vulkan.c:1300-1344: hidden[s, o] = silu(gate x_s) * up x_s
+COLI_API int coli_vk_gate_up(ColiVkTensor **gate, ColiVkTensor **up, float *hidden, const float *x, const void *gw,
+                             const float *gsc, const void *uw, const float *usc, int fmt, int S, int D, int I,
+                             int grp) {
+    if (!gate || !up || !hidden || !x || S < 1 || D < 1 || I < 1) return 0;
+    if (!coli_vk_tensor_ensure(gate, gw, gsc, fmt, D, I, grp) || !coli_vk_tensor_ensure(up, uw, usc, fmt, D, I, grp))
+        return 0;
+    const size_t xb = (size_t)S * D * 4, hb = (size_t)S * I * 4;
+    if (!scratch(&g_gu_d, &g_gu_dc, al256(xb) + 3 * al256(hb)) || !host_scratch(&g_gu_h, &g_gu_hc, xb > hb ? xb : hb))
+        return 0;
+    uint8_t *db = (uint8_t *)g_gu_d;
+    float *dx = (float *)db, *dg = (float *)(db + al256(xb)), *du = (float *)(db + al256(xb) + al256(hb));
+    float *dh = (float *)(db + al256(xb) + 2 * al256(hb));
+    memcpy(g_gu_h, x, xb);
+    hipError_t e = hipMemcpyAsync(dx, g_gu_h, xb, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("gate_up upload", e) ? 1 : 0;
+    if (!gemv(*gate, dx, dg, S, stream()) || !gemv(*up, dx, du, S, stream())) return 0;
+    const size_t n = (size_t)S * I;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream(), dg, du, dh, n);
+    e = hipMemcpyAsync(g_gu_h, dh, hb, hipMemcpyDeviceToHost, stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(stream());
+    if (e != hipSuccess) return fail("gate_up", e) ? 1 : 0;
+    memcpy(hidden, g_gu_h, hb);
+    return 1;
+}
+
+// ---------------------------------------------------------------- ABI: expert table
+// c/backend_vulkan.h:243-252, c/backend_vulkan.c:3019-3091: slot [layer][eid], the shared
+// expert at eid = E, plus the layer's shared-expert gate vector.  All experts of a layer
+// must be set before the layer's indexed MoE runs (every expert stays resident in HBM).
+COLI_API int coli_vk_moe_ix_available(void) { return ok() ? 1 : 0; }
+
+// Calling init again re-dimensions the table and clears every slot (as the reference,
+// :3028-3049); the old device arrays are kept when they are large enough.
+COLI_API int coli_vk_eg_table_init(int n_layers, int E, int D, int I, int gs) {
+    EgTable &T = g_eg;
+    if (!ok() || n_layers < 1 || E < 1 || E > kMaxE || D < 1 || I < 1 || gs < 8) return 0;
+    const size_t nrec = (size_t)n_layers * (E + 1), nsg = (size_t)n_layers * D;
+    if (!sync_stream("expert table")) return 0;   // launches in flight may read the table
+    if (nrec > T.rec_cap) {
+        ExpertRec *d_rec = (ExpertRec *)arena_alloc(nrec * sizeof(ExpertRec));
+        ExpertRec *h_rec = (ExpertRec *)calloc(nrec, sizeof(ExpertRec));
+        uint8_t *valid = (uint8_t *)calloc(nrec, 1);
+        if (!d_rec || !h_rec || !valid) {
+            free(h_rec);
+            free(valid);
+            return 0;
+        }
+        free(T.h_rec);
+        free(T.valid);
+        T.d_rec = d_rec;
+        T.h_rec = h_rec;
+        T.valid = valid;
+        T.rec_cap = nrec;
+    }
+    if (nsg > T.sg_cap) {
+        float *d_sg = (float *)arena_alloc(nsg * 4);
+        if (!d_sg) return 0;
+        T.d_shgate = d_sg;
+        T.sg_cap = nsg;
+    }
+    memset(T.valid, 0, T.rec_cap);
+    T.geom_set = 0;
+    T.n_layers = n_layers;
+    T.E = E;
+    T.D = D;
+    T.I = I;
+    T.gs = gs;
+    return 1;
+}
+
+static int eg_table_put(int layer, int eid, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d) {
+    EgTable &T = g_eg;
+    if (!ok() || !T.d_rec || layer < 0 || layer >= T.n_layers || eid < 0 || eid > T.E || !g || !u || !d) return 0;
+    MoeGeom m, mu;
+    if (!geom_of(g, d, m) || !geom_of(u, d, mu) || !same_geom(m, mu) || !geom_supported(m)) return 0;
+    if (m.D != T.D || m.I != T.I || m.gs != T.gs) return 0;
+    if (T.geom_set && !same_geom(m, T.geom)) return 0;
+    T.geom = m;
+    T.geom_set = 1;
+    const size_t i = (size_t)layer * (T.E + 1) + eid;
+    T.h_rec[i] = {g->w, u->w, d->w, g->sz, u->sz, d->sz};
+    // stream-ordered after any launch that still reads the table
+    const hipError_t e = hipMemcpyAsync(T.d_rec + i, &T.h_rec[i], sizeof(ExpertRec), hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("expert table", e) ? 1 : 0;
+    if (!sync_stream("expert table")) return 0;
+    T.valid[i] = 1;
+    return 1;
+}
+
+COLI_API int coli_vk_eg_table_set(int layer, int eid, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d) {
+    if (eid < 0 || eid >= g_eg.E) return 0;
+    return eg_table_put(layer, eid, g, u, d);
+}
+
+COLI_API int coli_vk_eg_table_set_shared(int layer, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d,
+                                         const float *sh_gate, int D) {
+    EgTable &T = g_eg;
+    if (!sh_gate || D != T.D || !eg_table_put(layer, T.E, g, u, d)) return 0;
+    const hipError_t e =
+        hipMemcpyAsync(T.d_shgate + (size_t)layer * T.D, sh_gate, (size_t)D * 4, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("shared gate upload", e) ? 1 : 0;
+    return sync_stream("shared gate upload") ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- ABI: residual stream
+// c/backend_vulkan.h:206-221.  The stream-routed decode (c/qwen.c:1495-1560) also needs
+// the GDN/GQA route_pipe layer blocks, which this library does not provide:
+// stream_available reports 0 so the engine keeps its host-routed flow.  The residual
+// entry points themselves work.
 COLI_API int coli_vk_stream_available(void) { return 0; }
-COLI_API int coli_vk_stream_begin(const float *, int) { return 0; }
-COLI_API int coli_vk_stream_end(float *, int) { return 0; }
-COLI_API int coli_vk_stream_add(const float *, int) { return 0; }
+
+COLI_API int coli_vk_stream_begin(const float *x, int D) {
+    if (!ok() || !x || D < 1) return 0;
+    if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4)) return 0;
+    if (!sync_stream("stream begin")) return 0;
+    const hipError_t e = hipMemcpy(g_str.d_resid, x, (size_t)D * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail("stream begin", e) ? 1 : 0;
+    g_str.D = D;
+    g_str.live = 1;
+    return 1;
+}
+
+COLI_API int coli_vk_stream_end(float *x, int D) {
+    if (!g_str.live || D != g_str.D) return 0;
+    if (!sync_stream("stream end")) return 0;
+    if (x && hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    g_str.live = 0;
+    return 1;
+}
+
+COLI_API int coli_vk_stream_add(const float *y, int D) {
+    if (!g_str.live || !y || D != g_str.D) return 0;
+    if (!host_scratch((void **)&g_str.h_y, &g_str.hy_cap, (size_t)D * 4) ||
+        !scratch((void **)&g_str.d_y, &g_str.dy_cap, (size_t)D * 4))
+        return 0;
+    memcpy(g_str.h_y, y, (size_t)D * 4);
+    const hipError_t e = hipMemcpyAsync(g_str.d_y, g_str.h_y, (size_t)D * 4, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("stream add", e) ? 1 : 0;
+    hipLaunchKernelGGL(vec_add_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), g_str.d_resid, g_str.d_y, D);
+    return sync_stream("stream add") ? 1 : 0;
+}
+
 COLI_API const float *coli_vk_stream_nrm(void) { return nullptr; }
-COLI_API int coli_vk_final_norm_weight(const float *, int) { return 0; }
-COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **, const void *, const float *, int, int, int, int, float,
-                                        int *, float *) { return 0; }
-COLI_API int coli_vk_stream_copy_resid(float *, int) { return 0; }
+
+COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
+    if (!x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
+    if (!sync_stream("copy resid")) return 0;
+    return hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+}
+
+// c/backend_vulkan.c:2692-2711
+COLI_API int coli_vk_final_norm_weight(const float *w, int D) {
+    if (!ok() || !w || D < 1) return 0;
+    if (!scratch((void **)&g_str.d_fnw, &g_str.fnw_cap, (size_t)D * 4)) return 0;
+    if (!sync_stream("final norm weight")) return 0;
+    if (hipMemcpy(g_str.d_fnw, w, (size_t)D * 4, hipMemcpyHostToDevice) != hipSuccess) return 0;
+    g_str.fn_D = D;
+    return 1;
+}
+
+// c/backend_vulkan.c:2713-2782: final RMSNorm of the device residual + lm_head + argmax,
+// only the winner is read back
+COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weights, const float *scales, int fmt,
+                                        int I, int O, int gs, float eps, int *idx, float *val) {
+    if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
+    if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
+    if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, (size_t)I * 4 + 64)) return 0;
+    float *xn = g_str.d_xn;
+    int *d_iv = (int *)(xn + I);
+    if (!rmsnorm_zc(g_str.d_resid, g_str.d_fnw, xn, I, eps, stream())) return 0;
+    TopkOut tk = {1, d_iv, (float *)(d_iv + 8)};
+    if (!gemv(*tensor, xn, nullptr, 1, stream(), &tk)) return 0;
+    int res[16];
+    if (!sync_stream("stream_norm_argmax") || hipMemcpy(res, d_iv, 64, hipMemcpyDeviceToHost) != hipSuccess)
+        return 0;
+    *idx = res[0];
+    if (val) memcpy(val, &res[8], 4);
+    return 1;
+}
+
 COLI_API void coli_vk_route_cache_stats(void) {}
-COLI_API void coli_vk_decode_prof(double, int) {}
-COLI_API int coli_vk_expert_group_issue_pipe(ColiVkTensor *const *, ColiVkTensor *const *, ColiVkTensor *const *,
-                                             const int *, const float *, int, int) { return 0; }
-COLI_API int coli_vk_expert_group_take_pipe(void) { return 0; }
-COLI_API int coli_vk_moe_ix_available(void) { return 0; }
-COLI_API int coli_vk_eg_table_init(int, int, int, int, int) { return 0; }
-COLI_API int coli_vk_eg_table_set(int, int, ColiVkTensor *, ColiVkTensor *, ColiVkTensor *) { return 0; }
-COLI_API int coli_vk_eg_table_set_shared(int, ColiVkTensor *, ColiVkTensor *, ColiVkTensor *, const float *, int) {
+COLI_API void coli_vk_decode_prof(double decode_ms, int tokens) { (void)decode_ms, (void)tokens; }
+
+// stream-routed MoE pieces (c/backend_vulkan.h:229-252): they need the route_pipe blocks
+COLI_API int coli_vk_expert_group_issue_pipe(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
+                                             ColiVkTensor *const *downs, const int *rows, const float *weights,
+                                             int count, int D) {
+    (void)gates, (void)ups, (void)downs, (void)rows, (void)weights, (void)count, (void)D;
     return 0;
 }
+COLI_API int coli_vk_expert_group_take_pipe(void) { return 0; }
 COLI_API int coli_vk_stream_moe_fused(void) { return 0; }
 COLI_API int coli_vk_stream_ix_pending(void) { return 0; }
-COLI_API int coli_vk_stream_ix_hist(int, int *, int) { return 0; }
+COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
+    (void)layer, (void)idx_out, (void)K;
+    return 0;
+}
+
+// ---------------------------------------------------------------- device-pointer MoE
+// The layer's whole MoE block in one launch on `stream` (NULL = the library's stream):
+// out = sum_k val_k y_k + shgt y_sh (accumulate != 0: out += that).  d_idx [K] and d_val
+// [K + 1] (renormed weights, then shgt) are optional.  Launches share one scratch area:
+// issue them on one stream.
+COLI_API int coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out,
+                                 int accumulate, int *d_idx, float *d_val, void *stream_) {
+    return moe_decode(layer, router, K, d_x, d_out, accumulate, d_idx, d_val,
+                      stream_ ? (hipStream_t)stream_ : stream())
+               ? 1
+               : 0;
+}
+
+// Error flag of the MoE launches since the last call (synchronizes the device):
+// 0 none, 1 a poll gave up, 2 a route held an out-of-range expert id, -1 runtime error.
+COLI_API int coli_hip_moe_error(void) { return moe_error(); }
