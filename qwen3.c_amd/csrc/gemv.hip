@@ -13,8 +13,9 @@
 // plus one scale recombination per lane, about 35 VALU wave-instructions per KiB of
 // weights.
 //
-// Top-k: each block reduces its rows' candidates and writes k partials; a one-block
-// kernel merges them (stream order makes the partials visible; no device-scope fences).
+// Top-k (fused): each block reduces its rows' candidates and publishes its k best as
+// epoch-tagged 64-bit keys; the last block of the grid merges them in the same launch,
+// polling the tags (agent-scope atomics: no device-scope fences, no second launch).
 #include "fmt6_device.h"
 
 #include <stdio.h>
@@ -24,10 +25,12 @@ namespace coli {
 
 struct TopkArgs {
     int k;                       // 0 = off
-    float *part_v;               // k > 1: [gridDim.x * kTopK] block partials
+    float *part_v;               // topk_partial: [gridDim.x * kTopK] block partials
     int *part_i;
-    unsigned long long *slots;   // k == 1: kArgSlots epoch-tagged keys
-    uint32_t epoch;              // k == 1: tag of this launch (8 bits used)
+    unsigned long long *slots;   // argmax: kArgSlots keys; fused top-k: [gridDim.x * kTopK] keys
+    uint32_t epoch;              // tag of this launch (8 bits used)
+    int *out_i;                  // fused top-k: the k best (value desc, index asc)
+    float *out_v;
 };
 
 // ---- argmax as a 64-bit key: [63:56] launch epoch, [55:24] order-preserving bits of the
@@ -54,6 +57,184 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 // merge this block's per-thread lists and publish its k best as partials
 __device__ void topk_publish(float (&tv)[kTopK], int (&ti)[kTopK], const TopkArgs &tk) {
     block_topk_merge<kTopK>(tv, ti, tk.k, tk.part_v + blockIdx.x * kTopK, tk.part_i + blockIdx.x * kTopK);
+}
+
+__device__ __forceinline__ unsigned long long aload64(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kFusedGrid = 1024;           // largest grid of a fused top-k launch
+constexpr int kFusedWaves = kFusedGrid * 4;   // wave maxima slots (kWaves waves per block)
+constexpr int kFusedSlots = 64;             // largest per-wave candidate count
+constexpr int kFusedPollLimit = 1 << 20;
+
+// Selection works on keys without the tag: a real key keeps its 56 bits, the padding key
+// (tag only) becomes 1 so that it ranks below every real key but above "no entry" (0).
+__device__ __forceinline__ unsigned long long strip_tag(unsigned long long key) {
+    const unsigned long long v = key & 0x00FFFFFFFFFFFFFFull;
+    return v ? v : (key ? 1ull : 0ull);
+}
+
+// decode a (tag-stripped) key into (row, value); padding and "no entry" -> (INT_MAX, -inf)
+__device__ __forceinline__ void key_decode(unsigned long long key, int *row, float *val) {
+    const uint32_t low = (uint32_t)(key & 0xFFFFFFu);
+    if (key <= 1ull || low == 0u) {
+        *row = INT_MAX;
+        *val = -INFINITY;
+        return;
+    }
+    const uint32_t ord = (uint32_t)(key >> 24);
+    const uint32_t u = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+    *row = (int)(0xFFFFFFu - low);
+    *val = __uint_as_float(u);
+}
+
+// Wave-wide maximum of an unsigned value by DPP (no LDS traffic), broadcast to all lanes.
+#define COLI_DPP_UMAX(v, ctrl, rmask) \
+    max((v), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xF, false))
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror
+    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15
+    v = COLI_DPP_UMAX(v, 0x143, 0xC);   // row_bcast31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Wave-wide maximum of 56-bit keys (ordered value, then 0xFFFFFF - row; the launch tag is
+// common to all): two DPP passes.  Returns the key without its tag.
+__device__ __forceinline__ unsigned long long wave_key_max(unsigned long long key) {
+    const uint32_t hi = (uint32_t)(key >> 24), lo = (uint32_t)(key & 0xFFFFFFu);
+    const uint32_t mh = wave_umax(hi);
+    const uint32_t ml = wave_umax(hi == mh ? lo : 0u);
+    return ((unsigned long long)mh << 24) | ml;
+}
+
+// Selection rounds in one wave over per-lane key lists kv[N] (unsorted, tags stripped):
+// round r takes the wave's largest key, the lane holding it drops it.  out[r] = that key
+// (uniform; 0 once the lists are empty) and src[r] = its lane-major index lane * N + q.
+template <int N>
+__device__ __forceinline__ void wave_select(unsigned long long (&kv)[N], int k, unsigned long long (&out)[kTopK],
+                                            int (&src)[kTopK]) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long lm = 0ull;
+    int li = 0;
+#pragma unroll
+    for (int q = 0; q < N; q++)
+        if (kv[q] > lm) {
+            lm = kv[q];
+            li = q;
+        }
+#pragma unroll
+    for (int r = 0; r < kTopK; r++) {
+        out[r] = 0ull;
+        src[r] = -1;
+        if (r >= k) continue;
+        const unsigned long long m = wave_key_max(lm);
+        const unsigned long long who = __ballot(lm == m && lm != 0ull);
+        if (!who) continue;
+        const int wl = __ffsll((long long)who) - 1;
+        out[r] = m;
+        src[r] = __builtin_amdgcn_readlane(li + lane * N, wl);
+        if (lane == wl) {
+#pragma unroll
+            for (int q = 0; q < N; q++)
+                if (q == li) kv[q] = 0ull;
+            lm = 0ull;
+            li = 0;
+#pragma unroll
+            for (int q = 0; q < N; q++)
+                if (kv[q] > lm) {
+                    lm = kv[q];
+                    li = q;
+                }
+        }
+    }
+}
+
+// The grid's last block: the k best keys of the launch.  Units are waves: every wave
+// published its largest key (wmax) and one key per slot it owns (cand).  The global top k
+// can only come from the k waves whose maxima rank in the top k (a key of any other wave
+// is beaten by k maxima), so: (1) each of the 4 waves selects the k best maxima of a
+// quarter of the units, (2) wave 0 selects the k best of those 4k, (3) wave 0 selects the
+// k best of the <= k x 64 keys of the chosen waves.  Keys of another launch carry another
+// tag and are polled until overwritten.
+__device__ void topk_final_block(const TopkArgs &tk, int nunits, int per_wave) {
+    __shared__ unsigned long long s_key[kWaves * kTopK];
+    __shared__ int s_unit[kWaves * kTopK];
+    constexpr int kQ = kFusedWaves / kThreads;   // 16 maxima per lane
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = tk.k;
+    const unsigned long long tag = (unsigned long long)(tk.epoch & 0xFFu);
+    const unsigned long long *wmax = tk.slots, *cand = tk.slots + kFusedWaves;
+    unsigned long long top[kTopK];
+    int src[kTopK];
+    bool fine = true;
+    {   // (1) wave w: units w * 1024 + lane + 64 q
+        unsigned long long kv[kQ];
+        for (int polls = 0;; polls++) {
+            bool all = true;
+#pragma unroll
+            for (int q = 0; q < kQ; q++) {
+                const int u = wave * (kFusedWaves / kWaves) + lane + 64 * q;
+                kv[q] = u < nunits ? aload64(&wmax[u]) : 0ull;
+                all &= u >= nunits || (kv[q] >> 56) == tag;
+            }
+            if (__all(all)) break;
+            if (polls > kFusedPollLimit) {
+                fine = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int q = 0; q < kQ; q++) kv[q] = strip_tag(kv[q]);
+        wave_select<kQ>(kv, k, top, src);
+#pragma unroll
+        for (int r = 0; r < kTopK; r++)
+            if (lane == r) {   // src = lane' * kQ + q  ->  unit w * 1024 + lane' + 64 q
+                s_key[wave * kTopK + r] = top[r];
+                s_unit[wave * kTopK + r] =
+                    src[r] < 0 ? -1 : wave * (kFusedWaves / kWaves) + src[r] / kQ + 64 * (src[r] % kQ);
+            }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // (2) the k best of the 4k unit maxima (one per lane)
+    unsigned long long k1[1] = {lane < kWaves * kTopK ? s_key[lane] : 0ull};
+    wave_select<1>(k1, k, top, src);
+    int sel[kTopK];
+#pragma unroll
+    for (int r = 0; r < kTopK; r++) sel[r] = src[r] < 0 ? -1 : s_unit[src[r]];
+    // (3) the keys of the chosen units: entry q of lane = slot `lane` of unit sel[q]
+    unsigned long long kc[kTopK];
+    for (int polls = 0;; polls++) {
+        bool all = true;
+#pragma unroll
+        for (int q = 0; q < kTopK; q++) {
+            const bool on = sel[q] >= 0 && lane < per_wave;
+            kc[q] = on ? aload64(&cand[(size_t)sel[q] * per_wave + lane]) : 0ull;
+            all &= !on || (kc[q] >> 56) == tag;
+        }
+        if (__all(all)) break;
+        if (polls > kFusedPollLimit) {
+            fine = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int q = 0; q < kTopK; q++) kc[q] = strip_tag(kc[q]);
+    wave_select<kTopK>(kc, k, top, src);
+#pragma unroll
+    for (int r = 0; r < kTopK; r++)
+        if (lane == r && r < k) {
+            int row;
+            float v;
+            key_decode(top[r], &row, &v);
+            tk.out_i[r] = fine ? row : -1;
+            tk.out_v[r] = v;
+        }
 }
 
 // The k best of nblk sorted partial lists (k entries each).  The global top k can only
@@ -142,16 +323,16 @@ __global__ void argmax_reset(unsigned long long *slots) {
 //   MODE 1: also argmax: leader lanes keep their best key, the block reduces it and
 //           atomicMax-es it into slot blockIdx % kArgSlots (no fences: atomics are
 //           coherent, and the reader runs after the kernel).
-//   MODE 2: also top-k: every (value, row) is parked in dynamic LDS (wave-private slots,
-//           `per_wave` entries per wave); after the row loop the block publishes the k
-//           best of its rows as partials for topk_final.
+//   MODE 2: also top-k, fused: leader lanes store one tagged key per row slot of their
+//           wave (`per_wave` slots, padding keys for slots past the end) and keep the
+//           wave's largest key, which lane 0 publishes; the grid's last block then
+//           merges (topk_final_block).
 template <int LPR, int CU, int U, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restrict__ W, const float *__restrict__ SZ,
                                                         const float *__restrict__ x, float *__restrict__ y, int I,
                                                         int O, int gs, int ng, int nl, int row_bytes, TopkArgs tk,
                                                         int per_wave) {
     __shared__ XPrep P;
-    extern __shared__ float2 s_cand[];   // MODE 2: [kWaves * per_wave] (value, row as bits)
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane % LPR, seg = lane / LPR;
@@ -178,15 +359,15 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
         sro[u] = rr[u] * srb;
         lane_load<CU>(rw, rs, min(wro[u], wtot), min(sro[u], stot), L, wq[u], sv[u]);
     }
-    if constexpr (MODE == 2)   // unfilled slots rank below every real candidate
-        for (int e = threadIdx.x; e < kWaves * per_wave; e += kThreads)
-            s_cand[e] = make_float2(-INFINITY, __int_as_float(INT_MAX));
-    prep_x(xr, gs, ncols, P);   // (its barriers also order the padding stores)
+    prep_x(xr, gs, ncols, P);
     lane_x<CU>(P, gs, L);
 
     const uint32_t rlim = (uint32_t)((O + RPW - 1) / RPW) * RPW;   // rows the grid walks
-    int slot = 0;                    // MODE 2: next LDS slot of this wave
-    unsigned long long best = 0ull;  // MODE 1: best key of this lane's rows
+    int slot = 0;                    // MODE 2: next candidate slot of this wave
+    // best key of this lane's rows (MODE 2 starts at the padding key: waves without
+    // rows still publish a tagged maximum)
+    unsigned long long best = MODE == 2 ? (unsigned long long)(tk.epoch & 0xFFu) << 56 : 0ull;
+    unsigned long long *cand = tk.slots + kFusedWaves + (size_t)(blockIdx.x * kWaves + wave) * per_wave;
     for (uint32_t base = (uint32_t)rg0 * RPW; base < rlim; base += rstep) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -204,9 +385,11 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
                     const unsigned long long key = valid ? arg_key(tk.epoch, acc, r) : 0ull;
                     best = key > best ? key : best;
                 }
-                if constexpr (MODE == 2)
-                    s_cand[wave * per_wave + slot + seg] =
-                        valid ? make_float2(acc, __int_as_float((int)r)) : make_float2(-INFINITY, __int_as_float(INT_MAX));
+                if constexpr (MODE == 2) {
+                    const unsigned long long key = valid ? arg_key(tk.epoch, acc, r) : best & (0xFFull << 56);
+                    __hip_atomic_store(&cand[slot + seg], key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    best = key > best ? key : best;
+                }
             }
             if constexpr (MODE == 2) slot += RPW;
         }
@@ -224,16 +407,21 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
         }
     }
     if constexpr (MODE == 2) {
-        __syncthreads();
-        float tv[kTopK];
-        int ti[kTopK];
-        topk_clear<kTopK>(tv, ti);
-        for (int e = threadIdx.x; e < kWaves * per_wave; e += kThreads) {
-            const float2 c = s_cand[e];
-            topk_insert<kTopK>(tv, ti, c.x, __float_as_int(c.y));
-        }
-        topk_publish(tv, ti, tk);
+        const unsigned long long pad = (unsigned long long)(tk.epoch & 0xFFu) << 56;
+        for (int e = slot + lane; e < per_wave; e += 64)   // slots this wave's rows did not reach
+            __hip_atomic_store(&cand[e], pad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        best = wave_max_u64(best);
+        if (lane == 0)
+            __hip_atomic_store(&tk.slots[blockIdx.x * kWaves + wave], best, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (blockIdx.x == gridDim.x - 1) topk_final_block(tk, gridDim.x * kWaves, per_wave);
     }
+}
+
+// clear the fused top-k keys (all tags 0) when the 8-bit launch tag wraps
+__global__ void keys_reset(unsigned long long *keys, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) keys[i] = 0ull;
 }
 
 // Top-k pass over a logit vector: each block keeps per-thread lists of a strided slice
@@ -361,14 +549,14 @@ static int launch_lanes(const ColiVkTensor *t, const float *x, float *y, hipStre
     const long nrg = (t->O + rpw - 1) / rpw;
     const long work = (nrg + (long)kWaves * kU - 1) / ((long)kWaves * kU);
     auto kern = gemv6_lanes<LPR, CU, kU, MODE>;
-    const int nb = grid_size(work, occupancy(kern));
+    int nb = grid_size(work, occupancy(kern));
+    if (MODE == 2 && nb > kFusedGrid) nb = kFusedGrid;   // the fused merge reads at most kFusedGrid blocks
     int per_wave = 0;
     size_t lds = 0;
     if (MODE == 2) {
         const long nw = (long)nb * kWaves;
         per_wave = (int)((nrg + nw * kU - 1) / (nw * kU)) * kU * rpw;   // slots one wave fills
-        lds = (size_t)kWaves * per_wave * sizeof(float2);
-        if (lds > 96 * 1024) return 0;
+        if (per_wave > kFusedSlots) return 0;   // more rows than the fused merge reads per wave
     }
     hipLaunchKernelGGL(kern, dim3(nb), dim3(kThreads), lds, st, t->w, t->sz, x, y, t->I, t->O, t->gs, t->ng, t->nl,
                        t->row_bytes, ta, per_wave);
@@ -404,7 +592,7 @@ static int launch_lanes_mode(const ColiVkTensor *t, const float *x, float *y, hi
 static bool launch_one(const ColiVkTensor *t, const float *x, float *y, hipStream_t st) {
     int nb;
     if (t->layout == kLayoutLanes) {
-        const TopkArgs none = {0, nullptr, nullptr, nullptr, 0};
+        const TopkArgs none = {0, nullptr, nullptr, nullptr, 0, nullptr, nullptr};
         nb = launch_lanes_mode<0>(t, x, y, st, none);
     } else {
         nb = grid_size((t->O + kWaves - 1) / kWaves, occupancy(gemv_generic));
@@ -421,13 +609,16 @@ static size_t g_logits_cap = 0;
 static void *g_slots = nullptr;    // argmax slots (kArgSlots keys)
 static size_t g_slots_cap = 0;
 static uint32_t g_epoch = 0;
+static void *g_keys = nullptr;     // fused top-k keys: wave maxima, then per-slot candidates
+static size_t g_keys_cap = 0;
+static uint32_t g_tk_epoch = 0;
 
 bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t st) {
     if (k < 1 || k > kTopK || n < 1) return false;
     long nbp = ((long)n + kThreads * 8 - 1) / (kThreads * 8);
     if (nbp > (long)n_cu() * 2) nbp = (long)n_cu() * 2;
     if (!scratch(&g_tk.buf, &g_tk.cap, (size_t)nbp * kTopK * 8)) return false;
-    TopkArgs ta = {k, (float *)g_tk.buf, (int *)((float *)g_tk.buf + (size_t)nbp * kTopK), nullptr, 0};
+    TopkArgs ta = {k, (float *)g_tk.buf, (int *)((float *)g_tk.buf + (size_t)nbp * kTopK), nullptr, 0, nullptr, nullptr};
     hipLaunchKernelGGL(topk_partial, dim3((unsigned)nbp), dim3(kThreads), 0, st, d_v, n, ta);
     hipLaunchKernelGGL(topk_final, dim3(1), dim3(kFinalThreads), 0, st, ta.part_v, ta.part_i, (int)nbp, k, d_val,
                        d_idx);
@@ -451,7 +642,7 @@ bool gemv_argmax(const ColiVkTensor *t, const float *d_x, float *d_y, hipStream_
         hipLaunchKernelGGL(argmax_reset, dim3(1), dim3(64), 0, st, (unsigned long long *)g_slots);
         g_epoch = 1;
     }
-    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch};
+    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch, nullptr, nullptr};
     if (!launch_lanes_mode<1>(t, d_x, d_y, st, ta)) return false;
     *epoch = g_epoch;
     *slots = (const unsigned long long *)g_slots;
@@ -475,18 +666,16 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
         if (e != hipSuccess) return fail("argmax decode", e);
         return true;
     }
-    if (want_k && t->layout == kLayoutLanes) {   // fused: block partials from the GEMV itself
-        const size_t maxb = (size_t)n_cu() * kMaxBlocksPerCU;
-        if (!scratch(&g_tk.buf, &g_tk.cap, maxb * kTopK * 8)) return false;
-        const TopkArgs ta = {tk->k, (float *)g_tk.buf, (int *)((float *)g_tk.buf + maxb * kTopK), nullptr, 0};
-        const int nb = launch_lanes_mode<2>(t, d_x, d_y, st, ta);
-        if (nb) {
-            hipLaunchKernelGGL(topk_final, dim3(1), dim3(kFinalThreads), 0, st, ta.part_v, ta.part_i, nb, ta.k,
-                               tk->val, tk->idx);
-            const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return fail("topk launch", e);
-            return true;
+    if (want_k && t->layout == kLayoutLanes && t->O < (1 << 24)) {   // fused: one launch
+        const int n = kFusedWaves + kFusedGrid * kWaves * kFusedSlots;
+        if (!scratch(&g_keys, &g_keys_cap, (size_t)n * 8)) return false;
+        g_tk_epoch = (g_tk_epoch + 1) & 0xFFu;
+        if (g_tk_epoch == 0) {   // tags wrap: clear the keys so no old key carries the new tag
+            hipLaunchKernelGGL(keys_reset, dim3((n + 255) / 256), dim3(256), 0, st, (unsigned long long *)g_keys, n);
+            g_tk_epoch = 1;
         }
+        const TopkArgs ta = {tk->k, nullptr, nullptr, (unsigned long long *)g_keys, g_tk_epoch, tk->idx, tk->val};
+        if (launch_lanes_mode<2>(t, d_x, d_y, st, ta)) return true;
         if (!ok()) return false;   // otherwise (LDS too small) fall through to separate passes
     }
     for (int s = 0; s < S; s++)

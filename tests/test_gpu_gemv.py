@@ -270,3 +270,46 @@ def test_device_synth_matches_host(lib, gen):
     r = np.empty(64 * inf["row_bytes"] // 4, np.float32)
     lib.memcpy(r.ctypes.data, inf["d_w"], r.nbytes)
     assert np.array_equal(r.reshape(64, -1)[:, :I].reshape(-1), gen.f32rows(64, I, seed, 0.02))
+
+
+def test_topk_fused_many_launches(lib, orc, torch_dev):
+    """300 fused top-8 launches in a row (the 8-bit launch tag wraps), new x each time:
+    every result equals the exact selection over that launch's logits."""
+    import torch
+    O, I = 3000, 2048
+    t = lib.tensor_synth(6, I, O, 128, 0x70F, 0.02)
+    dx = torch.empty(I, dtype=torch.float32, device=torch_dev)
+    dy = torch.empty(O, dtype=torch.float32, device=torch_dev)
+    di = torch.empty(8, dtype=torch.int32, device=torch_dev)
+    dv = torch.empty(8, dtype=torch.float32, device=torch_dev)
+    oi = np.empty(8, np.int32)
+    ov = np.empty(8, np.float32)
+    for n in range(300):
+        lib.synth_normal_dev(dx.data_ptr(), I, 1000 + n, 1.0)
+        k = 1 + n % 8
+        lib.gemv_topk_dev(t, dx.data_ptr(), dy.data_ptr(), k, di.data_ptr(), dv.data_ptr())
+        lib.sync()
+        y = dy.cpu().numpy()
+        orc.orc_topk_logits(P(y), O, k, P(oi), P(ov))
+        assert np.array_equal(di.cpu().numpy()[:k], oi[:k]), n
+        assert np.array_equal(dv.cpu().numpy()[:k], ov[:k]), n
+
+
+def test_topk_unfused_shape(lib, orc, torch_dev):
+    """A shape whose rows per wave exceed the fused merge (O=300000, I=256): GEMV then a
+    separate top-k pass; same exact selection."""
+    import torch
+    O, I = 300000, 256
+    t = lib.tensor_synth(6, I, O, 64, 0x7A1, 0.02)
+    dx = torch.empty(I, dtype=torch.float32, device=torch_dev)
+    dy = torch.empty(O, dtype=torch.float32, device=torch_dev)
+    di = torch.empty(8, dtype=torch.int32, device=torch_dev)
+    dv = torch.empty(8, dtype=torch.float32, device=torch_dev)
+    lib.synth_normal_dev(dx.data_ptr(), I, 5, 1.0)
+    lib.gemv_topk_dev(t, dx.data_ptr(), dy.data_ptr(), 8, di.data_ptr(), dv.data_ptr())
+    lib.sync()
+    y = dy.cpu().numpy()
+    oi = np.empty(8, np.int32)
+    ov = np.empty(8, np.float32)
+    orc.orc_topk_logits(P(y), O, 8, P(oi), P(ov))
+    assert np.array_equal(di.cpu().numpy(), oi) and np.array_equal(dv.cpu().numpy(), ov)
