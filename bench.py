@@ -8,10 +8,13 @@ launch.  One step = one such launch with all inputs resident in HBM; two weight 
 alternate so the 287 MB stream cannot be served from the 256 MB Infinity Cache.
 
 Prints ONE JSON line (rank 0, N=1).  `value` is the achieved HBM bandwidth of the step
-in GB/s from algorithmic bytes (nibbles + f32 [scale, zero] pairs + x + logits).
-`roofline` prices the launch against the 8 TB/s HBM3E peak; `cpu_baseline` times the
-reference's own CPU kernel (c/qwen.c:211-229, compiled from the reference checkout into
-oracle/_ref) on this host over a bounded row sample.
+in GB/s from algorithmic bytes (nibbles + f32 [scale, zero] pairs + x + logits) over the
+average launch duration, measured with one pair of HIP events around the K launches on
+the library's stream.  `roofline` prices that launch against the 8 TB/s HBM3E peak, with
+`traffic` = HBM bytes per launch from rocprofv3 counters (profiles/gemv6_lmhead_traffic.json).
+`moe_cfg2` times configs[2] (one decode MoE block, one launch) the same way.
+`cpu_baseline` times the reference's own CPU kernel (c/qwen.c:211-229, compiled from the
+reference checkout into oracle/_ref) on this host over a bounded row sample.
 """
 import argparse
 import ctypes as C
@@ -40,14 +43,78 @@ def load_product():
     return mod
 
 
-def profile_traffic():
+def profile_traffic(name):
     """HBM bytes per launch measured by rocprofv3 --pmc (committed summary), or None."""
-    p = os.path.join(ROOT, "profiles", "gemv6_lmhead_traffic.json")
+    p = os.path.join(ROOT, "profiles", name)
     try:
         with open(p) as f:
             return json.load(f).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
+
+
+def time_launches(lib, ext, step, steps, warmup):
+    """Average duration of `step` (launches on the library stream): one event pair around
+    `steps` back-to-back launches; also the host wall time per step."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    lib.sync()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(ext)
+    for i in range(steps):
+        step(i)
+    b.record(ext)
+    lib.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return a.elapsed_time(b) / steps, wall * 1e3 / steps
+
+
+def moe_cfg2(lib, torch, dev, steps, warmup):
+    """router f32 256x2048, 256 routed + 1 shared expert (gate/up 512x2048,
+    down 2048x512, fmt 6 gs 128, all resident), top-8, one launch per block.  x changes
+    every step (16 seeded vectors) so the routed experts change."""
+    D, I, E, K, gs = 2048, 512, 256, 8, 128
+    base = 0xC2
+    lib.eg_table_init(1, E, D, I, gs)
+    keep = []
+    for e in range(E + 1):
+        g = lib.tensor_synth(6, D, I, gs, base * 4096 + 3 * e, 0.02)
+        u = lib.tensor_synth(6, D, I, gs, base * 4096 + 3 * e + 1, 0.02)
+        d = lib.tensor_synth(6, I, D, gs, base * 4096 + 3 * e + 2, 0.02)
+        keep.append((g, u, d))
+        if e < E:
+            lib.eg_table_set(0, e, g, u, d)
+    router = lib.tensor_synth(0, D, E, 0, base * 4096 + 9999, 0.02)
+    sh_gate = torch.empty(D, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(sh_gate.data_ptr(), D, base + 5, 0.02)
+    lib.sync()
+    lib.eg_table_set_shared(0, *keep[E], sh_gate.cpu().numpy())
+    nx = 16
+    xs = torch.empty(nx, D, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(xs.data_ptr(), nx * D, base + 6, 1.0)
+    out = torch.empty(D, dtype=torch.float32, device=dev)
+    lib.sync()
+
+    def step(i):
+        lib.moe_decode_dev(0, router, K, xs[i % nx].data_ptr(), out.data_ptr())
+
+    ext = torch.cuda.ExternalStream(lib.stream())
+    ms, wall_ms = time_launches(lib, ext, step, steps, warmup)
+    if lib.moe_error():
+        raise RuntimeError("MoE block reported a device-side error")
+    # per expert: gate + up (I rows of D) and down (D rows of I): nibbles + [scale, zero]
+    per_expert = 2 * (I * D // 2 + I * (D // gs) * 8) + (D * I // 2 + D * (I // gs) * 8)
+    nbytes = (K + 1) * per_expert + E * D * 4 + D * 4 + D * 4 + D * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "cfg2: MoE block decode, router f32 256x2048 + top-8 of 256 experts + shared, "
+                        "gate/up 512x2048 down 2048x512 fmt6 gs128, one launch",
+            "us_per_op": round(ms * 1e3, 2), "wall_us_per_step": round(wall_ms * 1e3, 2),
+            "alg_bytes_per_launch": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+            "traffic": profile_traffic("moe_cfg2_traffic.json")}
 
 
 def cpu_baseline(budget_s=12.0):
@@ -96,7 +163,21 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-moe", action="store_true", help="skip the configs[2] MoE block line")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 plain 256 MiB device copies (the reference point that scales the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        n = 256 * 1024 * 1024 // 4
+        a = torch.empty(n, dtype=torch.float32, device="cuda:0").normal_()
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_each_way": n * 4, "copies": 5}), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the fmt=6 GEMV/MoE path runs on a single "
               "MI355X; see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
@@ -122,26 +203,9 @@ def main():
     def step(i):
         lib.gemv_topk_dev(w[i & 1], x.data_ptr(), y.data_ptr(), 8, idx.data_ptr(), val.data_ptr())
 
-    for i in range(args.warmup):
-        step(i)
-    lib.sync()
-    torch.cuda.synchronize()
-
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(ext)
-        step(i)
-        ev[i][1].record(ext)
-    lib.sync()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    kern_ms.sort()
-    avg_ms = sum(kern_ms) / len(kern_ms)
+    avg_ms, ms_per_step = time_launches(lib, ext, step, args.steps, args.warmup)
     bytes_per = alg_bytes_lmhead()
     achieved = bytes_per / (avg_ms * 1e-3) / 1e9
-    ms_per_step = wall * 1e3 / args.steps
 
     out = {
         "metric": METRIC,
@@ -159,12 +223,14 @@ def main():
         "config": {"workload": "cfg1: lm_head fmt6 GEMV 248320x2048 gs128 + fused device top-8",
                    "rows": O_VOCAB, "K": K_HID, "group_size": GS, "topk": 8, "weight_copies": 2},
         "us_per_op": round(avg_ms * 1e3, 2),
-        "us_per_op_median": round(kern_ms[len(kern_ms) // 2] * 1e3, 2),
         "lmhead_tok_s": round(1e3 / avg_ms, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": profile_traffic(),
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": profile_traffic("gemv6_lmhead_traffic.json"),
+                     "kernel": "gemv6_lanes<32,2,4,2> (fmt6 GEMV + fused top-8)",
                      "alg_bytes_per_launch": bytes_per},
     }
+    if not args.no_moe:
+        out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

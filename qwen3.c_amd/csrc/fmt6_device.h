@@ -45,6 +45,92 @@ __device__ __forceinline__ float seg_sum(float v) {
     return v;
 }
 
+// Wave-wide sum of a double by DPP on its two halves; the sum is valid in lane 63 and
+// is returned broadcast to all lanes.
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, RMASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, RMASK, 0xF, false);
+    return __builtin_bit_cast(double, ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+    v += dpp_d<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v += dpp_d<0x141, 0xF>(v);   // row_half_mirror
+    v += dpp_d<0x140, 0xF>(v);   // row_mirror
+    v += dpp_d<0x142, 0xA>(v);   // row_bcast15
+    v += dpp_d<0x143, 0xC>(v);   // row_bcast31
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// Wave-wide maximum of an unsigned value by DPP (no LDS traffic), broadcast to all lanes.
+#define COLI_DPP_UMAX(v, ctrl, rmask) \
+    max((v), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xF, false))
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror
+    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15
+    v = COLI_DPP_UMAX(v, 0x143, 0xC);   // row_bcast31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Wave-wide maximum of 56-bit keys (ordered value, then 0xFFFFFF - row; the launch tag is
+// common to all): two DPP passes.  Returns the key without its tag.
+__device__ __forceinline__ unsigned long long wave_key_max(unsigned long long key) {
+    const uint32_t hi = (uint32_t)(key >> 24), lo = (uint32_t)(key & 0xFFFFFFu);
+    const uint32_t mh = wave_umax(hi);
+    const uint32_t ml = wave_umax(hi == mh ? lo : 0u);
+    return ((unsigned long long)mh << 24) | ml;
+}
+
+// Selection rounds in one wave over per-lane key lists kv[N] (unsorted, tags stripped):
+// round r takes the wave's largest key, the lane holding it drops it.  out[r] = that key
+// (uniform; 0 once the lists are empty) and src[r] = its lane-major index lane * N + q.
+template <int N>
+__device__ __forceinline__ void wave_select(unsigned long long (&kv)[N], int k, unsigned long long (&out)[kTopK],
+                                            int (&src)[kTopK]) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long lm = 0ull;
+    int li = 0;
+#pragma unroll
+    for (int q = 0; q < N; q++)
+        if (kv[q] > lm) {
+            lm = kv[q];
+            li = q;
+        }
+#pragma unroll
+    for (int r = 0; r < kTopK; r++) {
+        out[r] = 0ull;
+        src[r] = -1;
+        if (r >= k) continue;
+        const unsigned long long m = wave_key_max(lm);
+        const unsigned long long who = __ballot(lm == m && lm != 0ull);
+        if (!who) continue;
+        const int wl = __ffsll((long long)who) - 1;
+        out[r] = m;
+        src[r] = __builtin_amdgcn_readlane(li + lane * N, wl);
+        if (lane == wl) {
+#pragma unroll
+            for (int q = 0; q < N; q++)
+                if (q == li) kv[q] = 0ull;
+            lm = 0ull;
+            li = 0;
+#pragma unroll
+            for (int q = 0; q < N; q++)
+                if (kv[q] > lm) {
+                    lm = kv[q];
+                    li = q;
+                }
+        }
+    }
+}
+
 // (value desc, index asc): the order of c/shaders/argmax.comp:28,41 and of the host scan
 // c/qwen.c:1471-1472 (ties resolve to the lowest index).
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {

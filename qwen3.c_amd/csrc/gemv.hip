@@ -89,70 +89,6 @@ __device__ __forceinline__ void key_decode(unsigned long long key, int *row, flo
     *val = __uint_as_float(u);
 }
 
-// Wave-wide maximum of an unsigned value by DPP (no LDS traffic), broadcast to all lanes.
-#define COLI_DPP_UMAX(v, ctrl, rmask) \
-    max((v), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xF, false))
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
-    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
-    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
-    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror
-    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15
-    v = COLI_DPP_UMAX(v, 0x143, 0xC);   // row_bcast31
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
-// Wave-wide maximum of 56-bit keys (ordered value, then 0xFFFFFF - row; the launch tag is
-// common to all): two DPP passes.  Returns the key without its tag.
-__device__ __forceinline__ unsigned long long wave_key_max(unsigned long long key) {
-    const uint32_t hi = (uint32_t)(key >> 24), lo = (uint32_t)(key & 0xFFFFFFu);
-    const uint32_t mh = wave_umax(hi);
-    const uint32_t ml = wave_umax(hi == mh ? lo : 0u);
-    return ((unsigned long long)mh << 24) | ml;
-}
-
-// Selection rounds in one wave over per-lane key lists kv[N] (unsorted, tags stripped):
-// round r takes the wave's largest key, the lane holding it drops it.  out[r] = that key
-// (uniform; 0 once the lists are empty) and src[r] = its lane-major index lane * N + q.
-template <int N>
-__device__ __forceinline__ void wave_select(unsigned long long (&kv)[N], int k, unsigned long long (&out)[kTopK],
-                                            int (&src)[kTopK]) {
-    const int lane = threadIdx.x & 63;
-    unsigned long long lm = 0ull;
-    int li = 0;
-#pragma unroll
-    for (int q = 0; q < N; q++)
-        if (kv[q] > lm) {
-            lm = kv[q];
-            li = q;
-        }
-#pragma unroll
-    for (int r = 0; r < kTopK; r++) {
-        out[r] = 0ull;
-        src[r] = -1;
-        if (r >= k) continue;
-        const unsigned long long m = wave_key_max(lm);
-        const unsigned long long who = __ballot(lm == m && lm != 0ull);
-        if (!who) continue;
-        const int wl = __ffsll((long long)who) - 1;
-        out[r] = m;
-        src[r] = __builtin_amdgcn_readlane(li + lane * N, wl);
-        if (lane == wl) {
-#pragma unroll
-            for (int q = 0; q < N; q++)
-                if (q == li) kv[q] = 0ull;
-            lm = 0ull;
-            li = 0;
-#pragma unroll
-            for (int q = 0; q < N; q++)
-                if (kv[q] > lm) {
-                    lm = kv[q];
-                    li = q;
-                }
-        }
-    }
-}
-
 // The grid's last block: the k best keys of the launch.  Units are waves: every wave
 // published its largest key (wmax) and one key per slot it owns (cand).  The global top k
 // can only come from the k waves whose maxima rank in the top k (a key of any other wave

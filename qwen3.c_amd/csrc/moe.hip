@@ -48,9 +48,12 @@ constexpr int kMaxK = 64;                 // c/backend_vulkan.c:3298 (topk <= 64
 constexpr int kMaxE = 1024;
 constexpr int kMaxSlots = kTopK + 1;      // fused kernel: K <= 8 routed + the shared expert
 constexpr int kMoeMaxI = 512;             // expert intermediate size (h staged in LDS)
-constexpr int kRRows = 8;                 // router rows per tile
+constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
 constexpr int kGSteps = 2;                // gate/up row steps per tile
-constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.5-2 us)
+constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
+constexpr int kRouteReps = 16;            // copies of the route block (readers spread over them)
+constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1], K <= 8
+constexpr int kCounterStride = 64;        // u32 counters 256 bytes apart (one per line)
 
 struct MoeArgs {
     const float *x;                       // [D] expert input (post-attention RMSNorm)
@@ -64,12 +67,16 @@ struct MoeArgs {
     int accumulate;                       // out += (residual stream) instead of out =
     int *idx_out;                         // optional [K]
     float *val_out;                       // optional [K + 1] (renormed weights, then shgt)
-    unsigned long long *tagv;             // logits [E] | idx [K] | w [K + 1] | h [(K + 1) * I]
+    unsigned long long *tagv;             // logits [E + 1] | route [kRouteReps][kRouteStride] |
+                                          // h [(K + 1) * I] | y [(K + 1) * D]
+                                          // (logit E = the shared-expert gate dot)
     unsigned *tickets;                    // [2]
+    unsigned *done;                       // [2][2][kMaxSlots] G, then D tiles finished per slot, by
+                                          // launch parity; kCounterStride apart
     int *err;
     uint32_t epoch;
     int gRows, nG;                        // gate/up rows per tile, tiles per expert
-    int dRows, nD;                        // down rows per tile, tiles
+    int nD, nC;                           // down tiles per slot (kDRows rows), combine tiles
     MoeGeom g;
 };
 
@@ -86,8 +93,24 @@ __device__ __forceinline__ bool poll_give_up(int *err, int polls) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     }
-    __builtin_amdgcn_s_sleep(2);
+    if (polls < 8) __builtin_amdgcn_s_sleep(1);   // back off: the line may be in demand
+    else __builtin_amdgcn_s_sleep(8);
     return false;
+}
+
+// tag-buffer regions
+__device__ __forceinline__ unsigned long long *route_of(const MoeArgs &a, int rep) {
+    return a.tagv + a.E + 1 + (size_t)rep * kRouteStride;
+}
+__device__ __forceinline__ unsigned long long *h_of(const MoeArgs &a, int slot) {
+    return a.tagv + a.E + 1 + kRouteReps * kRouteStride + (size_t)slot * a.g.I;
+}
+__device__ __forceinline__ unsigned long long *y_of(const MoeArgs &a, int slot) {
+    return h_of(a, a.K + 1) + (size_t)slot * a.g.D;
+}
+// per-slot counters of this launch: which 0 = G tiles done, 1 = D tiles done
+__device__ __forceinline__ unsigned *counter(const MoeArgs &a, uint32_t epoch, int which, int slot) {
+    return a.done + ((size_t)((epoch & 1) * 2 + which) * kMaxSlots + slot) * kCounterStride;
 }
 __device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t epoch, int *err) {
     for (int polls = 0;; polls++) {
@@ -97,11 +120,6 @@ __device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t e
     }
 }
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -111,13 +129,13 @@ __device__ __forceinline__ float wave_max_f(float v) {
 // ---------------------------------------------------------------- h -> digit planes
 // The down projection uses the same integer-dot arithmetic as the GEMV (fmt6_device.h)
 // with h in place of x: per slot s, limb[s * I/8 + word][digit], qsum[s * I/32 + chunk],
-// gmax[s * ngI + group].
+// gmax[s * ngI + group] (the down tiles prepare one slot, s = 0).
 struct HPrep {
-    uint32_t limb[kMaxSlots * kMoeMaxI / 8][kLimbs];
-    int qsum[kMaxSlots * kMoeMaxI / 32];
-    unsigned gmax[kMaxSlots * kMoeMaxI / 64];
+    uint32_t limb[kMoeMaxI / 8][kLimbs];
+    int qsum[kMoeMaxI / 32];
+    unsigned gmax[kMoeMaxI / 64];
 };
-constexpr int kHWords = (kMaxSlots * kMoeMaxI / 8 + kThreads - 1) / kThreads;
+constexpr int kHWords = (kMoeMaxI / 8 + kThreads - 1) / kThreads;
 
 // v: the thread's words q = tid + k * kThreads (8 columns each) of the NS x I values.
 // Ends with __syncthreads().
@@ -204,39 +222,36 @@ __device__ __forceinline__ float down_chunk(const HPrep &H, int s, int I, int gs
     return sz.x * fmaf(-(sz.y - 8.f), ucs, ldexpf(T, ue));
 }
 
-// Rows r0 + wave * RPW + seg of the down projections of NS slots (recs in LDS), combined
-// as out[r] = ((0 + w_0 y_0) + w_1 y_1) + ... (accumulate: out[r] + that).  gather(hv)
-// fills the thread's h words (see prep_h); weight loads are issued before it.
-template <int TPR, typename Gather>
-__device__ __forceinline__ void down_rows(const MoeGeom &g, int NS, const ExpertRec *recs, const float *wts,
-                                          HPrep &H, int r0, int rows, float *out, int accumulate, Gather gather) {
-    constexpr int RPW = 64 / TPR;
+// Down projection of one slot for kDRows rows r0 ..: y[r] = down row r . h.  Wave w takes
+// rows r0 + (p * kWaves + w) * RPW + seg for passes p; every pass's weight loads are
+// issued before gather(hv) fills the thread's h words (see prep_h).  emit(r, y) per row.
+constexpr int kDRows = 64;
+template <int TPR, typename Gather, typename Emit>
+__device__ __forceinline__ void down_slot(const MoeGeom &g, const ExpertRec &rec, HPrep &H, int r0, Gather gather,
+                                          Emit emit) {
+    constexpr int RPW = 64 / TPR, P = kDRows / (kWaves * RPW);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = lane % TPR, seg = lane / TPR;
     const DownThread d = down_thread<TPR>(g);
     const uint32_t wtot = (uint32_t)g.D * g.rbD, stot = (uint32_t)g.D * g.ngI * 8;
-    const int r = r0 + wave * RPW + seg;
-    const uint32_t rc = (uint32_t)(r < g.D ? r : g.D);   // row D reads 0 (past the end)
-    uint4 wq[kMaxSlots];
-    float2 sv[kMaxSlots];
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(rec.wd, wtot), rs = buf_rsrc(rec.sd, stot);
+    uint4 wq[P];
+    float2 sv[P];
 #pragma unroll
-    for (int s = 0; s < kMaxSlots; s++) {
-        if (s < NS) {
-            wq[s] = buf_load16(buf_rsrc(recs[s].wd, wtot), rc * g.rbD + d.woff);
-            sv[s] = buf_load8f(buf_rsrc(recs[s].sd, stot), rc * g.ngI * 8 + d.soff);
-        }
+    for (int p = 0; p < P; p++) {
+        const int r = r0 + (p * kWaves + wave) * RPW + seg;
+        const uint32_t rc = (uint32_t)(r < g.D ? r : g.D);   // row D reads 0 (past the end)
+        wq[p] = buf_load16(rw, rc * g.rbD + d.woff);
+        sv[p] = buf_load8f(rs, rc * g.ngI * 8 + d.soff);
     }
     float hv[kHWords][8];
     gather(hv);
-    prep_h(hv, NS, g.I, g.gs, g.ngI, H);
-    float accum = 0.f;
+    prep_h(hv, 1, g.I, g.gs, g.ngI, H);
 #pragma unroll
-    for (int s = 0; s < kMaxSlots; s++) {
-        if (s < NS) {
-            const float y = seg_sum<TPR>(down_chunk(H, s, g.I, g.gs, g.ngI, d, wq[s], sv[s]));
-            accum = accum + wts[s] * y;
-        }
+    for (int p = 0; p < P; p++) {
+        const int r = r0 + (p * kWaves + wave) * RPW + seg;
+        const float y = seg_sum<TPR>(down_chunk(H, 0, g.I, g.gs, g.ngI, d, wq[p], sv[p]));
+        if (t == TPR - 1 && r < g.D) emit(r, y);
     }
-    if (t == TPR - 1 && r < g.D && r < r0 + rows) out[r] = accumulate ? out[r] + accum : accum;
 }
 
 // ---------------------------------------------------------------- gate/up rows
@@ -269,121 +284,185 @@ __device__ __forceinline__ void gateup_rows(const LaneX<CU> &L, const ExpertRec 
 }
 
 // ---------------------------------------------------------------- R: router rows
-// Dot products accumulate in fp64 from exact fp64 products, so each logit is the correctly
-// rounded value of the exact sum (the reference sums sequentially in fp32).
+// One row per wave: rows r < E are the router (c/qwen.c:178-189 f32, :230-238 int8), row
+// E is the shared-expert gate vector (c/qwen.c:833).  Dot products accumulate in fp64 from
+// exact fp64 products, so each logit is the correctly rounded value of the exact sum (the
+// reference sums sequentially in fp32).
+__device__ __forceinline__ float4 int8x4(uint32_t q) {
+    return make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16), (float)(int8_t)(q >> 24));
+}
+
 __device__ void tile_router(const MoeArgs &a, int r0) {
     constexpr int kRC = 8;   // float4 per lane and pass: 2048 columns
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.g.D;
-    for (int rr = wave; rr < kRRows; rr += kWaves) {
-        const int r = r0 + rr;
-        if (r >= a.E) break;
-        const uint8_t *row = a.rw + (size_t)r * a.rrb;
-        double acc = 0.0;
-        for (int c0 = 0; c0 < D; c0 += kRC * 256) {
-            float4 xv[kRC];
-            float4 w[kRC];
+    const int r = r0 + wave;
+    if (r > a.E) return;
+    const bool gate = r == a.E;
+    const uint8_t *row = gate ? (const uint8_t *)a.sh_gate : a.rw + (size_t)r * a.rrb;
+    const bool f32 = gate || a.rfmt == 0;
+    double acc = 0.0;
+    for (int c0 = 0; c0 < D; c0 += kRC * 256) {
+        float4 xv[kRC], w[kRC];
 #pragma unroll
-            for (int c = 0; c < kRC; c++) {
-                const int col = c0 + (lane + c * 64) * 4;
-                const bool in = col < D;
-                xv[c] = in ? *(const float4 *)(a.x + col) : make_float4(0.f, 0.f, 0.f, 0.f);
-                if (a.rfmt == 0) {
-                    w[c] = in ? *(const float4 *)(row + (size_t)col * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {   // fmt 1: int8 rows
-                    const uint32_t q = in ? *(const uint32_t *)(row + col) : 0u;
-                    w[c] = make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16),
-                                       (float)(int8_t)(q >> 24));
-                }
-            }
+        for (int c = 0; c < kRC; c++) {
+            const int col = c0 + (lane + c * 64) * 4;
+            const bool in = col < D;
+            xv[c] = in ? *(const float4 *)(a.x + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+            w[c] = !in ? make_float4(0.f, 0.f, 0.f, 0.f)
+                       : f32 ? *(const float4 *)(row + (size_t)col * 4) : int8x4(*(const uint32_t *)(row + col));
+        }
 #pragma unroll
-            for (int c = 0; c < kRC; c++) {
-                acc = fma((double)xv[c].x, (double)w[c].x, acc);
-                acc = fma((double)xv[c].y, (double)w[c].y, acc);
-                acc = fma((double)xv[c].z, (double)w[c].z, acc);
-                acc = fma((double)xv[c].w, (double)w[c].w, acc);
-            }
+        for (int c = 0; c < kRC; c++) {
+            acc = fma((double)xv[c].x, (double)w[c].x, acc);
+            acc = fma((double)xv[c].y, (double)w[c].y, acc);
+            acc = fma((double)xv[c].z, (double)w[c].z, acc);
+            acc = fma((double)xv[c].w, (double)w[c].w, acc);
         }
-        acc = wave_sum_d(acc);
-        if (lane == 0) {
-            float l = (float)acc;
-            if (a.rfmt == 1) l *= a.rs[r];   // c/qwen.c:237: acc * scale[o]
-            tag_put(&a.tagv[r], a.epoch, l);
-        }
+    }
+    acc = wave_sum_dpp(acc);
+    if (lane == 0) {
+        float l = (float)acc;
+        if (!gate && a.rfmt == 1) l *= a.rs[r];   // c/qwen.c:237: acc * scale[o]
+        tag_put(&a.tagv[r], a.epoch, l);
     }
 }
 
 // ---------------------------------------------------------------- T: route
 // c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate.
 struct RouteLds {
-    float p[kMaxE];
+    float p[kMaxE + 64];               // probabilities, zero padded to a multiple of 64
+    unsigned long long cand[kMaxE];    // candidate keys (p bits << 24 | 0xFFFFFF - e)
+    unsigned hmax[2 * kWaves];         // half-wave maxima of the p bits
     float red[kWaves];
-    double redd[kWaves];
-    float sum;
-    int idx[kMaxK];
-    float val[kMaxK];
+    float sum, gate, vsum;
+    int ncand;
+    int idx[kTopK];
+    float val[kTopK];
 };
 
+// u32 maximum over each half wave (32 lanes): valid in lanes 31 and 63
+__device__ __forceinline__ uint32_t half_wave_umax(uint32_t v) {
+    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror: every lane holds its row's max
+    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15: rows 1 and 3 take rows 0 and 2
+    return v;
+}
+
 __device__ void tile_route(const MoeArgs &a, RouteLds &R) {
+    constexpr int kPer = kMaxE / kThreads;   // experts per thread
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.E, K = a.K;
+    const int Epad = (E + 63) & ~63;
     float m = -1e30f;   // the reference's initial max
-    for (int e = tid; e < E; e += kThreads) {
+    for (int e = tid; e <= E; e += kThreads) {   // logit E is the shared-expert gate dot
         const float l = tag_get(&a.tagv[e], a.epoch, a.err);
-        R.p[e] = l;
-        m = fmaxf(m, l);
+        if (e < E) {
+            R.p[e] = l;
+            m = fmaxf(m, l);
+        } else {
+            R.gate = l;
+        }
     }
+    if (tid == 0) R.ncand = 0;
     m = wave_max_f(m);
     if (lane == 0) R.red[wave] = m;
-    // shared expert gate: fp64 dot, rounded once
-    double sg = 0.0;
-    for (int d = tid; d < a.g.D; d += kThreads) sg = fma((double)a.sh_gate[d], (double)a.x[d], sg);
-    sg = wave_sum_d(sg);
-    if (lane == 0) R.redd[wave] = sg;
     __syncthreads();
     m = R.red[0];
 #pragma unroll
     for (int w = 1; w < kWaves; w++) m = fmaxf(m, R.red[w]);
-    for (int e = tid; e < E; e += kThreads) R.p[e] = expf(R.p[e] - m);
+    for (int e = tid; e < Epad; e += kThreads) R.p[e] = e < E ? expf(R.p[e] - m) : 0.f;
     __syncthreads();
-    if (tid == 0) {   // sequential sum in index order, as the reference
+    if (tid == 0) {   // sequential sum in index order, as the reference (the padding adds 0)
         float s = 0.f;
-        for (int e = 0; e < E; e++) s += R.p[e];
+        for (int e0 = 0; e0 < Epad; e0 += 64) {
+            float4 v[16];
+#pragma unroll
+            for (int c = 0; c < 16; c++) v[c] = *(const float4 *)&R.p[e0 + 4 * c];
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                s += v[c].x;
+                s += v[c].y;
+                s += v[c].z;
+                s += v[c].w;
+            }
+        }
         R.sum = s;
     }
     __syncthreads();
     const float s = R.sum;
-    for (int e = tid; e < E; e += kThreads) R.p[e] = R.p[e] / s;
+    uint32_t pb[kPer], mx = 0u;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = tid + q * kThreads;
+        pb[q] = 0u;
+        if (e < E) {
+            const float pv = R.p[e] / s;
+            R.p[e] = pv;
+            pb[q] = __float_as_uint(pv);   // p >= 0: the bits order like the values
+            mx = max(mx, pb[q]);
+        }
+    }
+    // Candidates: p >= theta = the least of the 8 half-wave maxima.  Those maxima are 8
+    // distinct experts with p >= theta, so the K <= 8 best (p desc, index asc) and every
+    // expert tied with the K-th are candidates.
+    mx = half_wave_umax(mx);
+    if (lane == 31 || lane == 63) R.hmax[2 * wave + (lane >> 5)] = mx;
     __syncthreads();
-    // rank(e) = #{f better than e}, better = (p desc, index asc): the reference's strict
-    // '>' scan from the lowest index picks exactly this order
-    for (int e = tid; e < E; e += kThreads) {
-        const float pe = R.p[e];
+    uint32_t theta = R.hmax[0];
+#pragma unroll
+    for (int i = 1; i < 2 * kWaves; i++) theta = min(theta, R.hmax[i]);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = tid + q * kThreads;
+        if (e < E && pb[q] >= theta)
+            R.cand[atomicAdd(&R.ncand, 1)] = ((unsigned long long)pb[q] << 24) | (0xFFFFFFu - (uint32_t)e);
+    }
+    __syncthreads();
+    // rank among the candidates: (p desc, index asc) is the order of the reference's strict
+    // '>' scan from the lowest index (c/qwen.c:810-815)
+    const int nc = R.ncand;
+    for (int c = tid; c < nc; c += kThreads) {
+        const unsigned long long me = R.cand[c];
         int rank = 0;
-        for (int f = 0; f < E; f++) {
-            const float pf = R.p[f];
-            rank += (pf > pe || (pf == pe && f < e)) ? 1 : 0;
+        for (int o0 = 0; o0 < nc; o0 += 8) {   // 8 LDS reads in flight
+            unsigned long long o8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) o8[u] = o0 + u < nc ? R.cand[o0 + u] : 0ull;
+#pragma unroll
+            for (int u = 0; u < 8; u++) rank += o8[u] > me ? 1 : 0;
         }
         if (rank < K) {
-            R.idx[rank] = e;
-            R.val[rank] = pe;
+            R.idx[rank] = (int)(0xFFFFFFu - (uint32_t)(me & 0xFFFFFFu));
+            R.val[rank] = __uint_as_float((uint32_t)(me >> 24));
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        double t = 0.0;
-        for (int w = 0; w < kWaves; w++) t += R.redd[w];
-        const float shgt = 1.f / (1.f + expf(-(float)t));
-        float sm = 0.f;
-        for (int k = 0; k < K; k++) sm += R.val[k];
-        unsigned long long *route = a.tagv + E;
-        for (int k = 0; k < K; k++) {
-            const float v = R.val[k] / sm;
-            tag_put(&route[k], a.epoch, __int_as_float(R.idx[k]));
-            tag_put(&route[K + k], a.epoch, v);
-            if (a.idx_out) a.idx_out[k] = R.idx[k];
-            if (a.val_out) a.val_out[k] = v;
+    // renorm (c/qwen.c:816-817): the sum in rank order, then one lane per slot
+    // thread (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
+    // renormed weights, 2K the shared gate
+    if (tid == 0) {   // the renorm sum in rank order (trailing +0 leaves it unchanged)
+        float v8[kTopK], sm = 0.f;
+#pragma unroll
+        for (int j = 0; j < kTopK; j++) v8[j] = j < K ? R.val[j] : 0.f;
+#pragma unroll
+        for (int j = 0; j < kTopK; j++) sm += v8[j];
+        R.vsum = sm;
+    }
+    __syncthreads();
+    const float sm = R.vsum;
+    for (int q = tid; q < kRouteReps * kRouteStride; q += kThreads) {
+        const int c = q / kRouteStride, k = q % kRouteStride;
+        if (k > 2 * K) continue;
+        float v;
+        if (k < K) v = __int_as_float(R.idx[k]);
+        else if (k < 2 * K) v = R.val[k - K] / sm;
+        else v = 1.f / (1.f + expf(-R.gate));
+        tag_put(&route_of(a, c)[k], a.epoch, v);
+        if (c == 0) {
+            if (k < K && a.idx_out) a.idx_out[k] = R.idx[k];
+            if (k >= K && a.val_out) a.val_out[k - K] = v;
         }
-        tag_put(&route[2 * K], a.epoch, shgt);
-        if (a.val_out) a.val_out[K] = shgt;
     }
 }
 
@@ -398,9 +477,13 @@ union MoeLds {
 template <int LPR, int CU>
 __device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, int *s_e) {
     const MoeGeom &g = a.g;
+    const int j = (threadIdx.x & 63) % LPR;
+    LaneX<CU> L;   // x digits of the lane first: they do not depend on the route
+    lane_geo<CU>(j, g.nlG, g.D, g.gs, L);
+    lane_x<CU>(P, g.gs, L);
     if (threadIdx.x == 0) {
         int e = a.E;
-        if (slot < a.K) e = __float_as_int(tag_get(&a.tagv[a.E + slot], a.epoch, a.err));
+        if (slot < a.K) e = __float_as_int(tag_get(&route_of(a, blockIdx.x % kRouteReps)[slot], a.epoch, a.err));
         if (e < 0 || e > a.E) {
             __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             e = a.E;
@@ -409,41 +492,47 @@ __device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, 
     }
     __syncthreads();
     const ExpertRec rec = a.rec[*s_e];
-    const int j = (threadIdx.x & 63) % LPR;
-    LaneX<CU> L;
-    lane_geo<CU>(j, g.nlG, g.D, g.gs, L);
-    lane_x<CU>(P, g.gs, L);
-    unsigned long long *hs = a.tagv + a.E + 2 * a.K + 1 + (size_t)slot * g.I;
+    unsigned long long *hs = h_of(a, slot);
     const uint32_t ep = a.epoch;
     gateup_rows<LPR, CU>(L, rec, g, r0, [&](int r, float h) { tag_put(&hs[r], ep, h); });
+    __syncthreads();
+    if (threadIdx.x == 0)   // a hint for the D tiles (they still check every tag)
+        __hip_atomic_fetch_add(counter(a, a.epoch, 0, slot), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---------------------------------------------------------------- D tile
-// y_s[r] = down_s row r . h_s for the K routed slots and the shared one, then
-// out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt y_sh, the reference's order
-// (c/qwen.c:870-877, :917).  Weight loads go out as soon as the route is known.
+// ---------------------------------------------------------------- D and C tiles
+// D: y_s[r] = down_s row r . h_s for one slot and kDRows rows.  The slot's G tiles count
+// themselves when done; the tile waits for that count, then reads the tagged h (words not
+// yet of this launch are read again).  C: out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt
+// y_sh, the reference's order (c/qwen.c:870-877, :917).
 template <int TPR>
-__device__ void tile_down(const MoeArgs &a, HPrep &H, int r0, ExpertRec *s_rec, float *s_w) {
-    const int tid = threadIdx.x;
-    const int K = a.K, NS = K + 1;
-    const unsigned long long *route = a.tagv + a.E;
-    if (tid < NS) {
+__device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertRec *s_rec) {
+    const int tid = threadIdx.x, K = a.K;
+    const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
+    if (tid == 0) {
         int e = a.E;
-        if (tid < K) e = __float_as_int(tag_get(&route[tid], a.epoch, a.err));
+        if (slot < K) e = __float_as_int(tag_get(&route[slot], a.epoch, a.err));
         if (e < 0 || e > a.E) {
             __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             e = a.E;
         }
-        s_rec[tid] = a.rec[e];
-        s_w[tid] = tag_get(&route[K + tid], a.epoch, a.err);   // val[0..K), then shgt at K
+        s_rec[0] = a.rec[e];
     }
     __syncthreads();
-    // h of every slot: each thread polls its words until all carry this launch's tag
-    const unsigned long long *hall = a.tagv + a.E + 2 * K + 1;
-    const int nw = NS * (a.g.I / 8);
+    const unsigned long long *hs = h_of(a, slot);
+    unsigned long long *ys = y_of(a, slot);
+    const int nw = a.g.I / 8;
     const uint32_t ep = a.epoch;
     int *err = a.err;
-    down_rows<TPR>(a.g, NS, s_rec, s_w, H, r0, a.dRows, a.out, a.accumulate, [&](float (&hv)[kHWords][8]) {
+    const unsigned *done = counter(a, a.epoch, 0, slot);
+    const unsigned nG = (unsigned)a.nG;
+    auto gather = [&](float (&hv)[kHWords][8]) {
+        if (tid == 0)
+            for (int polls = 0;; polls++)
+                if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nG ||
+                    poll_give_up(err, polls))
+                    break;
+        __syncthreads();
         for (int polls = 0;; polls++) {
             bool all = true;
 #pragma unroll
@@ -451,35 +540,79 @@ __device__ void tile_down(const MoeArgs &a, HPrep &H, int r0, ExpertRec *s_rec, 
                 const int q = tid + k * kThreads;
 #pragma unroll
                 for (int c = 0; c < 8; c++) {
-                    const unsigned long long v = q < nw ? aload(hall + (size_t)q * 8 + c) : 0ull;
+                    const unsigned long long v = q < nw ? aload(hs + (size_t)q * 8 + c) : 0ull;
                     all &= q >= nw || (uint32_t)(v >> 32) == ep;
                     hv[k][c] = __uint_as_float((uint32_t)v);
                 }
             }
             if (all || poll_give_up(err, polls)) break;
         }
-    });
+    };
+    down_slot<TPR>(a.g, s_rec[0], H, r0, gather, [&](int r, float y) { tag_put(&ys[r], ep, y); });
+    __syncthreads();
+    if (tid == 0)   // a hint for the C tiles (they still check every tag)
+        __hip_atomic_fetch_add(counter(a, a.epoch, 1, slot), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kCRows = 64;   // combine tile rows (one thread each)
+__device__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
+    const int tid = threadIdx.x, K = a.K, NS = K + 1, D = a.g.D;
+    const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
+    const unsigned long long *ys = y_of(a, 0);
+    if (tid < NS) {   // the weights, then wait until every slot's D tiles have counted
+        s_w[tid] = tag_get(&route[K + tid], a.epoch, a.err);   // val[0..K), then shgt at K
+        const unsigned *dd = counter(a, a.epoch, 1, tid);
+        for (int polls = 0;; polls++)
+            if (__hip_atomic_load(dd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)a.nD ||
+                poll_give_up(a.err, polls))
+                break;
+    }
+    __syncthreads();
+    const int r = r0 + tid;
+    if (tid >= kCRows || r >= D) return;
+    float y[kMaxSlots];
+    for (int polls = 0;; polls++) {
+        bool all = true;
+#pragma unroll
+        for (int s = 0; s < kMaxSlots; s++) {
+            const unsigned long long v = s < NS ? aload(ys + (size_t)s * D + r) : 0ull;
+            all &= s >= NS || (uint32_t)(v >> 32) == a.epoch;
+            y[s] = __uint_as_float((uint32_t)v);
+        }
+        if (all || poll_give_up(a.err, polls)) break;
+    }
+    float accum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; s++)
+        if (s < NS) accum = accum + s_w[s] * y[s];
+    a.out[r] = a.accumulate ? a.out[r] + accum : accum;
 }
 
 // ---------------------------------------------------------------- the persistent kernel
 template <int LPRG, int TPRD>
-__global__ __launch_bounds__(kThreads) void moe_block_kernel(MoeArgs a) {
+__global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     __shared__ MoeLds S;
     __shared__ int s_ticket, s_xvalid;
     __shared__ int s_e[1];
-    __shared__ ExpertRec s_rec[kMaxSlots];
+    __shared__ ExpertRec s_rec[1];
     __shared__ float s_w[kMaxSlots];
     const MoeGeom &g = a.g;
     const int K = a.K;
-    const int nR = (a.E + kRRows - 1) / kRRows;
-    const int tGs = nR, tT = nR + a.nG, tGk = tT + 1, tD = tGk + K * a.nG, total = tD + a.nD;
-    if (blockIdx.x == 0 && threadIdx.x == 0)   // the previous launch's counter is free now
+    // tile list: R router rows | Gs shared gate/up | Dsh shared down | T route |
+    //            Gk routed gate/up | Dk routed down | C combine
+    const int nR = (a.E + 1 + kRRows - 1) / kRRows;
+    const int tGs = nR, tDsh = tGs + a.nG, tT = tDsh + a.nD, tGk = tT + 1, tDk = tGk + K * a.nG;
+    const int tC = tDk + K * a.nD, total = tC + a.nC;
+    if (blockIdx.x == 0 && threadIdx.x == 0)   // the previous launch's ticket counter is free now
         __hip_atomic_store(&a.tickets[(a.epoch + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (blockIdx.x == 0 && threadIdx.x < 2 * kMaxSlots)   // and so are its per-slot counters
+        __hip_atomic_store(counter(a, a.epoch + 1, threadIdx.x / kMaxSlots, threadIdx.x % kMaxSlots), 0u,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (threadIdx.x == 0) s_xvalid = 0;
     __syncthreads();
     int t = blockIdx.x;
     while (t < total) {
-        const bool gtile = t >= tGs && t < tD && t != tT;
+        const bool gtile = (t >= tGs && t < tDsh) || (t >= tGk && t < tDk);
         if (gtile && !s_xvalid) {   // x digits for the G tiles of this block
             XRegs xr;
             prep_load(a.x, g.D, g.nlG * kLaneChunks * 32, xr);
@@ -487,10 +620,12 @@ __global__ __launch_bounds__(kThreads) void moe_block_kernel(MoeArgs a) {
             if (threadIdx.x == 0) s_xvalid = 1;
         }
         if (t < tGs) tile_router(a, t * kRRows);
-        else if (t < tT) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
+        else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
+        else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
         else if (t == tT) tile_route(a, S.r);
-        else if (t < tD) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
-        else tile_down<TPRD>(a, S.h, (t - tD) * a.dRows, s_rec, s_w);
+        else if (t < tDk) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
+        else if (t < tC) tile_dslot<TPRD>(a, S.h, (t - tDk) / a.nD, ((t - tDk) % a.nD) * kDRows, s_rec);
+        else tile_combine(a, (t - tC) * kCRows, s_w);
         if ((int)gridDim.x >= total) break;
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -518,7 +653,7 @@ static EgTable g_eg;
 struct MoeScratch {
     void *tag = nullptr;
     size_t tag_cap = 0;
-    void *misc = nullptr;         // tickets [2] at 0, err at 64
+    void *misc = nullptr;         // tickets [2] at 0, err at 64, per-slot counters from 256
     size_t misc_cap = 0;
     uint32_t epoch = 0;
 };
@@ -574,15 +709,15 @@ struct LaunchMoe {
         auto kern = moe_block_kernel<LPRG, TPRD>;
         a.gRows = kGSteps * kWaves * (64 / LPRG);
         a.nG = (a.g.I + a.gRows - 1) / a.gRows;
-        a.dRows = kWaves * (64 / TPRD);
-        a.nD = (a.g.D + a.dRows - 1) / a.dRows;
+        a.nD = (a.g.D + kDRows - 1) / kDRows;
+        a.nC = (a.g.D + kCRows - 1) / kCRows;
         static int per = 0;
         if (!per) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, kThreads, 0) != hipSuccess || per < 1)
                 per = 1;
         }
-        const int nR = (a.E + kRRows - 1) / kRRows;
-        const long tiles = nR + a.nG + 1 + (long)a.K * a.nG + a.nD;
+        const int nR = (a.E + 1 + kRRows - 1) / kRRows;
+        const long tiles = nR + (long)(a.K + 1) * (a.nG + a.nD) + 1 + a.nC;
         long nb = (long)n_cu() * per;
         if (nb > tiles) nb = tiles;
         hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
@@ -615,8 +750,9 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     for (int e = 0; e <= T.E; e++)
         if (!T.valid[(size_t)layer * (T.E + 1) + e]) return reject("expert table slot not set");
     const MoeGeom &m = T.geom;
-    const size_t ntag = (size_t)T.E + 2 * K + 1 + (size_t)(K + 1) * m.I;
-    if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, 256)) return false;
+    const size_t ntag = (size_t)T.E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
+    const size_t misc = 256 + (size_t)4 * kMaxSlots * kCounterStride * 4;
+    if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, misc)) return false;
     if (++g_ms.epoch == 0) g_ms.epoch = 1;   // 0 is what fresh scratch holds
     MoeArgs a;
     memset(&a, 0, sizeof(a));
@@ -636,6 +772,7 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.tagv = (unsigned long long *)g_ms.tag;
     a.tickets = (unsigned *)g_ms.misc;
     a.err = (int *)((uint8_t *)g_ms.misc + 64);
+    a.done = (unsigned *)((uint8_t *)g_ms.misc + 256);
     a.epoch = g_ms.epoch;
     a.g = m;
     return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
@@ -664,7 +801,7 @@ struct EgItems {
     float *h;                 // [n, I]
     float *y;                 // [n, D]
     int n;
-    int gRows, nG, dRows, nD;
+    int gRows, nG, nD;
     MoeGeom g;
 };
 
@@ -687,14 +824,11 @@ __global__ __launch_bounds__(kThreads) void eg_gateup_kernel(EgItems it) {
 template <int TPR>
 __global__ __launch_bounds__(kThreads) void eg_down_kernel(EgItems it) {
     __shared__ HPrep H;
-    __shared__ ExpertRec s_rec[1];
-    const int item = blockIdx.x / it.nD, r0 = (blockIdx.x % it.nD) * it.dRows;
-    if (threadIdx.x == 0) s_rec[0] = it.rec[item];
-    __syncthreads();
-    const float one = 1.f;
+    const int item = blockIdx.x / it.nD, r0 = (blockIdx.x % it.nD) * kDRows;
     const float *hsrc = it.h + (size_t)item * it.g.I;
+    float *y = it.y + (size_t)item * it.g.D;
     const int nw = it.g.I / 8;
-    down_rows<TPR>(it.g, 1, s_rec, &one, H, r0, it.dRows, it.y + (size_t)item * it.g.D, 0,
+    down_slot<TPR>(it.g, it.rec[item], H, r0,
                    [&](float (&hv)[kHWords][8]) {
 #pragma unroll
                        for (int k = 0; k < kHWords; k++) {
@@ -702,7 +836,8 @@ __global__ __launch_bounds__(kThreads) void eg_down_kernel(EgItems it) {
 #pragma unroll
                            for (int c = 0; c < 8; c++) hv[k][c] = q < nw ? hsrc[q * 8 + c] : 0.f;
                        }
-                   });
+                   },
+                   [&](int r, float v) { y[r] = v; });
 }
 
 template <int LPRG, int TPRD>
@@ -710,8 +845,7 @@ struct LaunchEg {
     static bool run(EgItems &it, hipStream_t st) {
         it.gRows = kGSteps * kWaves * (64 / LPRG);
         it.nG = (it.g.I + it.gRows - 1) / it.gRows;
-        it.dRows = kWaves * (64 / TPRD);
-        it.nD = (it.g.D + it.dRows - 1) / it.dRows;
+        it.nD = (it.g.D + kDRows - 1) / kDRows;
         hipLaunchKernelGGL(eg_gateup_kernel<LPRG>, dim3(it.n * it.nG), dim3(kThreads), 0, st, it);
         hipLaunchKernelGGL(eg_down_kernel<TPRD>, dim3(it.n * it.nD), dim3(kThreads), 0, st, it);
         const hipError_t e = hipGetLastError();
