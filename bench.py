@@ -110,7 +110,8 @@ def moe_cfg2(lib, torch, dev, steps, warmup):
     per_expert = 2 * (I * D // 2 + I * (D // gs) * 8) + (D * I // 2 + D * (I // gs) * 8)
     nbytes = (K + 1) * per_expert + E * D * 4 + D * 4 + D * 4 + D * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": "cfg2: MoE block decode, router f32 256x2048 + top-8 of 256 experts + shared, "
+    layer = (router, keep, torch)
+    return layer, {"workload": "cfg2: MoE block decode, router f32 256x2048 + top-8 of 256 experts + shared, "
                         "gate/up 512x2048 down 2048x512 fmt6 gs128, one launch",
             "us_per_op": round(ms * 1e3, 2), "wall_us_per_step": round(wall_ms * 1e3, 2),
             "alg_bytes_per_launch": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
@@ -155,6 +156,37 @@ def cpu_baseline(budget_s=12.0):
     return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
             "sample": f"matmul_q4g_asym on {rows} of the 248320 lm_head rows (K=2048, gs=128), "
                       f"median of {len(times)} runs; full-op time {med * O_VOCAB / rows * 1e3:.1f} ms"}
+
+
+def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
+    """M=512 tokens x ~ N(0,1) through the configs[2] layer: routing, rows
+    grouped per expert (ragged), grouped GEMMs on MFMA, combine in ascending expert id."""
+    router, keep, _ = layer
+    D, I, E, K, gs, S = 2048, 512, 256, 8, 128, 512
+    xs = torch.empty(S * D, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(xs.data_ptr(), S * D, 0xC4, 1.0)
+    out = torch.empty(S * D, dtype=torch.float32, device=dev)
+    idx = torch.empty(S * K, dtype=torch.int32, device=dev)
+    lib.sync()
+
+    def step(i):
+        lib.moe_prefill_dev(0, router, K, xs.data_ptr(), S, out.data_ptr(), idx.data_ptr())
+
+    ext = torch.cuda.ExternalStream(lib.stream())
+    ms, wall_ms = time_launches(lib, ext, step, steps, warmup)
+    counts = torch.bincount(idx.long(), minlength=E).cpu()
+    touched = int((counts > 0).sum())
+    per_expert = 2 * (I * D // 2 + I * (D // gs) * 8) + (D * I // 2 + D * (I // gs) * 8)
+    nbytes = (touched + 1) * per_expert + E * D * 4 + 2 * S * D * 4
+    flops = 2.0 * (S * K + S) * (2 * I * D + D * I)   # gate + up + down over routed and shared rows
+    return {"workload": "cfg4: MoE block prefill, 512 tokens, ragged groups (256 experts, top-8 + shared), "
+                        "grouped int4 x int8-digit GEMMs on MFMA",
+            "us_per_block": round(ms * 1e3, 1), "tokens_per_s": round(S / (ms * 1e-3), 1),
+            "experts_touched": touched, "rows_per_expert_max": int(counts.max()),
+            "alg_bytes": nbytes, "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "useful_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+            "frac_bf16_dense_peak": round(flops / (ms * 1e-3) / 2.5e15, 4)}
 
 
 def main():
@@ -230,7 +262,8 @@ def main():
                      "alg_bytes_per_launch": bytes_per},
     }
     if not args.no_moe:
-        out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
+        layer, out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
+        out["moe_prefill_cfg4"] = moe_prefill_cfg4(lib, torch, dev, layer, max(args.steps // 10, 5), 2)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

@@ -229,6 +229,13 @@ int   coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const fl
 /* Error flag of the MoE launches since the last call (synchronizes the device): 0 none,
  * 1 a bounded wait gave up, 2 an out-of-range expert id, -1 runtime error. */
 int   coli_hip_moe_error(void);
+/* The layer's MoE block over S token rows d_xs[S, D] (prefill / ragged batch,
+ * c/qwen.c:1050-1183): per-token routing, rows grouped by expert, expert projections as
+ * grouped GEMMs on MFMA (int8 digits of the activations x int4 weights, exact integer
+ * group sums), out[t] = sum in ascending expert id of w * y + shgt * y_shared.  K <= 8.
+ * d_idx / d_val [S, K] (routing, rank order) may be NULL. */
+int   coli_hip_moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs, int S,
+                           float *d_out, int *d_idx, float *d_val, void *stream);
 
 #ifdef __cplusplus
 }

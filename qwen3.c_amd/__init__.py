@@ -53,6 +53,7 @@ _SIGS = {
     "coli_vk_eg_table_set_shared": (_I, [_I, _P, _P, _P, _P, _I]),
     "coli_hip_moe_decode": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "coli_hip_moe_error": (_I, []),
+    "coli_hip_moe_prefill": (_I, [_I, _P, _I, _P, _I, _P, _P, _P, _P]),
 }
 
 
@@ -242,6 +243,10 @@ class Lib:
         if not self.L.coli_hip_moe_decode(layer, router.handle, K, d_x, d_out, int(accumulate), d_idx, d_val,
                                           stream):
             raise RuntimeError("coli_hip_moe_decode failed")
+
+    def moe_prefill_dev(self, layer, router, K, d_xs, S, d_out, d_idx=None, d_val=None, stream=None):
+        if not self.L.coli_hip_moe_prefill(layer, router.handle, K, d_xs, S, d_out, d_idx, d_val, stream):
+            raise RuntimeError("coli_hip_moe_prefill failed")
 
     def moe_error(self):
         return int(self.L.coli_hip_moe_error())

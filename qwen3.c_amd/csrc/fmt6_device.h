@@ -265,17 +265,20 @@ struct XPrep {
 // ncols: columns to prepare (a multiple of 32 covering every lane's chunks, <= kLaneMaxI);
 // columns at or past I are zero.  Each thread owns whole 8-column words: it loads its
 // x values once (all loads in flight together), publishes one max per word, then turns
-// them into digit planes.  Ends with __syncthreads().
-constexpr int kPrepWords = kLaneMaxI / 8 / kThreads;   // words per thread
-struct XRegs {
-    float v[kPrepWords][8];
+// them into digit planes.  NT = threads of the block.  Ends with __syncthreads().
+template <int NT>
+struct XRegsT {
+    static constexpr int kWords = (kLaneMaxI / 8 + NT - 1) / NT;   // words per thread
+    float v[kWords][8];
 };
+using XRegs = XRegsT<kThreads>;
 // Issue the x loads (split from prep_x so that they can go out before other loads).
-__device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, int ncols, XRegs &xr) {
+template <int NT = kThreads>
+__device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, int ncols, XRegsT<NT> &xr) {
     const int tid = threadIdx.x, nwords = ncols / 8;
 #pragma unroll
-    for (int k = 0; k < kPrepWords; k++) {
-        const int w = tid + k * kThreads;
+    for (int k = 0; k < XRegsT<NT>::kWords; k++) {
+        const int w = tid + k * NT;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const int i = w * 8 + c;
@@ -284,16 +287,17 @@ __device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, in
     }
 }
 
-__device__ inline void prep_x(const XRegs &xr, int gs, int ncols, XPrep &P) {
+template <int NT = kThreads>
+__device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P) {
     const int tid = threadIdx.x;
     const int nwords = ncols / 8, nch = ncols / 32, ngrp = (ncols + gs - 1) / gs;
     const auto &xv = xr.v;
-    for (int g = tid; g < ngrp; g += kThreads) P.gmax[g] = 0u;
-    for (int c = tid; c < nch; c += kThreads) P.qsum[c] = 0;
+    for (int g = tid; g < ngrp; g += NT) P.gmax[g] = 0u;
+    for (int c = tid; c < nch; c += NT) P.qsum[c] = 0;
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kPrepWords; k++) {
-        const int w = tid + k * kThreads;
+    for (int k = 0; k < XRegsT<NT>::kWords; k++) {
+        const int w = tid + k * NT;
         float m = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(xv[k][c]));
@@ -301,8 +305,8 @@ __device__ inline void prep_x(const XRegs &xr, int gs, int ncols, XPrep &P) {
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kPrepWords; k++) {
-        const int w = tid + k * kThreads;
+    for (int k = 0; k < XRegsT<NT>::kWords; k++) {
+        const int w = tid + k * NT;
         if (w >= nwords) continue;
         const float m = __uint_as_float(P.gmax[(w * 8) / gs]);
         const int e = m > 0.f ? ilogbf(m) + 1 : 0;    // m < 2^e

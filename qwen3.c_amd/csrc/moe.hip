@@ -23,7 +23,7 @@
 // tag equals the launch epoch.  No counters need ordering, so no device-scope fences (an
 // L2 write-back each on gfx950) are issued.  Polls are bounded: past the limit they set an
 // error flag and give up, so every wave always exits.
-#include "fmt6_device.h"
+#include "moe_common.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -31,23 +31,6 @@
 
 namespace coli {
 
-struct ExpertRec {
-    const uint8_t *wg, *wu, *wd;
-    const float *sg, *su, *sd;
-};
-
-// geometry shared by every expert of a table (fmt 6, lanes layout)
-struct MoeGeom {
-    int D, I, gs;
-    int ngD, ngI;   // groups per gate/up row (over D) and per down row (over I)
-    int nlG, nlD;   // lanes with data per gate/up row and per down row
-    int rbG, rbD;   // device row bytes of gate/up and of down
-};
-
-constexpr int kMaxK = 64;                 // c/backend_vulkan.c:3298 (topk <= 64)
-constexpr int kMaxE = 1024;
-constexpr int kMaxSlots = kTopK + 1;      // fused kernel: K <= 8 routed + the shared expert
-constexpr int kMoeMaxI = 512;             // expert intermediate size (h staged in LDS)
 constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
 constexpr int kGSteps = 2;                // gate/up row steps per tile
 constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
@@ -118,12 +101,6 @@ __device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t e
         if ((uint32_t)(v >> 32) == epoch) return __uint_as_float((uint32_t)v);
         if (poll_give_up(err, polls)) return 0.f;
     }
-}
-
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
 }
 
 // ---------------------------------------------------------------- h -> digit planes
@@ -329,127 +306,16 @@ __device__ void tile_router(const MoeArgs &a, int r0) {
 
 // ---------------------------------------------------------------- T: route
 // c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate.
-struct RouteLds {
-    float p[kMaxE + 64];               // probabilities, zero padded to a multiple of 64
-    unsigned long long cand[kMaxE];    // candidate keys (p bits << 24 | 0xFFFFFF - e)
-    unsigned hmax[2 * kWaves];         // half-wave maxima of the p bits
-    float red[kWaves];
-    float sum, gate, vsum;
-    int ncand;
-    int idx[kTopK];
-    float val[kTopK];
-};
-
-// u32 maximum over each half wave (32 lanes): valid in lanes 31 and 63
-__device__ __forceinline__ uint32_t half_wave_umax(uint32_t v) {
-    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
-    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
-    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
-    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror: every lane holds its row's max
-    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15: rows 1 and 3 take rows 0 and 2
-    return v;
-}
-
 __device__ void tile_route(const MoeArgs &a, RouteLds &R) {
-    constexpr int kPer = kMaxE / kThreads;   // experts per thread
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = a.E, K = a.K;
-    const int Epad = (E + 63) & ~63;
-    float m = -1e30f;   // the reference's initial max
+    const int tid = threadIdx.x, E = a.E, K = a.K;
     for (int e = tid; e <= E; e += kThreads) {   // logit E is the shared-expert gate dot
         const float l = tag_get(&a.tagv[e], a.epoch, a.err);
-        if (e < E) {
-            R.p[e] = l;
-            m = fmaxf(m, l);
-        } else {
-            R.gate = l;
-        }
+        if (e < E) R.p[e] = l;
+        else R.gate = l;
     }
-    if (tid == 0) R.ncand = 0;
-    m = wave_max_f(m);
-    if (lane == 0) R.red[wave] = m;
-    __syncthreads();
-    m = R.red[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; w++) m = fmaxf(m, R.red[w]);
-    for (int e = tid; e < Epad; e += kThreads) R.p[e] = e < E ? expf(R.p[e] - m) : 0.f;
-    __syncthreads();
-    if (tid == 0) {   // sequential sum in index order, as the reference (the padding adds 0)
-        float s = 0.f;
-        for (int e0 = 0; e0 < Epad; e0 += 64) {
-            float4 v[16];
-#pragma unroll
-            for (int c = 0; c < 16; c++) v[c] = *(const float4 *)&R.p[e0 + 4 * c];
-#pragma unroll
-            for (int c = 0; c < 16; c++) {
-                s += v[c].x;
-                s += v[c].y;
-                s += v[c].z;
-                s += v[c].w;
-            }
-        }
-        R.sum = s;
-    }
-    __syncthreads();
-    const float s = R.sum;
-    uint32_t pb[kPer], mx = 0u;
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
-        pb[q] = 0u;
-        if (e < E) {
-            const float pv = R.p[e] / s;
-            R.p[e] = pv;
-            pb[q] = __float_as_uint(pv);   // p >= 0: the bits order like the values
-            mx = max(mx, pb[q]);
-        }
-    }
-    // Candidates: p >= theta = the least of the 8 half-wave maxima.  Those maxima are 8
-    // distinct experts with p >= theta, so the K <= 8 best (p desc, index asc) and every
-    // expert tied with the K-th are candidates.
-    mx = half_wave_umax(mx);
-    if (lane == 31 || lane == 63) R.hmax[2 * wave + (lane >> 5)] = mx;
-    __syncthreads();
-    uint32_t theta = R.hmax[0];
-#pragma unroll
-    for (int i = 1; i < 2 * kWaves; i++) theta = min(theta, R.hmax[i]);
-#pragma unroll
-    for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
-        if (e < E && pb[q] >= theta)
-            R.cand[atomicAdd(&R.ncand, 1)] = ((unsigned long long)pb[q] << 24) | (0xFFFFFFu - (uint32_t)e);
-    }
-    __syncthreads();
-    // rank among the candidates: (p desc, index asc) is the order of the reference's strict
-    // '>' scan from the lowest index (c/qwen.c:810-815)
-    const int nc = R.ncand;
-    for (int c = tid; c < nc; c += kThreads) {
-        const unsigned long long me = R.cand[c];
-        int rank = 0;
-        for (int o0 = 0; o0 < nc; o0 += 8) {   // 8 LDS reads in flight
-            unsigned long long o8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) o8[u] = o0 + u < nc ? R.cand[o0 + u] : 0ull;
-#pragma unroll
-            for (int u = 0; u < 8; u++) rank += o8[u] > me ? 1 : 0;
-        }
-        if (rank < K) {
-            R.idx[rank] = (int)(0xFFFFFFu - (uint32_t)(me & 0xFFFFFFu));
-            R.val[rank] = __uint_as_float((uint32_t)(me >> 24));
-        }
-    }
-    __syncthreads();
-    // renorm (c/qwen.c:816-817): the sum in rank order, then one lane per slot
+    route_select(R, E, K);
     // thread (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
     // renormed weights, 2K the shared gate
-    if (tid == 0) {   // the renorm sum in rank order (trailing +0 leaves it unchanged)
-        float v8[kTopK], sm = 0.f;
-#pragma unroll
-        for (int j = 0; j < kTopK; j++) v8[j] = j < K ? R.val[j] : 0.f;
-#pragma unroll
-        for (int j = 0; j < kTopK; j++) sm += v8[j];
-        R.vsum = sm;
-    }
-    __syncthreads();
     const float sm = R.vsum;
     for (int q = tid; q < kRouteReps * kRouteStride; q += kThreads) {
         const int c = q / kRouteStride, k = q % kRouteStride;
@@ -776,6 +642,18 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.epoch = g_ms.epoch;
     a.g = m;
     return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
+}
+
+bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGeom *geom, int *E) {
+    EgTable &T = g_eg;
+    if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return false;
+    for (int e = 0; e <= T.E; e++)
+        if (!T.valid[(size_t)layer * (T.E + 1) + e]) return false;
+    *d_rec = T.d_rec + (size_t)layer * (T.E + 1);
+    *d_shgate = T.d_shgate + (size_t)layer * T.D;
+    *geom = T.geom;
+    *E = T.E;
+    return true;
 }
 
 // 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id

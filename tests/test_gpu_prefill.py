@@ -1,0 +1,67 @@
+"""Prefill MoE block on the GPU (coli_hip_moe_prefill) vs the CPU oracle's restatement of
+moe_batch_from_logits (c/qwen.c:1050-1183), which is bit-identical to the compiled
+reference on the committed fixture tests/golden/moe_batch_small.npz.
+
+Per token: routed expert ids identical to the oracle's (rank order), renormed weights
+within 1e-5, output within maxrel 1e-3 (floor scaled to the output magnitude, see
+_util.maxrel_scaled).  The expert projections run as grouped GEMMs on MFMA with exact
+integer group sums, so fp32-accumulation tolerance applies.
+"""
+import numpy as np
+import pytest
+
+import _util
+from _moe import Layer, Table
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def run_prefill(lib, torch, dev, L, K, xs, S):
+    dxs = torch.from_numpy(xs).to(dev)
+    dout = torch.full((S * L.D,), np.nan, device=dev)
+    didx = torch.full((S * K,), -1, dtype=torch.int32, device=dev)
+    dval = torch.zeros(S * K, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    lib.moe_prefill_dev(0, L.router, K, dxs.data_ptr(), S, dout.data_ptr(), didx.data_ptr(), dval.data_ptr())
+    lib.sync()
+    return dout.cpu().numpy(), didx.cpu().numpy(), dval.cpu().numpy()
+
+
+def check(orc, L, K, xs, S, got):
+    out, tidx, tval = L.oracle_prefill(orc, xs, S, K)
+    gout, gidx, gval = got
+    assert np.array_equal(gidx, tidx), np.nonzero(gidx != tidx)[0][:10]
+    np.testing.assert_allclose(gval, tval, rtol=1e-5, atol=1e-7)
+    worst = max(_util.maxrel_scaled(gout[t * L.D:(t + 1) * L.D], out[t * L.D:(t + 1) * L.D]) for t in range(S))
+    print(f"  S={S}: worst per-token maxrel_scaled {worst:.2e}", flush=True)
+    assert worst <= TOL, worst
+
+
+@pytest.mark.parametrize("S,K", [(1, 4), (37, 4), (64, 8)])
+def test_prefill_small(lib, orc, gen, torch_dev, S, K):
+    import torch
+    L = Layer(lib, gen, 0x9F1, 256, 128, 32, 128)
+    Table(lib, [L]).activate()
+    xs = gen.normal(S * L.D, 0x9F2 + S)
+    check(orc, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S))
+
+
+@pytest.fixture(scope="module")
+def cfg4(lib, gen):
+    """configs[4]'s layer: router f32 256x2048, 256 + 1 experts (gate/up 512x2048, down
+    2048x512, fmt 6 gs 128)."""
+    return Table(lib, [Layer(lib, gen, 0xC0F4, 2048, 512, 256, 128)])
+
+
+def test_prefill_cfg4(lib, orc_omp, gen, torch_dev, cfg4):
+    """configs[4] shape at S = 128 tokens (the oracle's cost grows with S; the full
+    S = 512 run is the benchmark's)."""
+    import torch
+    L, K, S = cfg4.activate()[0], 8, 128
+    xs = gen.normal(S * L.D, 0xC0F5)
+    got = run_prefill(lib, torch, torch_dev, L, K, xs, S)
+    check(orc_omp, L, K, xs, S, got)
+    counts = np.bincount(got[1], minlength=L.E)
+    assert counts.max() > 8 and (counts == 0).sum() < L.E   # ragged groups
