@@ -280,6 +280,156 @@ void orc_moe_prefill(const float *xs, int S, const float *router, const OrcExper
     free(pr);
 }
 
+/* ---------------- layer blocks ---------------- */
+/* c/qwen.c:296-309: quantized host copy first (fmt 6), else the f32 original. */
+void orc_proj(const OrcMat *m, const float *x, float *y) {
+    if (m->fmt == 6)
+        orc_matmul_q4g_asym(y, x, (const uint8_t *)m->w, m->sz, m->I, m->O, m->gs);
+    else
+        orc_matmul_f32(y, x, (const float *)m->w, 1, m->I, m->O);
+}
+
+/* c/qwen.c:570-579 */
+void orc_rope_partial(float *x, int pos, int rot, float theta) {
+    const int hr = rot / 2;
+    for (int j = 0; j < hr; j++) {
+        const float inv = powf(theta, -2.0f * j / rot);
+        const float ang = (float)pos * inv, cs = cosf(ang), sn = sinf(ang);
+        const float lo = x[j], hi = x[j + hr];
+        x[j] = lo * cs - hi * sn;
+        x[j + hr] = hi * cs + lo * sn;
+    }
+}
+
+/* c/qwen.c:581-667 with S = 1 (CPU branch). */
+void orc_gqa_decode(const OrcGqa *L, float *Kc, float *Vc, int max_t, int pos, const float *x, float *out) {
+    const int H = L->H, KH = L->KH, hd = L->hd, qo = H * hd * 2, ko = KH * hd;
+    float *qg = malloc((size_t)qo * sizeof(float)), *k = malloc((size_t)ko * sizeof(float));
+    float *v = malloc((size_t)ko * sizeof(float)), *ctx = malloc((size_t)H * hd * sizeof(float));
+    float *sc = malloc((size_t)(pos + 1) * sizeof(float));
+    orc_proj(&L->q, x, qg);
+    orc_proj(&L->k, x, k);
+    orc_proj(&L->v, x, v);
+    for (int h = 0; h < H; h++) {            /* :598-604 per-head q norm, then RoPE */
+        float *qh = qg + (int64_t)h * 2 * hd;
+        orc_rmsnorm_zc(qh, qh, L->qn, hd, L->eps);
+        orc_rope_partial(qh, pos, L->rot, L->theta);
+    }
+    for (int h = 0; h < KH; h++) {           /* :605-614 k norm + RoPE, cache rows */
+        float *kh = k + (int64_t)h * hd;
+        orc_rmsnorm_zc(kh, kh, L->kn, hd, L->eps);
+        orc_rope_partial(kh, pos, L->rot, L->theta);
+        memcpy(Kc + ((int64_t)h * max_t + pos) * hd, kh, (size_t)hd * sizeof(float));
+        memcpy(Vc + ((int64_t)h * max_t + pos) * hd, v + (int64_t)h * hd, (size_t)hd * sizeof(float));
+    }
+    const float scale = 1.f / sqrtf((float)hd);
+    const int gq = H / KH;
+    for (int h = 0; h < H; h++) {            /* :638-665 */
+        const int kvh = h / gq;
+        const float *qv = qg + (int64_t)h * 2 * hd;
+        for (int t = 0; t <= pos; t++) {
+            const float *kv = Kc + ((int64_t)kvh * max_t + t) * hd;
+            float acc = 0;
+            for (int d = 0; d < hd; d++) acc += qv[d] * kv[d];
+            sc[t] = acc * scale;
+        }
+        orc_softmax_row(sc, pos + 1);
+        float *cx = ctx + (int64_t)h * hd;
+        for (int d = 0; d < hd; d++) cx[d] = 0;
+        for (int t = 0; t <= pos; t++) {
+            const float *vr = Vc + ((int64_t)kvh * max_t + t) * hd;
+            const float a = sc[t];
+            for (int d = 0; d < hd; d++) cx[d] += a * vr[d];
+        }
+        const float *gate = qv + hd;
+        for (int d = 0; d < hd; d++) cx[d] *= orc_sigmoid(gate[d]);
+    }
+    orc_proj(&L->o, ctx, out);
+    free(qg);
+    free(k);
+    free(v);
+    free(ctx);
+    free(sc);
+}
+
+/* c/qwen.c:175 softplus (torch default beta 1, threshold 20) */
+static float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+/* c/qwen.c:669-776 (CPU branch). */
+void orc_gdn_step(const OrcGdn *L, float *st, float *S, const float *x, float *out) {
+    const int KH = L->KH, KD = L->KD, VH = L->VH, VD = L->VD, K = L->K;
+    const int key_dim = KH * KD, value_dim = VH * VD, CD = 2 * key_dim + value_dim;
+    float *qkv = malloc((size_t)CD * sizeof(float)), *cv = malloc((size_t)CD * sizeof(float));
+    float *z = malloc((size_t)value_dim * sizeof(float)), *y = malloc((size_t)value_dim * sizeof(float));
+    float *qn = malloc((size_t)key_dim * sizeof(float)), *kn = malloc((size_t)key_dim * sizeof(float));
+    float *a = malloc((size_t)VH * sizeof(float)), *b = malloc((size_t)VH * sizeof(float));
+    float *dec = malloc((size_t)VH * sizeof(float)), *bet = malloc((size_t)VH * sizeof(float));
+    float *kvm = malloc((size_t)VD * sizeof(float)), *del = malloc((size_t)VD * sizeof(float));
+    orc_proj(&L->qkv, x, qkv);
+    orc_proj(&L->z, x, z);
+    /* :697-707 ring shift, append, conv + SiLU */
+    memmove(st, st + CD, (size_t)(K - 1) * CD * sizeof(float));
+    memcpy(st + (size_t)(K - 1) * CD, qkv, (size_t)CD * sizeof(float));
+    for (int ch = 0; ch < CD; ch++) {
+        const float *w = L->conv + (int64_t)ch * K;
+        float acc = 0;
+        for (int j = 0; j < K; j++) acc += w[j] * st[(size_t)j * CD + ch];
+        cv[ch] = orc_silu(acc);
+    }
+    orc_proj(&L->b, x, b);                  /* :710-711 */
+    orc_proj(&L->a, x, a);
+    for (int h = 0; h < KH; h++) {           /* :713-721 */
+        const float *qs = cv + h * KD, *ks = cv + key_dim + h * KD;
+        float sq = 0, sk = 0;
+        for (int d = 0; d < KD; d++) {
+            sq += qs[d] * qs[d];
+            sk += ks[d] * ks[d];
+        }
+        const float rq = 1.f / sqrtf(sq + L->eps) / sqrtf((float)KD), rk = 1.f / sqrtf(sk + L->eps);
+        for (int d = 0; d < KD; d++) {
+            qn[h * KD + d] = qs[d] * rq;
+            kn[h * KD + d] = ks[d] * rk;
+        }
+    }
+    for (int h = 0; h < VH; h++) {           /* :722-728 */
+        bet[h] = orc_sigmoid(b[h]);
+        dec[h] = expf(-expf(L->alog[h]) * softplus(a[h] + L->dtb[h]));
+    }
+    for (int h = 0; h < VH; h++) {           /* :749-773 delta rule + gated RMSNorm */
+        const int src = h / (VH / KH);
+        const float *qh = qn + src * KD, *kh = kn + src * KD, *vh = cv + 2 * key_dim + h * VD;
+        float *Sh = S + (size_t)h * KD * VD;
+        for (int d = 0; d < VD; d++) kvm[d] = 0;
+        for (int i = 0; i < KD; i++) {
+            float *row = Sh + (size_t)i * VD;
+            const float kk = kh[i];
+            for (int d = 0; d < VD; d++) {
+                row[d] *= dec[h];
+                kvm[d] += row[d] * kk;
+            }
+        }
+        for (int d = 0; d < VD; d++) del[d] = (vh[d] - kvm[d]) * bet[h];
+        float *yh = y + (size_t)h * VD;
+        for (int d = 0; d < VD; d++) yh[d] = 0;
+        for (int i = 0; i < KD; i++) {
+            float *row = Sh + (size_t)i * VD;
+            const float kk = kh[i], qq = qh[i];
+            for (int d = 0; d < VD; d++) {
+                row[d] += kk * del[d];
+                yh[d] += row[d] * qq;
+            }
+        }
+        const float *zh = z + (size_t)h * VD;
+        double ms = 0;
+        for (int d = 0; d < VD; d++) ms += (double)yh[d] * yh[d];
+        const float r = 1.f / sqrtf((float)(ms / VD) + L->eps);
+        for (int d = 0; d < VD; d++) yh[d] = yh[d] * r * L->gnorm[d] * orc_silu(zh[d]);
+    }
+    orc_proj(&L->out, y, out);
+    free(qkv); free(cv); free(z); free(y); free(qn); free(kn);
+    free(a); free(b); free(dec); free(bet); free(kvm); free(del);
+}
+
 /* c/qwen.c:1471-1472 */
 int orc_argmax(const float *v, int n) {
     int best = 0;

@@ -23,6 +23,10 @@
  *   orc_moe_prefill        golden vectors from the compiled reference (moe_batch);
  *                          per-token brute force
  *   orc_argmax/_topk_logits  full sort on random and forced-tie inputs
+ *   orc_gqa_decode         golden vectors from the compiled reference (attention);
+ *                          closed forms (pos 0 attends to itself; rope identities)
+ *   orc_gdn_step           golden vectors from the compiled reference (gdn_step);
+ *                          f64 brute force of the recurrence
  *   orc_gen_*              hash / stream known-answer values; distribution moments
  */
 #ifndef QWEN_HIP_ORACLE_H
@@ -88,6 +92,45 @@ void orc_moe_prefill(const float *xs, int S, const float *router, const OrcExper
                      const OrcExpert *shared, const float *sh_gate,
                      int D, int I, int E, int K, int gs,
                      float *out, int *tidx, float *tval);
+
+/* ---- attention / GatedDeltaNet layer blocks (decode, one token) ----
+ * A dense projection as c/qwen.c:296-309 mm_dense evaluates it on the CPU: fmt 6 = the
+ * quantized host copy through matmul_q4g_asym, fmt 0 = f32 rows [O, I] through matmul. */
+typedef struct {
+    int fmt;
+    const void *w;
+    const float *sz;
+    int I, O, gs;
+} OrcMat;
+void orc_proj(const OrcMat *m, const float *x, float *y);
+
+/* c/qwen.c:570-579 rope_partial: half-half rotation of the first rot dims. */
+void orc_rope_partial(float *x, int pos, int rot, float theta);
+
+/* Gated GQA layer (c/qwen.c:581-667, S = 1): q_proj emits [q | gate] per head; per-head
+ * zero-centred q/k norm, partial RoPE at pos, K/V rows written to the caches
+ * ([KH][max_t][hd]), softmax attention over positions 0..pos, output gate
+ * sigmoid(gate), o_proj. */
+typedef struct {
+    OrcMat q, k, v, o;
+    const float *qn, *kn;
+    int H, KH, hd, rot;
+    float theta, eps;
+} OrcGqa;
+void orc_gqa_decode(const OrcGqa *L, float *Kc, float *Vc, int max_t, int pos, const float *x, float *out);
+
+/* GatedDeltaNet layer, one token (c/qwen.c:669-776, CPU branch): qkv/z projections,
+ * causal conv1d over the ring convst [K][CD] (slot K-1 newest) + SiLU, per-k-head l2norm
+ * (q also / sqrt(KD)), decay = exp(-exp(alog) softplus(a + dtb)), beta = sigmoid(b),
+ * delta rule on S [VH][KD][VD], gated RMSNorm (gnorm, SiLU(z)), out projection. */
+typedef struct {
+    OrcMat qkv, z, a, b, out;
+    const float *conv;
+    const float *alog, *dtb, *gnorm;
+    int KH, KD, VH, VD, K;
+    float eps;
+} OrcGdn;
+void orc_gdn_step(const OrcGdn *L, float *convst, float *S, const float *x, float *out);
 
 /* c/qwen.c:1471-1472: ascending scan, strict '>' (ties -> lowest index). */
 int orc_argmax(const float *v, int n);

@@ -114,3 +114,56 @@ void ref_moe_batch(const float *xs, int S, const float *router, const RefExpert 
     if (usage) memcpy(usage, r.m.eusage, (size_t)E * sizeof(uint32_t));
     ref_moe_free(&r);
 }
+
+/* ---- layer blocks: c/qwen.c:581-667 attention and :669-776 gdn_step, CPU branch ----
+ * Projections arrive as fmt 6 quantized host copies (VkDense.q, the mm_dense fallback
+ * c/qwen.c:300-305); GDN a/b are f32 [VH, D] as the CPU branch reads them. */
+typedef struct {
+    const uint8_t *q;
+    const float *s;
+} RefQ6;
+
+static void set_dense(VkDense *d, const RefQ6 *w, int gs) {
+    memset(d, 0, sizeof(*d));
+    d->q = (uint8_t *)w->q;
+    d->s = (float *)w->s;
+    d->fmt = 6;
+    d->gs = gs;
+}
+
+/* One token at position pos through attention(); Kc/Vc [KH][max_t][hd] are updated. */
+void ref_attention(const RefQ6 *q, const RefQ6 *k, const RefQ6 *v, const RefQ6 *o, const float *qn,
+                   const float *kn, int D, int H, int KH, int hd, int rot, float theta, float eps, int gs,
+                   float *Kc, float *Vc, int max_t, int pos, const float *x, float *out) {
+    Model m;
+    Layer l;
+    memset(&m, 0, sizeof(m));
+    memset(&l, 0, sizeof(l));
+    Cfg *c = &m.c;
+    c->hidden = D; c->n_heads = H; c->n_kv_heads = KH; c->head_dim = hd; c->rot = rot;
+    c->theta = theta; c->eps = eps;
+    m.K = &Kc; m.V = &Vc; m.max_t = max_t;
+    set_dense(&l.gq, q, gs); set_dense(&l.gk, k, gs); set_dense(&l.gv, v, gs); set_dense(&l.go, o, gs);
+    l.qn = (float *)qn; l.kn = (float *)kn;
+    attention(&m, &l, 0, x, 1, pos, out);
+}
+
+/* One token through gdn_step(); convst [K][CD] and S [VH][KD][VD] are updated. */
+void ref_gdn_step(const RefQ6 *qkv, const RefQ6 *z, const RefQ6 *outp, const float *a, const float *b,
+                  const float *conv, const float *alog, const float *dtb, const float *gnorm, int D, int KH,
+                  int KD, int VH, int VD, int K, float eps, int gs, float *convst, float *S, const float *x,
+                  float *out) {
+    Model m;
+    Layer l;
+    memset(&m, 0, sizeof(m));
+    memset(&l, 0, sizeof(l));
+    Cfg *c = &m.c;
+    c->hidden = D; c->eps = eps;
+    c->gdn_kh = KH; c->gdn_kd = KD; c->gdn_vh = VH; c->gdn_vd = VD; c->conv_k = K;
+    c->key_dim = KH * KD; c->value_dim = VH * VD; c->conv_dim = 2 * c->key_dim + c->value_dim;
+    m.gdnS = &S; m.convst = &convst;
+    set_dense(&l.gqkv, qkv, gs); set_dense(&l.gz, z, gs); set_dense(&l.gout, outp, gs);
+    l.a = (float *)a; l.b = (float *)b; l.conv = (float *)conv;
+    l.alog = (float *)alog; l.dtb = (float *)dtb; l.gnorm = (float *)gnorm;
+    gdn_step(&m, &l, 0, x, out);
+}

@@ -17,6 +17,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
+import _layers  # noqa: E402
 import _util  # noqa: E402
 from _util import P, eptr  # noqa: E402
 
@@ -117,15 +118,51 @@ def moe_cases(ref, gen):
     return out
 
 
+# GQA / GDN layer blocks: (shape..., base, tokens); the reference runs the tokens in order
+# from a zeroed KV cache / recurrent state, so the later outputs depend on the earlier.
+GQA_SPECS = {
+    "small": dict(D=256, H=4, KH=2, hd=64, rot=16, gs=32, max_t=8, base=0x6A, T=6),
+    "cfg3": dict(D=2048, H=16, KH=2, hd=256, rot=64, gs=128, max_t=4096, base=0x6C, T=3),
+}
+GDN_SPECS = {
+    "small": dict(D=256, KH=2, KD=32, VH=4, VD=32, K=4, gs=32, base=0x6B, T=4),
+    "cfg3": dict(D=2048, KH=16, KD=128, VH=32, VD=128, K=4, gs=128, base=0x6D, T=2),
+}
+
+
+def layer_cases(ref, gen):
+    out = {}
+    for name, sp in GQA_SPECS.items():
+        W = _layers.GqaWeights(gen, sp["base"], sp["D"], sp["H"], sp["KH"], sp["hd"], sp["rot"], sp["gs"])
+        cache = W.new_cache(sp["max_t"])
+        xs = gen.normal(sp["T"] * sp["D"], gen.stream(sp["base"], 50))
+        ys = [W.reference(ref, cache, sp["max_t"], t, xs[t * sp["D"]:(t + 1) * sp["D"]].copy()) for t in range(sp["T"])]
+        extra = dict(K=cache[0], V=cache[1]) if name == "small" else {}
+        out[f"layer_gqa_{name}"] = dict(**sp, digest=digest(W.q.q, W.o.sz, W.qn, W.kn, xs), out=np.stack(ys),
+                                        **extra)
+    for name, sp in GDN_SPECS.items():
+        W = _layers.GdnWeights(gen, sp["base"], sp["D"], sp["KH"], sp["KD"], sp["VH"], sp["VD"], sp["K"], sp["gs"])
+        st = W.new_state()
+        xs = gen.normal(sp["T"] * sp["D"], gen.stream(sp["base"], 50))
+        ys = [W.reference(ref, st, xs[t * sp["D"]:(t + 1) * sp["D"]].copy()) for t in range(sp["T"])]
+        extra = dict(conv=st[0], S=st[1]) if name == "small" else dict(state_digest=digest(st[0], st[1]))
+        out[f"layer_gdn_{name}"] = dict(**sp, digest=digest(W.qkv.q, W.out.sz, W.a.w, W.conv, xs), out=np.stack(ys),
+                                        **extra)
+    return out
+
+
 def main():
     ref = _util.load_ref()
     if ref is None:
         sys.exit("oracle/_ref/libqwenref.so missing: build it with `make -C oracle ref`")
-    gen = _util.Gen(_util.load_oracle())
+    orc = _util.load_oracle()
+    _layers.bind(orc, ref)
+    gen = _util.Gen(orc)
     cases = {}
     cases.update(gemv_cases(ref, gen))
     cases.update(dense_cases(ref, gen))
     cases.update(moe_cases(ref, gen))
+    cases.update(layer_cases(ref, gen))
     for name, d in cases.items():
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **{k: np.asarray(v) for k, v in d.items()})
