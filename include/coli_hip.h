@@ -236,6 +236,14 @@ int   coli_hip_moe_error(void);
  * d_idx / d_val [S, K] (routing, rank order) may be NULL. */
 int   coli_hip_moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs, int S,
                            float *d_out, int *d_idx, float *d_val, void *stream);
+/* Bulk form of coli_vk_kv_row: mirror rows [row0, row0 + n) of an attention layer from
+ * host arrays K [n][kd] and V [n][vd] (seeds a cache of a given length).  _read copies
+ * them back. */
+int   coli_hip_kv_load(int layer, int row0, int n, const float *K, const float *V);
+int   coli_hip_kv_read(int layer, int row0, int n, float *K, float *V);
+/* A GDN layer's state in the reference's host layouts: conv ring [conv_k][conv_dim]
+ * (slot conv_k - 1 newest) and recurrent state [VH][KD][VD] (c/qwen.c:749-767). */
+int   coli_hip_gdn_state_read(int layer, float *ring, float *S);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,44 @@ _SIGS = {
     "coli_hip_moe_decode": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "coli_hip_moe_error": (_I, []),
     "coli_hip_moe_prefill": (_I, [_I, _P, _I, _P, _I, _P, _P, _P, _P]),
+    # attention / GatedDeltaNet layer blocks and the residual stream (c/backend_vulkan.h:110-279)
+    "coli_vk_kv_ensure": (_I, [_I, _I, _I, _I]),
+    "coli_vk_kv_row": (_I, [_I, _I, _P, _P]),
+    "coli_vk_kv_reset": (None, []),
+    "coli_hip_kv_load": (_I, [_I, _I, _I, _P, _P]),
+    "coli_hip_kv_read": (_I, [_I, _I, _I, _P, _P]),
+    "coli_vk_gqa_norm_weight": (_I, [_I, _P, _P, _I]),
+    "coli_vk_gqa_full": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _I]),
+    "coli_vk_gdn_state_ensure": (_I, [_I, _I, _I, _I]),
+    "coli_vk_gdn_reset": (None, []),
+    "coli_vk_gdn_conv_ensure": (_I, [_I, _I, _I]),
+    "coli_vk_gdn_conv_weight": (_I, [_I, _P, _I, _I]),
+    "coli_vk_gdn_ba_weight": (_I, [_I, _P, _P, _P, _I, _I]),
+    "coli_hip_gdn_state_read": (_I, [_I, _P, _P]),
+    "coli_vk_gdn_full": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "coli_vk_gdn_full_seq": (_I, [_I, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
+    "coli_vk_layer_norm_weight": (_I, [_I, _P, _P, _I]),
+    "coli_vk_gqa_full_route": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                    _F, _F, _I, _I]),
+    "coli_vk_gdn_full_route": (_I, [_I, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                    _F, _I, _I]),
+    "coli_vk_stream_available": (_I, []),
+    "coli_vk_stream_begin": (_I, [_P, _I]),
+    "coli_vk_stream_end": (_I, [_P, _I]),
+    "coli_vk_stream_add": (_I, [_P, _I]),
+    "coli_vk_stream_nrm": (_P, []),
+    "coli_vk_stream_copy_resid": (_I, [_P, _I]),
+    "coli_vk_final_norm_weight": (_I, [_P, _I]),
+    "coli_vk_stream_norm_argmax": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P]),
+    "coli_vk_gqa_full_route_pipe": (_I, [_I, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                         _F, _F, _I, _I]),
+    "coli_vk_gdn_full_route_pipe": (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                         _F, _I, _I]),
+    "coli_vk_expert_group_issue_pipe": (_I, [_P, _P, _P, _P, _P, _I, _I]),
+    "coli_vk_expert_group_take_pipe": (_I, []),
+    "coli_vk_stream_moe_fused": (_I, []),
+    "coli_vk_stream_ix_pending": (_I, []),
+    "coli_vk_stream_ix_hist": (_I, [_I, _P, _I]),
 }
 
 
@@ -250,3 +288,146 @@ class Lib:
 
     def moe_error(self):
         return int(self.L.coli_hip_moe_error())
+
+    # ---- attention / GatedDeltaNet state (c/backend_vulkan.h:110-116, 146-156, 258-279) ----
+    def _ok(self, r, what):
+        if not r:
+            raise RuntimeError(f"{what} failed")
+
+    def kv_ensure(self, layer, max_rows, K, Rd):
+        self._ok(self.L.coli_vk_kv_ensure(layer, max_rows, K, Rd), "coli_vk_kv_ensure")
+
+    def kv_load(self, layer, row0, Krows, Vrows):
+        Krows = np.ascontiguousarray(Krows, dtype=np.float32)
+        Vrows = np.ascontiguousarray(Vrows, dtype=np.float32)
+        n = Krows.shape[0]
+        self._ok(self.L.coli_hip_kv_load(layer, row0, n, _ptr(Krows), _ptr(Vrows)), "coli_hip_kv_load")
+
+    def kv_read(self, layer, row0, n, kd, vd):
+        K = np.empty((n, kd), np.float32)
+        V = np.empty((n, vd), np.float32)
+        self._ok(self.L.coli_hip_kv_read(layer, row0, n, _ptr(K), _ptr(V)), "coli_hip_kv_read")
+        return K, V
+
+    def gqa_norm_weight(self, layer, qn, kn):
+        qn = np.ascontiguousarray(qn, dtype=np.float32)
+        kn = np.ascontiguousarray(kn, dtype=np.float32)
+        self._ok(self.L.coli_vk_gqa_norm_weight(layer, _ptr(qn), _ptr(kn), qn.size), "coli_vk_gqa_norm_weight")
+
+    def gdn_setup(self, layer, VH, KD, VD, K, CD, conv, alog=None, dtb=None, gnorm=None):
+        self._ok(self.L.coli_vk_gdn_state_ensure(layer, VH, KD, VD), "coli_vk_gdn_state_ensure")
+        self._ok(self.L.coli_vk_gdn_conv_ensure(layer, K, CD), "coli_vk_gdn_conv_ensure")
+        conv = np.ascontiguousarray(conv, dtype=np.float32)
+        self._ok(self.L.coli_vk_gdn_conv_weight(layer, _ptr(conv), K, CD), "coli_vk_gdn_conv_weight")
+        if alog is not None:
+            a, d, g = (np.ascontiguousarray(v, dtype=np.float32) for v in (alog, dtb, gnorm))
+            self._ok(self.L.coli_vk_gdn_ba_weight(layer, _ptr(a), _ptr(d), _ptr(g), VH, VD), "coli_vk_gdn_ba_weight")
+
+    def gdn_reset(self):
+        self.L.coli_vk_gdn_reset()
+
+    def gdn_state_read(self, layer, K, CD, VH, KD, VD):
+        ring = np.empty(K * CD, np.float32)
+        S = np.empty(VH * KD * VD, np.float32)
+        self._ok(self.L.coli_hip_gdn_state_read(layer, _ptr(ring), _ptr(S)), "coli_hip_gdn_state_read")
+        return ring, S
+
+    def layer_norm_weight(self, layer, in_ln, post_ln):
+        a = np.ascontiguousarray(in_ln, dtype=np.float32)
+        b = np.ascontiguousarray(post_ln, dtype=np.float32)
+        self._ok(self.L.coli_vk_layer_norm_weight(layer, _ptr(a), _ptr(b), a.size), "coli_vk_layer_norm_weight")
+
+    # ---- layer blocks on host rows ---------------------------------------------------
+    def gqa_full(self, layer, x, tq, tk, tv, to, S, H, KH, hd, rot, pos_base, max_t, eps, theta):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(S * to.O, np.float32)
+        self._ok(self.L.coli_vk_gqa_full(layer, _ptr(x), tq.I, tq.handle, tk.handle, tv.handle, to.handle, _ptr(out),
+                                         S, H, KH, hd, rot, pos_base, max_t, eps, theta, to.O), "coli_vk_gqa_full")
+        return out
+
+    def gdn_full_seq(self, layer, x, params, tqkv, tz, tout, S, KH, KD, VH, VD, CD, K, eps):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        p = np.ascontiguousarray(params, dtype=np.float32)
+        out = np.empty(S * tout.O, np.float32)
+        self._ok(self.L.coli_vk_gdn_full_seq(layer, _ptr(x), S, tqkv.I, tqkv.handle, tz.handle, _ptr(p), tout.handle,
+                                             _ptr(out), KH, KD, VH, VD, CD, K, eps, tout.O), "coli_vk_gdn_full_seq")
+        return out
+
+    def gqa_full_route(self, layer, resid, tq, tk, tv, to, router, ln_layer, S, H, KH, hd, rot, pos_base, max_t,
+                       eps, theta):
+        resid = np.ascontiguousarray(resid, dtype=np.float32)
+        D, E = tq.I, router.O
+        ro, no, pr = np.empty(S * D, np.float32), np.empty(S * D, np.float32), np.empty(S * E, np.float32)
+        self._ok(self.L.coli_vk_gqa_full_route(layer, _ptr(resid), D, tq.handle, tk.handle, tv.handle, to.handle,
+                                               router.handle, ln_layer, _ptr(ro), _ptr(no), _ptr(pr), S, H, KH, hd,
+                                               rot, pos_base, max_t, eps, theta, D, E), "coli_vk_gqa_full_route")
+        return ro, no, pr
+
+    def gdn_full_route(self, layer, x_in, resid, params, tqkv, tz, tout, router, ln_layer, KH, KD, VH, VD, CD, K,
+                       eps):
+        x_in = np.ascontiguousarray(x_in, dtype=np.float32)
+        resid = np.ascontiguousarray(resid, dtype=np.float32)
+        p = np.ascontiguousarray(params, dtype=np.float32)
+        D, E = tqkv.I, router.O
+        ro, no, pr = np.empty(D, np.float32), np.empty(D, np.float32), np.empty(E, np.float32)
+        self._ok(self.L.coli_vk_gdn_full_route(layer, _ptr(x_in), _ptr(resid), D, tqkv.handle, tz.handle, _ptr(p),
+                                               tout.handle, router.handle, ln_layer, _ptr(ro), _ptr(no), _ptr(pr),
+                                               KH, KD, VH, VD, CD, K, eps, D, E), "coli_vk_gdn_full_route")
+        return ro, no, pr
+
+    # ---- residual stream (c/backend_vulkan.h:199-252) ----------------------------------
+    def stream_begin(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        self._ok(self.L.coli_vk_stream_begin(_ptr(x), x.size), "coli_vk_stream_begin")
+
+    def stream_end(self, D, read=True):
+        x = np.empty(D, np.float32) if read else None
+        self._ok(self.L.coli_vk_stream_end(_ptr(x), D), "coli_vk_stream_end")
+        return x
+
+    def gqa_route_pipe(self, layer, tq, tk, tv, to, router, ln_layer, topk, H, KH, hd, rot, pos, max_t, eps, theta):
+        idx = np.full(topk, -1, np.int32)
+        val = np.zeros(topk, np.float32)
+        self._ok(self.L.coli_vk_gqa_full_route_pipe(layer, tq.I, tq.handle, tk.handle, tv.handle, to.handle,
+                                                    router.handle, ln_layer, _ptr(idx), _ptr(val), topk, H, KH, hd,
+                                                    rot, pos, max_t, eps, theta, to.O, router.O),
+                 "coli_vk_gqa_full_route_pipe")
+        return idx, val
+
+    def gdn_route_pipe(self, layer, tqkv, tz, ta, tb, tout, router, ln_layer, topk, KH, KD, VH, VD, CD, K, eps):
+        idx = np.full(topk, -1, np.int32)
+        val = np.zeros(topk, np.float32)
+        self._ok(self.L.coli_vk_gdn_full_route_pipe(layer, tqkv.I, tqkv.handle, tz.handle, ta.handle, tb.handle,
+                                                    tout.handle, router.handle, ln_layer, _ptr(idx), _ptr(val), topk,
+                                                    KH, KD, VH, VD, CD, K, eps, tout.O, router.O),
+                 "coli_vk_gdn_full_route_pipe")
+        return idx, val
+
+    def stream_moe_fused(self):
+        return bool(self.L.coli_vk_stream_moe_fused())
+
+    def stream_ix_hist(self, layer, K):
+        idx = np.full(K, -1, np.int32)
+        n = self.L.coli_vk_stream_ix_hist(layer, _ptr(idx), K)
+        return idx[:n]
+
+    def stream_nrm(self, D):
+        p = self.L.coli_vk_stream_nrm()
+        return None if not p else np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), (D,)).copy()
+
+    def expert_group_issue_pipe(self, gates, ups, downs, weights):
+        g, u, d, r = self._group(gates, ups, downs, [1] * len(gates))
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        self._ok(self.L.coli_vk_expert_group_issue_pipe(g, u, d, r, _ptr(w), len(gates), gates[0].I),
+                 "coli_vk_expert_group_issue_pipe")
+        self._ok(self.L.coli_vk_expert_group_take_pipe(), "coli_vk_expert_group_take_pipe")
+
+    def final_norm_weight(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        self._ok(self.L.coli_vk_final_norm_weight(_ptr(w), w.size), "coli_vk_final_norm_weight")
+
+    def stream_norm_argmax(self, t, eps):
+        idx, val = C.c_int(), C.c_float()
+        self._ok(self.L.coli_vk_stream_norm_argmax(t.ref, None, None, t.fmt, t.I, t.O, t.gs, eps, C.byref(idx),
+                                                   C.byref(val)), "coli_vk_stream_norm_argmax")
+        return idx.value, val.value

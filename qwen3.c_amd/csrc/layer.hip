@@ -1,0 +1,1402 @@
+// layer.hip - the attention and GatedDeltaNet layer blocks of the decode step, the device
+// residual stream and the route tail, on gfx950.
+//
+// Semantics (one token):
+//   gated GQA block        c/qwen.c:581-667   (q|gate projection, per-head zero-centred
+//                          q/k norm, partial RoPE, KV rows at pos, softmax attention,
+//                          sigmoid output gate, o_proj)
+//   GatedDeltaNet block    c/qwen.c:669-776   (qkv/z projections, causal conv1d ring +
+//                          SiLU, l2norm, decay/beta from a/b, delta rule, gated RMSNorm,
+//                          out_proj)
+//   layer composition      c/qwen.c:1340-1352 (resid += block(in_ln(resid));
+//                          resid += moe(post_ln(resid)))
+//   stream / route tail    c/qwen.c:1228-1290 (device residual, device top-k, MoE)
+//
+// Kernels of a layer (all stream-ordered, no host synchronisation inside a layer):
+//   proj_gemv   fmt 6 lanes-layout GEMV over up to 4 tensors that share the input row,
+//               with the input transform fused into the x prologue (in_ln RMSNorm of the
+//               residual, or the GDN per-head gated RMSNorm), the residual add fused into
+//               the store, and (GDN out_proj) the conv-ring shift as a side job.
+//   gdn_core    one block per (v-head, 16-column slice) of the recurrent state: a/b dots,
+//               conv + SiLU of the channels it needs, l2norm, then the delta rule on its
+//               columns.  The state is kept transposed ([VH][VD][KD]) so that a column is
+//               contiguous: each wave updates a column with one coalesced load and two
+//               DPP reductions, and blocks own disjoint columns (in-place, race free).
+//   attn_part   one block per (kv head, 32-position chunk): normalises and rotates the
+//               q rows of its query group (and the new key row, which the chunk holding
+//               pos writes to the cache), then scores, chunk softmax and P.V.
+//   attn_merge  one block per query head: merges the chunks (max, sum of exp), applies
+//               the sigmoid gate.
+#include "fmt6_device.h"
+#include "moe_common.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+namespace coli {
+
+// ---------------------------------------------------------------- block reductions
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Block-wide double sum in a fixed order (deterministic); every thread gets the sum.
+__device__ __forceinline__ double block_sum_d(double v, double *s_red) {
+    v = wave_sum_d(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double s = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += s_red[w];
+    return s;
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v = seg_sum<64>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+// ---------------------------------------------------------------- projections
+constexpr int kMaxSeg = 4;
+enum { XF_PLAIN = 0, XF_NORM = 1, XF_GATED = 2 };
+
+struct ProjSeg {
+    const uint8_t *w;
+    const float *sz;
+    float *y;
+    int O;
+    int g0;   // first row group of the segment in the launch's row-group space
+};
+
+struct ProjArgs {
+    ProjSeg seg[kMaxSeg];
+    int nseg, ngroups;
+    int I, gs, ng, nl, row_bytes;
+    const float *x;    // XF_PLAIN: the input row; XF_NORM: the residual; XF_GATED: raw y
+    const float *xw;   // XF_NORM: norm weight [I] (zero-centred); XF_GATED: gnorm [VD]
+    const float *z;    // XF_GATED: the z projection [I]
+    int VD;
+    float eps;
+    int add;           // 1: y[r] += acc (residual add), 0: y[r] = acc
+    float *ring;       // conv ring [K][CD] to shift (slot K-1 := ring_new), or NULL
+    const float *ring_new;
+    int ring_K, ring_CD;
+};
+
+// XF_NORM: x[i] * r * (1 + w[i]), r = 1/sqrt(mean(x^2) + eps) over the I columns
+// (c/qwen.c:326-330, double sum of squares).  XF_GATED: per head of VD columns,
+// y * r_h * gnorm[d] * silu(z) (c/qwen.c:768-772).  Zero columns past I stay zero.
+template <int XF>
+__device__ __forceinline__ void xf_apply(XRegs &xr, const ProjArgs &a, int ncols) {
+    const int tid = threadIdx.x, nwords = ncols / 8;
+    if constexpr (XF == XF_NORM) {
+        __shared__ double s_red[kWaves];
+        double ss = 0;
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];
+        ss = block_sum_d(ss, s_red);
+        const float r = 1.f / sqrtf((float)(ss / a.I) + a.eps);
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++) {
+            const int w = tid + k * kThreads;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i = w * 8 + c;
+                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * (1.f + a.xw[i]);
+            }
+        }
+    } else if constexpr (XF == XF_GATED) {
+        const int wph = a.VD / 8;   // words per head: a power of two <= 64, lane aligned
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++) {
+            const int w = tid + k * kThreads;
+            double ss = 0;
+#pragma unroll
+            for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];
+            for (int off = 1; off < wph; off <<= 1) ss += __shfl_xor(ss, off);
+            const float r = 1.f / sqrtf((float)(ss / a.VD) + a.eps);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i = w * 8 + c;
+                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * a.xw[i % a.VD] * silu_f(a.z[i]);
+            }
+        }
+    }
+}
+
+// The segment holding row group g (g wave-uniform, so the selection is scalar).
+struct SegSel {
+    const uint8_t *w;
+    const float *sz;
+    float *y;
+    int O, g0;
+};
+__device__ __forceinline__ SegSel seg_of(const ProjArgs &a, int g) {
+    SegSel s = {a.seg[0].w, a.seg[0].sz, a.seg[0].y, a.seg[0].O, a.seg[0].g0};
+#pragma unroll
+    for (int t = 1; t < kMaxSeg; t++)
+        if (t < a.nseg && g >= a.seg[t].g0) s = {a.seg[t].w, a.seg[t].sz, a.seg[t].y, a.seg[t].O, a.seg[t].g0};
+    return s;
+}
+
+// Row groups (RPW rows of one wave step) of all segments form one space; a segment
+// starts on a group boundary, so a wave step never mixes tensors.  U row steps per wave
+// are loaded before any is reduced (the loads of the next step go out while the current
+// one computes), as in the single-tensor GEMV.
+template <int LPR, int CU, int U, int XF>
+__global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
+    __shared__ XPrep P;
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane % LPR, sg = lane / LPR;
+    const int ncols = a.nl * kLaneChunks * 32;
+    const uint32_t srb = (uint32_t)a.ng * 8u;
+    XRegs xr;
+    prep_load(a.x, a.I, ncols, xr);
+    LaneX<CU> L;
+    lane_geo<CU>(j, a.nl, a.I, a.gs, L);
+    const int nw = gridDim.x * kWaves;
+    const int gbase = blockIdx.x * kWaves + wave;
+    uint4 wq[U][kLaneChunks];
+    float2 sv[U][LaneX<CU>::NU];
+    auto load = [&](int u, int g) {
+        if (g < a.ngroups) {
+            const SegSel s = seg_of(a, g);
+            const uint32_t r = (uint32_t)((g - s.g0) * RPW + sg);
+            const uint32_t wtot = (uint32_t)s.O * (uint32_t)a.row_bytes, stot = (uint32_t)s.O * srb;
+            lane_load<CU>(buf_rsrc(s.w, wtot), buf_rsrc(s.sz, stot), min(r * (uint32_t)a.row_bytes, wtot),
+                          min(r * srb, stot), L, wq[u], sv[u]);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < U; u++) load(u, gbase + u * nw);
+    if constexpr (XF != XF_PLAIN) xf_apply<XF>(xr, a, ncols);
+    prep_x(xr, a.gs, ncols, P);
+    lane_x<CU>(P, a.gs, L);
+    for (int g0 = gbase; g0 < a.ngroups; g0 += nw * U) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int g = g0 + u * nw;
+            if (g >= a.ngroups) break;
+            const float part = lane_row<CU>(wq[u], sv[u], L);
+            load(u, g + nw * U);
+            const float acc = seg_sum<LPR>(part);
+            const SegSel s = seg_of(a, g);
+            const int r = (g - s.g0) * RPW + sg;
+            if (j == LPR - 1 && r < s.O) {
+                if (a.add)
+                    s.y[r] += acc;
+                else
+                    s.y[r] = acc;
+            }
+        }
+    }
+    if (a.ring) {   // ring[j] = ring[j+1] (j < K-1), ring[K-1] = new (c/qwen.c:697-700)
+        const int CD = a.ring_CD, K = a.ring_K;
+        for (int ch = blockIdx.x * kThreads + threadIdx.x; ch < CD; ch += gridDim.x * kThreads) {
+            for (int t = 0; t + 1 < K; t++) a.ring[(size_t)t * CD + ch] = a.ring[(size_t)(t + 1) * CD + ch];
+            a.ring[(size_t)(K - 1) * CD + ch] = a.ring_new[ch];
+        }
+    }
+}
+
+// ---------------------------------------------------------------- GatedDeltaNet core
+constexpr int kGdnCols = 16;            // state columns per block (4 per wave)
+constexpr int kGdnColsPerWave = kGdnCols / kWaves;
+constexpr int kGdnMaxKD = 256;
+
+// A small projection row (GDN a/b: [VH, D]) in any device layout: element i of row r.
+struct RowMat {
+    const uint8_t *w;
+    const float *sz;
+    int fmt, layout, I, gs, ng, nl, row_bytes;
+};
+__device__ __forceinline__ float rowmat_w(const RowMat &m, int r, int i) {
+    const uint8_t *row = m.w + (size_t)r * m.row_bytes;
+    if (m.fmt == 0) return ((const float *)row)[i];
+    if (m.fmt == 1) return (float)(int8_t)row[i];   // times the row scale, applied by the caller
+    int nib;
+    if (m.layout == kLayoutLanes) {   // host chunk h = 2 jj + c at slot c * nl + jj, bytes ^ 0x88
+        const int h = i >> 5, jj = h >> 1, c = h & 1;
+        const uint8_t b = row[(c * m.nl + jj) * 16 + ((i & 31) >> 1)] ^ 0x88;
+        nib = (i & 1) ? (b >> 4) : (b & 15);
+    } else {
+        const uint8_t b = row[i >> 1];
+        nib = (i & 1) ? (b >> 4) : (b & 15);
+    }
+    const float *s = m.sz + ((size_t)r * m.ng + i / m.gs) * 2;
+    return ((float)nib - s[1]) * s[0];
+}
+
+struct GdnArgs {
+    const float *qkv;      // [CD] projection of this token (before the conv)
+    const float *ring;     // [K][CD] previous inputs, slot K-1 newest
+    const float *convw;    // [CD][K]
+    float *S;              // [VH][VD][KD]
+    float *y;              // [VH * VD] recurrence output (before the gated norm)
+    const float *params;   // host-packed [decay(VH) | beta(VH) | ...], or NULL: from a/b
+    const float *xin;      // a/b input: the normed row, or NULL: in_ln(resid) here
+    const float *resid, *in_ln;
+    RowMat a, b;
+    const float *alog, *dtb;
+    float eps;
+    int D, KH, KD, VH, VD, K, CD;
+};
+
+template <int KPL>   // state elements per lane of a column (KD = 64 KPL)
+__global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
+    __shared__ double s_red[kWaves];
+    __shared__ float s_q[kGdnMaxKD], s_k[kGdnMaxKD], s_v[kGdnCols];
+    __shared__ float s_ab[2][kWaves], s_nrm[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nsl = g.VD / kGdnCols;
+    const int h = blockIdx.x / nsl, c0 = (blockIdx.x % nsl) * kGdnCols;
+    const int src = h / (g.VH / g.KH), KD = g.KD, key_dim = g.KH * KD;
+
+    // the block's state columns: loads go out first
+    float sv[kGdnColsPerWave][KPL];
+#pragma unroll
+    for (int q = 0; q < kGdnColsPerWave; q++) {
+        const float *col = g.S + ((size_t)h * g.VD + c0 + wave * kGdnColsPerWave + q) * KD + lane * KPL;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) sv[q][e] = col[e];
+    }
+
+    // decay / beta (c/qwen.c:722-728): host params, or a/b over in_ln(resid) here
+    float decay, beta;
+    if (g.params) {
+        decay = g.params[h];
+        beta = g.params[g.VH + h];
+    } else {
+        float r = 0.f;
+        if (!g.xin) {
+            double ss = 0;
+            for (int i = tid; i < g.D; i += kThreads) ss += (double)g.resid[i] * g.resid[i];
+            ss = block_sum_d(ss, s_red);
+            r = 1.f / sqrtf((float)(ss / g.D) + g.eps);
+        }
+        float da = 0.f, db = 0.f;
+        for (int i = tid; i < g.D; i += kThreads) {
+            const float xv = g.xin ? g.xin[i] : g.resid[i] * r * (1.f + g.in_ln[i]);
+            da = fmaf(rowmat_w(g.a, h, i), xv, da);
+            db = fmaf(rowmat_w(g.b, h, i), xv, db);
+        }
+        da = wave_sum_f(da);
+        db = wave_sum_f(db);
+        if (lane == 0) {
+            s_ab[0][wave] = da;
+            s_ab[1][wave] = db;
+        }
+        __syncthreads();
+        float ta = 0.f, tb = 0.f;
+        for (int w = 0; w < kWaves; w++) {
+            ta += s_ab[0][w];
+            tb += s_ab[1][w];
+        }
+        if (g.a.fmt == 1) ta *= g.a.sz[h];
+        if (g.b.fmt == 1) tb *= g.b.sz[h];
+        const float sp_in = ta + g.dtb[h];
+        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
+        decay = expf(-expf(g.alog[h]) * sp);
+        beta = 1.f / (1.f + expf(-tb));
+    }
+
+    // conv1d + SiLU of the channels this block reads (c/qwen.c:697-707): q and k of the
+    // source k-head, v of the block's columns
+    for (int t = tid; t < 2 * KD + kGdnCols; t += kThreads) {
+        const int ch = t < KD ? src * KD + t : t < 2 * KD ? key_dim + src * KD + (t - KD)
+                                                          : 2 * key_dim + h * g.VD + c0 + (t - 2 * KD);
+        const float *w = g.convw + (size_t)ch * g.K;
+        float acc = 0.f;
+        for (int q = 0; q + 1 < g.K; q++) acc += w[q] * g.ring[(size_t)(q + 1) * g.CD + ch];
+        acc += w[g.K - 1] * g.qkv[ch];
+        const float v = silu_f(acc);
+        if (t < KD) s_q[t] = v;
+        else if (t < 2 * KD) s_k[t - KD] = v;
+        else s_v[t - 2 * KD] = v;
+    }
+    __syncthreads();
+    // l2norm of q and k (c/qwen.c:713-721)
+    float sq = 0.f, sk = 0.f;
+    if (wave == 0) {
+        for (int d = lane; d < KD; d += 64) {
+            sq += s_q[d] * s_q[d];
+            sk += s_k[d] * s_k[d];
+        }
+        sq = wave_sum_f(sq);
+        sk = wave_sum_f(sk);
+        if (lane == 0) {
+            s_nrm[0] = sq;
+            s_nrm[1] = sk;
+        }
+    }
+    __syncthreads();
+    const float rq = 1.f / sqrtf(s_nrm[0] + g.eps) / sqrtf((float)KD);
+    const float rk = 1.f / sqrtf(s_nrm[1] + g.eps);
+    float kq[KPL], qq[KPL];
+#pragma unroll
+    for (int e = 0; e < KPL; e++) {
+        kq[e] = s_k[lane * KPL + e] * rk;
+        qq[e] = s_q[lane * KPL + e] * rq;
+    }
+    // delta rule per column (c/qwen.c:749-767)
+#pragma unroll
+    for (int q = 0; q < kGdnColsPerWave; q++) {
+        const int vd = c0 + wave * kGdnColsPerWave + q;
+        float kv = 0.f;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) {
+            sv[q][e] *= decay;
+            kv = fmaf(sv[q][e], kq[e], kv);
+        }
+        kv = wave_sum_f(kv);
+        const float delta = (s_v[vd - c0] - kv) * beta;
+        float yv = 0.f;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) {
+            sv[q][e] = fmaf(kq[e], delta, sv[q][e]);
+            yv = fmaf(sv[q][e], qq[e], yv);
+        }
+        yv = wave_sum_f(yv);
+        float *col = g.S + ((size_t)h * g.VD + vd) * KD + lane * KPL;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) col[e] = sv[q][e];
+        if (lane == 0) g.y[(size_t)h * g.VD + vd] = yv;
+    }
+}
+
+// ---------------------------------------------------------------- GQA attention
+constexpr int kAttT = 32;       // positions per chunk (block)
+constexpr int kAttMaxG = 16;    // query heads per kv head
+constexpr int kAttMaxHD = 512;
+
+struct AttnArgs {
+    const float *q;      // [H][2 hd]: q | gate per head (projection output)
+    const float *k, *v;  // [KH][hd] projections of this token
+    const float *qn, *kn;
+    float *Kc, *Vc;      // [KH][max_t][hd]
+    float *part;         // [KH][nsplit][G][hd + 2]: ctx, then m, l
+    float *ctx;          // [H * hd] merged, gated
+    int H, KH, hd, rot, pos, max_t, nsplit;
+    float eps, theta, scale;
+};
+
+// zero-centred RMSNorm over hd, then partial RoPE at pos (c/qwen.c:326-330, :570-579), of
+// the row src into the LDS row x and, if gdst != NULL, into gdst.  One wave; every output
+// element is written by the lane that computes it from src (no cross-lane LDS reads).
+// The rotation angles are computed in double and rounded to float.
+__device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
+    const int lane = threadIdx.x & 63, hr = a.rot / 2;
+    double ss = 0;
+    for (int d = lane; d < a.hd; d += 64) {
+        const float v = src[d];
+        ss += (double)v * v;
+    }
+    ss = wave_sum_d(ss);
+    const float r = 1.f / sqrtf((float)(ss / a.hd) + a.eps);
+    for (int d = a.rot + lane; d < a.hd; d += 64) {
+        const float v = src[d] * r * (1.f + w[d]);
+        x[d] = v;
+        if (gdst) gdst[d] = v;
+    }
+    for (int jj = lane; jj < hr; jj += 64) {
+        const float inv = (float)pow((double)a.theta, (double)(-2.0f * jj / a.rot));
+        const float ang = (float)a.pos * inv;
+        const float cs = (float)cos((double)ang), sn = (float)sin((double)ang);
+        const float lo = src[jj] * r * (1.f + w[jj]), hi = src[jj + hr] * r * (1.f + w[jj + hr]);
+        const float o0 = lo * cs - hi * sn, o1 = hi * cs + lo * sn;
+        x[jj] = o0;
+        x[jj + hr] = o1;
+        if (gdst) {
+            gdst[jj] = o0;
+            gdst[jj + hr] = o1;
+        }
+    }
+}
+
+template <int DPL>
+__global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) float s_q[kAttMaxG][kAttMaxHD];
+    __shared__ __attribute__((aligned(16))) float s_k[kAttMaxHD];
+    __shared__ float s_p[kAttMaxG][kAttT];
+    __shared__ float s_m[kAttMaxG], s_l[kAttMaxG];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.H / a.KH, hd = a.hd;
+    const int kh = blockIdx.x / a.nsplit, sp = blockIdx.x % a.nsplit;
+    const int t0 = sp * kAttT, t1 = min(t0 + kAttT, a.pos + 1);
+    const bool owns_pos = a.pos >= t0 && a.pos < t1;
+    for (int gg = wave; gg < G; gg += kWaves)
+        norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
+    if (owns_pos && wave == kWaves - 1) {   // the new key row and value row (c/qwen.c:605-614)
+        const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
+        norm_rope_row(s_k, a.Kc + row, a.k + (size_t)kh * hd, a.kn, a);
+        for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
+    }
+    __syncthreads();
+    // scores: 16 lanes per position, 4 positions per wave step
+    const int pl = lane >> 4, part = lane & 15;
+    for (int tb = t0 + wave * 4; tb < t1; tb += kWaves * 4) {
+        const int t = tb + pl;
+        const bool valid = t < t1;
+        const float *kr = (valid && t == a.pos) ? s_k : a.Kc + ((size_t)kh * a.max_t + (valid ? t : t0)) * hd;
+        float kv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e += 4) {
+            const float4 v4 = *(const float4 *)(kr + part * DPL + e);
+            kv[e] = v4.x;
+            kv[e + 1] = v4.y;
+            kv[e + 2] = v4.z;
+            kv[e + 3] = v4.w;
+        }
+        for (int gg = 0; gg < G; gg++) {
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) s = fmaf(s_q[gg][part * DPL + e], kv[e], s);
+            s = seg_sum<16>(s);
+            if (part == 15 && valid) s_p[gg][t - t0] = s * a.scale;
+        }
+    }
+    __syncthreads();
+    const int n = t1 - t0;
+    if (tid < G) {   // chunk max and sum of exp per head
+        float m = -INFINITY;
+        for (int t = 0; t < n; t++) m = fmaxf(m, s_p[tid][t]);
+        float l = 0.f;
+        for (int t = 0; t < n; t++) {
+            const float p = expf(s_p[tid][t] - m);
+            s_p[tid][t] = p;
+            l += p;
+        }
+        s_m[tid] = m;
+        s_l[tid] = l;
+    }
+    __syncthreads();
+    // P.V: thread d of the head dims, all G heads
+    float *pb = a.part + ((size_t)kh * a.nsplit + sp) * G * (hd + 2);
+    for (int d = tid; d < hd; d += kThreads) {
+        float acc[kAttMaxG];
+#pragma unroll
+        for (int gg = 0; gg < kAttMaxG; gg++) acc[gg] = 0.f;
+        for (int t = 0; t < n; t++) {
+            const int tt = t0 + t;
+            const float v = tt == a.pos ? a.v[(size_t)kh * hd + d] : a.Vc[((size_t)kh * a.max_t + tt) * hd + d];
+#pragma unroll
+            for (int gg = 0; gg < kAttMaxG; gg++)
+                if (gg < G) acc[gg] = fmaf(s_p[gg][t], v, acc[gg]);
+        }
+#pragma unroll
+        for (int gg = 0; gg < kAttMaxG; gg++)
+            if (gg < G) pb[(size_t)gg * (hd + 2) + d] = acc[gg];
+    }
+    if (tid < G) {
+        pb[(size_t)tid * (hd + 2) + hd] = s_m[tid];
+        pb[(size_t)tid * (hd + 2) + hd + 1] = s_l[tid];
+    }
+}
+
+constexpr int kAttMaxSplit = 4096;
+
+__global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
+    __shared__ float s_w[kAttMaxSplit];
+    __shared__ float s_red[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x, G = a.H / a.KH, kh = h / G, gg = h % G, hd = a.hd;
+    const int ns = (a.pos + 1 + kAttT - 1) / kAttT;
+    const float *pb = a.part + ((size_t)kh * a.nsplit) * G * (hd + 2) + (size_t)gg * (hd + 2);
+    const size_t stride = (size_t)G * (hd + 2);
+    float m = -INFINITY;
+    for (int s = tid; s < ns; s += kThreads) m = fmaxf(m, pb[s * stride + hd]);
+    m = wave_max_f(m);
+    if (lane == 0) s_red[wave] = m;
+    __syncthreads();
+    m = s_red[0];
+    for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_red[w]);
+    float l = 0.f;
+    for (int s = tid; s < ns; s += kThreads) {
+        const float w = expf(pb[s * stride + hd] - m);
+        s_w[s] = w;
+        l += pb[s * stride + hd + 1] * w;
+    }
+    l = wave_sum_f(l);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = l;
+    __syncthreads();
+    l = 0.f;
+    for (int w = 0; w < kWaves; w++) l += s_red[w];
+    const float inv = 1.f / l;
+    const float *gate = a.q + (size_t)h * 2 * hd + hd;
+    for (int d = tid; d < hd; d += kThreads) {
+        float acc = 0.f;
+        for (int s = 0; s < ns; s++) acc = fmaf(pb[s * stride + d], s_w[s], acc);
+        a.ctx[(size_t)h * hd + d] = acc * inv * (1.f / (1.f + expf(-gate[d])));
+    }
+}
+
+// ---------------------------------------------------------------- small kernels
+__global__ void rms_rows(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ y, int D,
+                         float eps) {
+    __shared__ double s_red[kWaves];
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += kThreads) ss += (double)x[i] * x[i];
+    ss = block_sum_d(ss, s_red);
+    const float r = 1.f / sqrtf((float)(ss / D) + eps);
+    for (int i = threadIdx.x; i < D; i += kThreads) y[i] = x[i] * r * (1.f + w[i]);
+}
+
+// softmax + K greedy picks + renorm of one router row (device top-k of the route tail)
+__global__ __launch_bounds__(kThreads) void route_row(const float *__restrict__ logits, int E, int K, int *idx,
+                                                      float *val) {
+    __shared__ RouteLds R;
+    for (int e = threadIdx.x; e < E; e += kThreads) R.p[e] = logits[e];
+    route_select(R, E, K);
+    if (threadIdx.x < K) {
+        idx[threadIdx.x] = R.idx[threadIdx.x];
+        val[threadIdx.x] = R.val[threadIdx.x] / R.vsum;
+    }
+}
+
+// ================================================================ host side
+constexpr int kMaxLayers = 160;   // c/backend_vulkan.c:63 (VK_KV_LAYERS)
+
+struct KvState {             // device KV mirror: row = kv_head * max_t + pos
+    float *K = nullptr, *V = nullptr;
+    int rows = 0, kd = 0, vd = 0, cap_rows = 0;
+};
+struct QkNorm {
+    float *qn = nullptr, *kn = nullptr;
+    int hd = 0;
+};
+struct GdnState {
+    float *S = nullptr;      // [VH][VD][KD] (transposed from the reference's [VH][KD][VD])
+    int VH = 0, KD = 0, VD = 0;
+    float *ring = nullptr;   // [K][CD], slot K-1 newest
+    float *convw = nullptr;  // [CD][K]
+    int K = 0, CD = 0, convw_set = 0;
+    float *alog = nullptr, *dtb = nullptr, *gnorm = nullptr;
+    int ba_VH = 0, ba_VD = 0;
+};
+struct LnState {
+    float *in_ln = nullptr, *post_ln = nullptr;
+    int D = 0;
+};
+static KvState g_kv[kMaxLayers];
+static QkNorm g_qk[kMaxLayers];
+static GdnState g_gdn[kMaxLayers];
+static LnState g_ln[kMaxLayers];
+
+// one-shot failures of the layer blocks: one stderr line per reason
+static bool refuse(const char *why) {
+    static const char *last = nullptr;
+    if (why != last) fprintf(stderr, "[HIP] layer block refused: %s\n", why);
+    last = why;
+    return false;
+}
+
+static bool h2d(void *d, const void *h, size_t bytes, const char *who) {
+    if (!bytes) return true;
+    const hipError_t e = hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail(who, e);
+    return sync_stream(who);
+}
+
+// arena copy of a host vector (re-uploaded in place when the size matches)
+static bool put_vec(float **d, int *have, const float *h, int n, const char *who) {
+    if (!h || n < 1) return false;
+    if (!*d || *have != n) {
+        float *p = (float *)arena_alloc((size_t)n * 4);
+        if (!p) return false;
+        *d = p;
+        *have = n;
+    }
+    return h2d(*d, h, (size_t)n * 4, who);
+}
+
+// ---------------------------------------------------------------- work buffers
+enum {
+    W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
+    W_HIST, W_COUNT
+};
+struct WorkBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+static WorkBuf g_w[W_COUNT];
+static float *wbuf(int slot, size_t n) {
+    return scratch(&g_w[slot].p, &g_w[slot].cap, n * 4 + 256) ? (float *)g_w[slot].p : nullptr;
+}
+
+// ---------------------------------------------------------------- projection launch
+struct SegIn {
+    const ColiVkTensor *t;
+    float *y;
+};
+
+constexpr int kProjU = 4;
+
+template <int LPR, int CU, int XF>
+static bool launch_proj(ProjArgs &a, hipStream_t st) {
+    auto kern = proj_gemv<LPR, CU, kProjU, XF>;
+    static int per = 0;
+    if (!per) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, kThreads, 0) != hipSuccess || per < 1) per = 1;
+    }
+    long nb = ((long)a.ngroups + kWaves * kProjU - 1) / (kWaves * kProjU);
+    const long cap = (long)n_cu() * per;
+    if (nb > cap) nb = cap;
+    if (a.ring) {   // the ring shift wants a few blocks even when the projection is small
+        const long want = ((long)a.ring_CD + kThreads - 1) / kThreads;
+        if (nb < want) nb = want < cap ? want : cap;
+    }
+    if (nb < 1) nb = 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("projection launch", e);
+    return true;
+}
+
+template <int CU, int XF>
+static bool proj_lpr(ProjArgs &a, int lpr, hipStream_t st) {
+    switch (lpr) {
+    case 2: return launch_proj<2, CU, XF>(a, st);
+    case 4: return launch_proj<4, CU, XF>(a, st);
+    case 8: return launch_proj<8, CU, XF>(a, st);
+    case 16: return launch_proj<16, CU, XF>(a, st);
+    case 32: return launch_proj<32, CU, XF>(a, st);
+    case 64: return launch_proj<64, CU, XF>(a, st);
+    default: return refuse("projection row too short for the lanes kernel");
+    }
+}
+
+static int pow2_up(int n) {
+    int l = 1;
+    while (l < n) l <<= 1;
+    return l;
+}
+
+// y_s = W_s x' for the segments (same I, gs: they share the input row x' = XF(x)).
+static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *xw, const float *z, int VD, float eps,
+                 bool add, float *ring, const float *ring_new, int ring_K, int ring_CD, hipStream_t st) {
+    if (n < 1 || n > kMaxSeg) return refuse("projection segment count");
+    const ColiVkTensor *t0 = segs[0].t;
+    for (int i = 0; i < n; i++) {
+        const ColiVkTensor *t = segs[i].t;
+        if (!t || !segs[i].y) return refuse("NULL projection tensor");
+        if (t->fmt != 6 || t->layout != kLayoutLanes) return refuse("projection is not fmt 6 (gs % 32 == 0, I <= 4096)");
+        if (t->I != t0->I || t->gs != t0->gs || t->nl != t0->nl || t->row_bytes != t0->row_bytes)
+            return refuse("fused projections differ in input geometry");
+    }
+    ProjArgs a;
+    memset(&a, 0, sizeof(a));
+    const int lpr = pow2_up(t0->nl), rpw = 64 / (lpr < 2 ? 2 : lpr);
+    int g = 0;
+    for (int i = 0; i < n; i++) {
+        a.seg[i] = {segs[i].t->w, segs[i].t->sz, segs[i].y, segs[i].t->O, g};
+        g += (segs[i].t->O + rpw - 1) / rpw;
+    }
+    a.nseg = n;
+    a.ngroups = g;
+    a.I = t0->I;
+    a.gs = t0->gs;
+    a.ng = t0->ng;
+    a.nl = t0->nl;
+    a.row_bytes = t0->row_bytes;
+    a.x = x;
+    a.xw = xw;
+    a.z = z;
+    a.VD = VD;
+    a.eps = eps;
+    a.add = add ? 1 : 0;
+    a.ring = ring;
+    a.ring_new = ring_new;
+    a.ring_K = ring_K;
+    a.ring_CD = ring_CD;
+    if (xf == XF_GATED) {
+        const int wph = VD / 8;
+        if (VD % 8 || wph < 1 || wph > 64 || (wph & (wph - 1)) || a.I % VD) return refuse("gated norm head size");
+    }
+    const int l = lpr < 2 ? 2 : lpr;
+    const bool wide = t0->gs >= 32 * kLaneChunks;
+    switch (xf) {
+    case XF_PLAIN: return wide ? proj_lpr<kLaneChunks, XF_PLAIN>(a, l, st) : proj_lpr<1, XF_PLAIN>(a, l, st);
+    case XF_NORM: return wide ? proj_lpr<kLaneChunks, XF_NORM>(a, l, st) : proj_lpr<1, XF_NORM>(a, l, st);
+    default: return wide ? proj_lpr<kLaneChunks, XF_GATED>(a, l, st) : proj_lpr<1, XF_GATED>(a, l, st);
+    }
+}
+
+// ---------------------------------------------------------------- GQA block
+struct GqaDims {
+    int H, KH, hd, rot, max_t;
+    float eps, theta;
+};
+
+// One token at position pos.  ln != NULL: the input is the residual and the block applies
+// in_ln itself; otherwise src is the normed row.  add: dst += block, else dst = block.
+static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *tq, ColiVkTensor *tk, ColiVkTensor *tv,
+                      ColiVkTensor *to, float *dst, bool add, const GqaDims &d, int pos, hipStream_t st) {
+    if (kvi < 0 || kvi >= kMaxLayers) return refuse("attention layer index");
+    const KvState &kv = g_kv[kvi];
+    const QkNorm &qk = g_qk[kvi];
+    const int H = d.H, KH = d.KH, hd = d.hd;
+    if (!kv.K || kv.kd != hd || kv.vd != hd || (long)KH * d.max_t > kv.rows) return refuse("KV mirror not ensured");
+    if (!qk.qn || qk.hd != hd) return refuse("q/k norm weights not set");
+    if (H < 1 || KH < 1 || H % KH || H / KH > kAttMaxG || hd % 64 || hd > kAttMaxHD || d.rot < 2 || d.rot > hd ||
+        d.rot % 2 || pos < 0 || pos >= d.max_t)
+        return refuse("attention shape");
+    if (!tq || !tk || !tv || !to || tq->O != 2 * H * hd || tk->O != KH * hd || tv->O != KH * hd || to->I != H * hd)
+        return refuse("attention projection shapes");
+    const int nsplit = (pos + 1 + kAttT - 1) / kAttT, G = H / KH;
+    if (nsplit > kAttMaxSplit) return refuse("attention window");
+    float *q = wbuf(W_Q, (size_t)2 * H * hd), *k = wbuf(W_K, (size_t)KH * hd), *v = wbuf(W_V, (size_t)KH * hd);
+    float *ctx = wbuf(W_CTX, (size_t)H * hd), *part = wbuf(W_PART, (size_t)KH * nsplit * G * (hd + 2));
+    if (!q || !k || !v || !ctx || !part) return false;
+    const SegIn in[3] = {{tq, q}, {tk, k}, {tv, v}};
+    if (!proj(in, 3, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, nullptr, nullptr, 0, 0, st))
+        return false;
+    AttnArgs a;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.qn = qk.qn;
+    a.kn = qk.kn;
+    a.Kc = kv.K;
+    a.Vc = kv.V;
+    a.part = part;
+    a.ctx = ctx;
+    a.H = H;
+    a.KH = KH;
+    a.hd = hd;
+    a.rot = d.rot;
+    a.pos = pos;
+    a.max_t = d.max_t;
+    a.nsplit = nsplit;
+    a.eps = d.eps;
+    a.theta = d.theta;
+    a.scale = 1.f / sqrtf((float)hd);
+    switch (hd / 16) {
+    case 4: hipLaunchKernelGGL(attn_part<4>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(attn_part<8>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
+    case 16: hipLaunchKernelGGL(attn_part<16>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(attn_part<32>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
+    default: return refuse("head dim not in {64, 128, 256, 512}");
+    }
+    hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kThreads), 0, st, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("attention launch", e);
+    const SegIn o[1] = {{to, dst}};
+    return proj(o, 1, XF_PLAIN, ctx, nullptr, nullptr, 0, d.eps, add, nullptr, nullptr, 0, 0, st);
+}
+
+// ---------------------------------------------------------------- GDN block
+struct GdnDims {
+    int KH, KD, VH, VD, CD, K;
+    float eps;
+};
+
+static RowMat rowmat(const ColiVkTensor *t) {
+    RowMat m;
+    m.w = t->w;
+    m.sz = t->sz;
+    m.fmt = t->fmt;
+    m.layout = t->layout;
+    m.I = t->I;
+    m.gs = t->gs;
+    m.ng = t->ng;
+    m.nl = t->nl;
+    m.row_bytes = t->row_bytes;
+    return m;
+}
+
+// One token.  params != NULL: host-packed [decay | beta | gnorm] (device copy); otherwise
+// decay/beta from the a/b projections of in_ln(resid) and the layer's A_log/dt_bias/gnorm.
+static bool gdn_block(int gi, const float *src, const float *ln, const float *params, ColiVkTensor *tqkv,
+                      ColiVkTensor *tz, ColiVkTensor *ta, ColiVkTensor *tb, ColiVkTensor *tout, float *dst, bool add,
+                      const GdnDims &d, hipStream_t st) {
+    if (gi < 0 || gi >= kMaxLayers) return refuse("GDN layer index");
+    GdnState &G = g_gdn[gi];
+    if (!G.S || G.VH != d.VH || G.KD != d.KD || G.VD != d.VD) return refuse("GDN state not ensured");
+    if (!G.ring || !G.convw_set || G.K != d.K || G.CD != d.CD) return refuse("GDN conv ring/weights not set");
+    if (d.KH < 1 || d.VH % d.KH || d.CD != 2 * d.KH * d.KD + d.VH * d.VD || d.KD % 64 || d.KD > kGdnMaxKD ||
+        d.VD % kGdnCols || d.K < 1 || d.K > 16)
+        return refuse("GDN shape");
+    if (!tqkv || !tz || !tout || tqkv->O != d.CD || tz->O != d.VH * d.VD || tout->I != d.VH * d.VD)
+        return refuse("GDN projection shapes");
+    if (!params) {
+        if (!G.alog || G.ba_VH != d.VH || G.ba_VD != d.VD) return refuse("GDN A_log/dt_bias/gnorm not set");
+        if (!ta || !tb || ta->O != d.VH || tb->O != d.VH || ta->I != tqkv->I || tb->I != tqkv->I ||
+            (ta->fmt != 0 && ta->fmt != 1 && ta->fmt != 6) || (tb->fmt != 0 && tb->fmt != 1 && tb->fmt != 6))
+            return refuse("GDN a/b projections");
+    }
+    float *qkv = wbuf(W_QKV, d.CD), *z = wbuf(W_Z, (size_t)d.VH * d.VD), *y = wbuf(W_Y, (size_t)d.VH * d.VD);
+    if (!qkv || !z || !y) return false;
+    const SegIn in[2] = {{tqkv, qkv}, {tz, z}};
+    if (!proj(in, 2, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, nullptr, nullptr, 0, 0, st))
+        return false;
+    GdnArgs g;
+    memset(&g, 0, sizeof(g));
+    g.qkv = qkv;
+    g.ring = G.ring;
+    g.convw = G.convw;
+    g.S = G.S;
+    g.y = y;
+    g.params = params;
+    g.xin = ln ? nullptr : src;
+    g.resid = src;
+    g.in_ln = ln;
+    if (!params) {
+        g.a = rowmat(ta);
+        g.b = rowmat(tb);
+    }
+    g.alog = G.alog;
+    g.dtb = G.dtb;
+    g.eps = d.eps;
+    g.D = tqkv->I;
+    g.KH = d.KH;
+    g.KD = d.KD;
+    g.VH = d.VH;
+    g.VD = d.VD;
+    g.K = d.K;
+    g.CD = d.CD;
+    const dim3 grid(d.VH * (d.VD / kGdnCols));
+    switch (d.KD / 64) {
+    case 1: hipLaunchKernelGGL(gdn_core<1>, grid, dim3(kThreads), 0, st, g); break;
+    case 2: hipLaunchKernelGGL(gdn_core<2>, grid, dim3(kThreads), 0, st, g); break;
+    case 4: hipLaunchKernelGGL(gdn_core<4>, grid, dim3(kThreads), 0, st, g); break;
+    default: return refuse("GDN key head dim not in {64, 128, 256}");
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("GDN launch", e);
+    const float *gnorm = params ? params + 2 * d.VH : G.gnorm;
+    const SegIn o[1] = {{tout, dst}};
+    return proj(o, 1, XF_GATED, y, gnorm, z, d.VD, d.eps, add, G.ring, qkv, d.K, d.CD, st);
+}
+
+// ---------------------------------------------------------------- residual stream state
+struct StreamState {
+    float *d_resid = nullptr;
+    size_t resid_cap = 0;
+    float *h_y = nullptr;         // pinned staging (stream_add, route read-back)
+    size_t hy_cap = 0;
+    float *d_y = nullptr;
+    size_t dy_cap = 0;
+    float *d_fnw = nullptr;       // final norm weight
+    size_t fnw_cap = 0;
+    int fn_D = 0;
+    float *d_xn = nullptr;        // normed row + argmax result
+    size_t xn_cap = 0;
+    int D = 0, live = 0;
+    int fused_last = 0;           // the last route_pipe ran the MoE on the device
+    int pending = 0;              // top-k ids of fused layers await stream_end
+    int hist_K[kMaxLayers];       // ids recorded per layer in this stream (0 = none)
+    int h_hist[kMaxLayers * kMaxK];
+    float *h_nrm = nullptr;       // host copy of the last non-fused route's nrm
+    size_t hnrm_cap = 0;
+};
+static StreamState g_str;
+
+float *stream_resid(int D) { return g_str.live && g_str.D == D ? g_str.d_resid : nullptr; }
+const float *stream_nrm_dev(int D) {
+    return g_str.live && g_str.D == D && !g_str.fused_last && g_w[W_NRM].p ? (const float *)g_w[W_NRM].p : nullptr;
+}
+
+// post_ln + router (+ device top-k) after the block has updated the residual `resid`.
+// fused: the layer's MoE block runs on the device (expert table) and accumulates into
+// resid; otherwise idx/val (route_pipe) or nothing is produced here.
+static bool route_tail(int ln_layer, const float *resid, ColiVkTensor *router, int E, int topk, float eps,
+                       float *nrm, float *logits, hipStream_t st) {
+    const LnState &ln = g_ln[ln_layer];
+    hipLaunchKernelGGL(rms_rows, dim3(1), dim3(kThreads), 0, st, resid, ln.post_ln, nrm, ln.D, eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("post norm launch", e);
+    (void)E, (void)topk;
+    if (logits && !gemv(router, nrm, logits, 1, st)) return false;
+    return true;
+}
+
+}  // namespace coli
+
+using namespace coli;
+
+extern "C" int coli_vk_tensor_ensure(ColiVkTensor **, const void *, const float *, int, int, int, int);
+
+static bool ln_ok(int ln_layer, int D) {
+    return ln_layer >= 0 && ln_layer < kMaxLayers && g_ln[ln_layer].in_ln && g_ln[ln_layer].D == D;
+}
+
+// ---------------------------------------------------------------- ABI: KV mirror + GQA
+// c/backend_vulkan.h:110-116, c/backend_vulkan.c:1705-1743
+COLI_API int coli_vk_kv_ensure(int layer, int max_rows, int K, int Rd) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || max_rows < 1 || K < 1 || Rd < 1) return 0;
+    KvState &v = g_kv[layer];
+    if (v.K && v.rows) return v.rows >= max_rows && v.kd == K && v.vd == Rd;
+    if (!v.K || v.cap_rows < max_rows || v.kd != K || v.vd != Rd) {   // kv_reset keeps the old arena slice
+        v.K = (float *)arena_alloc((size_t)max_rows * K * 4);
+        v.V = (float *)arena_alloc((size_t)max_rows * Rd * 4);
+        if (!v.K || !v.V) {
+            v = KvState();
+            return 0;
+        }
+        v.cap_rows = max_rows;
+    }
+    v.rows = max_rows;
+    v.kd = K;
+    v.vd = Rd;
+    hipError_t e = hipMemsetAsync(v.K, 0, (size_t)max_rows * K * 4, stream());
+    if (e == hipSuccess) e = hipMemsetAsync(v.V, 0, (size_t)max_rows * Rd * 4, stream());
+    if (e != hipSuccess) return fail("kv ensure", e) ? 1 : 0;
+    return sync_stream("kv ensure") ? 1 : 0;
+}
+
+// one host cache row (normed + roped key, raw value) into the mirror
+COLI_API int coli_vk_kv_row(int layer, int pos, const float *L, const float *R) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || !L || !R) return 0;
+    KvState &v = g_kv[layer];
+    if (!v.K || pos < 0 || pos >= v.rows) return 0;
+    return h2d(v.K + (size_t)pos * v.kd, L, (size_t)v.kd * 4, "kv row") &&
+                   h2d(v.V + (size_t)pos * v.vd, R, (size_t)v.vd * 4, "kv row")
+               ? 1
+               : 0;
+}
+
+// Rows [row0, row0 + n) of a layer's mirror from host arrays [n][kd] and [n][vd] (a bulk
+// kv_row; used to seed a cache of a given length).
+COLI_API int coli_hip_kv_load(int layer, int row0, int n, const float *L, const float *R) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || !L || !R || n < 0) return 0;
+    KvState &v = g_kv[layer];
+    if (!v.K || row0 < 0 || row0 + n > v.rows) return 0;
+    return h2d(v.K + (size_t)row0 * v.kd, L, (size_t)n * v.kd * 4, "kv load") &&
+                   h2d(v.V + (size_t)row0 * v.vd, R, (size_t)n * v.vd * 4, "kv load")
+               ? 1
+               : 0;
+}
+
+// Rows [row0, row0 + n) of the mirror back to the host (tests).
+COLI_API int coli_hip_kv_read(int layer, int row0, int n, float *L, float *R) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || !L || !R || n < 0) return 0;
+    KvState &v = g_kv[layer];
+    if (!v.K || row0 < 0 || row0 + n > v.rows || !sync_stream("kv read")) return 0;
+    return hipMemcpy(L, v.K + (size_t)row0 * v.kd, (size_t)n * v.kd * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+                   hipMemcpy(R, v.V + (size_t)row0 * v.vd, (size_t)n * v.vd * 4, hipMemcpyDeviceToHost) ==
+                       hipSuccess
+               ? 1
+               : 0;
+}
+
+COLI_API void coli_vk_kv_reset(void) {
+    for (int i = 0; i < kMaxLayers; i++) g_kv[i].rows = 0;   // slices stay for a later kv_ensure
+}
+
+COLI_API int coli_vk_gqa_available(void) { return ok() ? 1 : 0; }
+COLI_API int coli_vk_gqa_full_available(void) { return ok() ? 1 : 0; }
+
+COLI_API int coli_vk_gqa_norm_weight(int layer, const float *qnw, const float *knw, int hd) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || hd < 1) return 0;
+    QkNorm &q = g_qk[layer];
+    int h1 = q.hd, h2 = q.hd;
+    if (!put_vec(&q.qn, &h1, qnw, hd, "q norm weight") || !put_vec(&q.kn, &h2, knw, hd, "k norm weight")) return 0;
+    q.hd = hd;
+    return 1;
+}
+
+// Host rows through the device block, S tokens in order (token s attends to the rows the
+// earlier tokens of the call wrote).
+static int gqa_rows(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTensor *tk, ColiVkTensor *tv,
+                    ColiVkTensor *to, float *out, int S, const GqaDims &d, int pos_base, int Dout) {
+    if (!ok() || !x || !out || S < 1 || D < 1 || !tq || tq->I != D || !to || to->O != Dout) return 0;
+    float *dx = wbuf(W_IO_X, (size_t)S * D), *dout = wbuf(W_IO_O, (size_t)S * Dout);
+    if (!dx || !dout || !h2d(dx, x, (size_t)S * D * 4, "gqa rows")) return 0;
+    for (int s = 0; s < S; s++)
+        if (!gqa_block(layer, dx + (size_t)s * D, nullptr, tq, tk, tv, to, dout + (size_t)s * Dout, false, d,
+                       pos_base + s, stream()))
+            return 0;
+    if (!sync_stream("gqa rows")) return 0;
+    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+}
+
+// c/backend_vulkan.h:171-178: x is the normed input [S, D]; out [S, Dout] = block output
+COLI_API int coli_vk_gqa_full(int layer, const float *x, int D, ColiVkTensor *gq_t, ColiVkTensor *gk_t,
+                              ColiVkTensor *gv_t, ColiVkTensor *out_t, float *out, int S, int H, int KH, int hd,
+                              int rot, int pos_base, int max_t, float eps, float theta, int Dout) {
+    const GqaDims d = {H, KH, hd, rot, max_t, eps, theta};
+    return gqa_rows(layer, x, D, gq_t, gk_t, gv_t, out_t, out, S, d, pos_base, Dout);
+}
+
+// The staged forms take host-computed q (already normed and rotated) and the host KV
+// mirror rows; the engine only reaches them when the fused block is off.  Not provided:
+// 0 makes the engine attend on the CPU (c/qwen.c:620-636).
+COLI_API int coli_vk_gqa(int, const float *, float *, int, int, int, int, int, int, int, float) { return 0; }
+COLI_API int coli_vk_gqa_project(int, const float *, ColiVkTensor *, float *, int, int, int, int, int, int, int,
+                                 float, int) {
+    return 0;
+}
+
+// ---------------------------------------------------------------- ABI: GDN state
+// c/backend_vulkan.h:146-156, :258-279, c/backend_vulkan.c:1745-1790
+COLI_API int coli_vk_gdn_available(void) { return ok() ? 1 : 0; }
+COLI_API int coli_vk_gdn_full_available(void) { return ok() ? 1 : 0; }
+
+COLI_API int coli_vk_gdn_state_ensure(int layer, int VH, int KD, int VD) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || VH < 1 || KD < 1 || VD < 1) return 0;
+    GdnState &G = g_gdn[layer];
+    if (G.S) return G.VH == VH && G.KD == KD && G.VD == VD;
+    const size_t bytes = (size_t)VH * KD * VD * 4;
+    G.S = (float *)arena_alloc(bytes);
+    if (!G.S) return 0;
+    G.VH = VH;
+    G.KD = KD;
+    G.VD = VD;
+    const hipError_t e = hipMemsetAsync(G.S, 0, bytes, stream());
+    if (e != hipSuccess) return fail("gdn state", e) ? 1 : 0;
+    return sync_stream("gdn state") ? 1 : 0;
+}
+
+COLI_API void coli_vk_gdn_reset(void) {
+    if (!ok()) return;
+    for (int i = 0; i < kMaxLayers; i++) {
+        GdnState &G = g_gdn[i];
+        if (G.S) (void)hipMemsetAsync(G.S, 0, (size_t)G.VH * G.KD * G.VD * 4, stream());
+        if (G.ring) (void)hipMemsetAsync(G.ring, 0, (size_t)G.K * G.CD * 4, stream());
+    }
+    (void)sync_stream("gdn reset");
+}
+
+COLI_API int coli_vk_gdn_conv_ensure(int layer, int conv_k, int conv_dim) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || conv_k < 1 || conv_k > 16 || conv_dim < 1) return 0;
+    GdnState &G = g_gdn[layer];
+    if (G.ring) return G.K == conv_k && G.CD == conv_dim;
+    const size_t n = (size_t)conv_k * conv_dim;
+    G.ring = (float *)arena_alloc(n * 4);
+    G.convw = (float *)arena_alloc(n * 4);
+    if (!G.ring || !G.convw) {
+        G.ring = G.convw = nullptr;
+        return 0;
+    }
+    G.K = conv_k;
+    G.CD = conv_dim;
+    const hipError_t e = hipMemsetAsync(G.ring, 0, n * 4, stream());
+    if (e != hipSuccess) return fail("gdn conv ring", e) ? 1 : 0;
+    return sync_stream("gdn conv ring") ? 1 : 0;
+}
+
+// cw [conv_dim][conv_k] (c/qwen.c:702: w = conv + ch * K)
+COLI_API int coli_vk_gdn_conv_weight(int layer, const float *cw, int conv_k, int conv_dim) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || !cw) return 0;
+    GdnState &G = g_gdn[layer];
+    if (!G.ring || G.K != conv_k || G.CD != conv_dim) return 0;
+    if (!h2d(G.convw, cw, (size_t)conv_k * conv_dim * 4, "gdn conv weight")) return 0;
+    G.convw_set = 1;
+    return 1;
+}
+
+// c/qwen.c:1525-1533: A_log [VH], dt_bias [VH], gated-norm weight [VD] of a GDN layer
+COLI_API int coli_vk_gdn_ba_weight(int layer, const float *alog, const float *dtb, const float *gnorm, int VH,
+                                   int VD) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || VH < 1 || VD < 1) return 0;
+    GdnState &G = g_gdn[layer];
+    int h1 = G.ba_VH, h2 = G.ba_VH, h3 = G.ba_VD;
+    if (!put_vec(&G.alog, &h1, alog, VH, "A_log") || !put_vec(&G.dtb, &h2, dtb, VH, "dt_bias") ||
+        !put_vec(&G.gnorm, &h3, gnorm, VD, "gdn norm weight"))
+        return 0;
+    G.ba_VH = VH;
+    G.ba_VD = VD;
+    return 1;
+}
+
+static int gdn_rows(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                    const float *params, ColiVkTensor *out_t, float *out, const GdnDims &d, int Dout) {
+    if (!ok() || !x || !params || !out || S < 1 || !gqkv_t || gqkv_t->I != D || !out_t || out_t->O != Dout)
+        return 0;
+    const int prs = 2 * d.VH + d.VD;
+    float *dx = wbuf(W_IO_X, (size_t)S * D), *dp = wbuf(W_IO_P, (size_t)S * prs),
+          *dout = wbuf(W_IO_O, (size_t)S * Dout);
+    if (!dx || !dp || !dout || !h2d(dx, x, (size_t)S * D * 4, "gdn rows") ||
+        !h2d(dp, params, (size_t)S * prs * 4, "gdn params"))
+        return 0;
+    for (int s = 0; s < S; s++)
+        if (!gdn_block(layer, dx + (size_t)s * D, nullptr, dp + (size_t)s * prs, gqkv_t, gz_t, nullptr, nullptr,
+                       out_t, dout + (size_t)s * Dout, false, d, stream()))
+            return 0;
+    if (!sync_stream("gdn rows")) return 0;
+    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+}
+
+// c/backend_vulkan.h:268-271: one token, x normed, params [decay | beta | gnorm]
+COLI_API int coli_vk_gdn_full(int layer, const float *x, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                              const float *params, ColiVkTensor *out_t, float *out, int KH, int KD, int VH, int VD,
+                              int conv_dim, int conv_k, float eps, int Dout) {
+    const GdnDims d = {KH, KD, VH, VD, conv_dim, conv_k, eps};
+    return gdn_rows(layer, x, 1, D, gqkv_t, gz_t, params, out_t, out, d, Dout);
+}
+
+// c/backend_vulkan.h:272-279: S tokens in order (the state and ring advance per token)
+COLI_API int coli_vk_gdn_full_seq(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                                  const float *params, ColiVkTensor *out_t, float *out, int KH, int KD, int VH, int VD,
+                                  int conv_dim, int conv_k, float eps, int Dout) {
+    const GdnDims d = {KH, KD, VH, VD, conv_dim, conv_k, eps};
+    return gdn_rows(layer, x, S, D, gqkv_t, gz_t, params, out_t, out, d, Dout);
+}
+
+// Staged forms (host qn/kn/v/z/decay/beta): reached only when the fused block is off; 0
+// keeps that token's recurrence on the CPU (c/qwen.c:741-761).
+COLI_API int coli_vk_gdn(int, const float *, const float *, const float *, const float *, const float *, const float *,
+                         const float *, float *, int, int, int, int, float) {
+    return 0;
+}
+COLI_API int coli_vk_gdn_project(int, const float *, const float *, const float *, const float *, const float *,
+                                 const float *, const float *, ColiVkTensor *, float *, int, int, int, int, float,
+                                 int) {
+    return 0;
+}
+
+// GDN state of a layer back to the host in the reference's layouts (tests): conv ring
+// [K][CD], recurrent state [VH][KD][VD].
+COLI_API int coli_hip_gdn_state_read(int layer, float *ring, float *S) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || !ring || !S) return 0;
+    GdnState &G = g_gdn[layer];
+    if (!G.S || !G.ring || !sync_stream("gdn state read")) return 0;
+    const size_t n = (size_t)G.VH * G.KD * G.VD;
+    float *t = (float *)malloc(n * 4);
+    if (!t) return 0;
+    int r = hipMemcpy(ring, G.ring, (size_t)G.K * G.CD * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+            hipMemcpy(t, G.S, n * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    for (int h = 0; r && h < G.VH; h++)   // device [h][vd][kd] -> host [h][kd][vd]
+        for (int kd = 0; kd < G.KD; kd++)
+            for (int vd = 0; vd < G.VD; vd++)
+                S[((size_t)h * G.KD + kd) * G.VD + vd] = t[((size_t)h * G.VD + vd) * G.KD + kd];
+    free(t);
+    return r;
+}
+
+// ---------------------------------------------------------------- ABI: route fusion
+// c/backend_vulkan.h:179-198
+COLI_API int coli_vk_moe_route_available(void) { return ok() ? 1 : 0; }
+
+COLI_API int coli_vk_layer_norm_weight(int layer, const float *in_ln, const float *post_ln, int D) {
+    if (!ok() || layer < 0 || layer >= kMaxLayers || D < 1) return 0;
+    LnState &L = g_ln[layer];
+    int h1 = L.D, h2 = L.D;
+    if (!put_vec(&L.in_ln, &h1, in_ln, D, "in_ln") || !put_vec(&L.post_ln, &h2, post_ln, D, "post_ln")) return 0;
+    L.D = D;
+    return 1;
+}
+
+// the tail outputs of the *_full_route forms: resid_out, nrm_out [S, D], pr_out [S, E]
+static bool full_route_out(const float *dres, const float *dnrm, const float *dlog, int S, int D, int E,
+                           float *resid_out, float *nrm_out, float *pr_out) {
+    if (!sync_stream("route read-back")) return false;
+    bool r = true;
+    if (resid_out) r &= hipMemcpy(resid_out, dres, (size_t)S * D * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    if (nrm_out) r &= hipMemcpy(nrm_out, dnrm, (size_t)S * D * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    if (pr_out) r &= hipMemcpy(pr_out, dlog, (size_t)S * E * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    return r;
+}
+
+COLI_API int coli_vk_gqa_full_route(int layer, const float *resid, int D, ColiVkTensor *gq_t, ColiVkTensor *gk_t,
+                                    ColiVkTensor *gv_t, ColiVkTensor *out_t, ColiVkTensor *router, int ln_layer,
+                                    float *resid_out, float *nrm_out, float *pr_out, int S, int H, int KH, int hd,
+                                    int rot, int pos_base, int max_t, float eps, float theta, int Dout, int E) {
+    if (!ok() || !resid || S < 1 || D != Dout || !ln_ok(ln_layer, D) || !router || router->I != D || router->O != E)
+        return 0;
+    const GqaDims d = {H, KH, hd, rot, max_t, eps, theta};
+    float *dr = wbuf(W_IO_R, (size_t)S * D), *dn = wbuf(W_IO_X, (size_t)S * D), *dl = wbuf(W_IO_P, (size_t)S * E);
+    if (!dr || !dn || !dl || !h2d(dr, resid, (size_t)S * D * 4, "gqa route")) return 0;
+    for (int s = 0; s < S; s++) {
+        float *rs = dr + (size_t)s * D;
+        if (!gqa_block(layer, rs, g_ln[ln_layer].in_ln, gq_t, gk_t, gv_t, out_t, rs, true, d, pos_base + s,
+                       stream()) ||
+            !route_tail(ln_layer, rs, router, E, 0, eps, dn + (size_t)s * D, dl + (size_t)s * E, stream()))
+            return 0;
+    }
+    return full_route_out(dr, dn, dl, S, D, E, resid_out, nrm_out, pr_out) ? 1 : 0;
+}
+
+COLI_API int coli_vk_gdn_full_route(int layer, const float *x_in, const float *resid, int D, ColiVkTensor *gqkv_t,
+                                    ColiVkTensor *gz_t, const float *params, ColiVkTensor *out_t, ColiVkTensor *router,
+                                    int ln_layer, float *resid_out, float *nrm_out, float *pr_out, int KH, int KD,
+                                    int VH, int VD, int conv_dim, int conv_k, float eps, int Dout, int E) {
+    if (!ok() || !x_in || !resid || !params || D != Dout || !ln_ok(ln_layer, D) || !router || router->I != D ||
+        router->O != E)
+        return 0;
+    const GdnDims d = {KH, KD, VH, VD, conv_dim, conv_k, eps};
+    const int prs = 2 * VH + VD;
+    float *dr = wbuf(W_IO_R, D), *dx = wbuf(W_IO_X, 2 * (size_t)D), *dp = wbuf(W_IO_P, (size_t)prs + E);
+    if (!dr || !dx || !dp || !h2d(dr, resid, (size_t)D * 4, "gdn route") || !h2d(dx, x_in, (size_t)D * 4, "gdn route") ||
+        !h2d(dp, params, (size_t)prs * 4, "gdn route"))
+        return 0;
+    float *dn = dx + D, *dl = dp + prs;
+    if (!gdn_block(layer, dx, nullptr, dp, gqkv_t, gz_t, nullptr, nullptr, out_t, dr, true, d, stream()) ||
+        !route_tail(ln_layer, dr, router, E, 0, eps, dn, dl, stream()))
+        return 0;
+    return full_route_out(dr, dn, dl, 1, D, E, resid_out, nrm_out, pr_out) ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- ABI: residual stream
+// c/backend_vulkan.h:199-252.  The decode stream keeps the residual on the device across
+// layers; each *_full_route_pipe runs in_ln + block + residual add + post_ln + router, then
+// either the layer's MoE block on the device (expert table set for the layer: fused, the
+// top-k ids go to a device history read at stream_end) or the device top-k whose ids and
+// weights the caller reads back (the engine then issues the experts, c/qwen.c:934-998).
+COLI_API int coli_vk_stream_available(void) { return ok() ? 1 : 0; }
+
+static int *hist_dev() { return (int *)wbuf(W_HIST, (size_t)kMaxLayers * kMaxK); }
+
+COLI_API int coli_vk_stream_begin(const float *x, int D) {
+    if (!ok() || !x || D < 1) return 0;
+    if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4)) return 0;
+    if (!h2d(g_str.d_resid, x, (size_t)D * 4, "stream begin")) return 0;
+    g_str.D = D;
+    g_str.live = 1;
+    g_str.pending = 0;
+    g_str.fused_last = 0;
+    memset(g_str.hist_K, 0, sizeof(g_str.hist_K));
+    return 1;
+}
+
+COLI_API int coli_vk_stream_end(float *x, int D) {
+    if (!g_str.live || D != g_str.D) return 0;
+    if (!sync_stream("stream end")) return 0;
+    if (x && hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    if (g_str.pending) {
+        int *dh = hist_dev();
+        if (!dh || hipMemcpy(g_str.h_hist, dh, sizeof(g_str.h_hist), hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    }
+    g_str.live = 0;
+    return 1;
+}
+
+__global__ void vec_add_kernel(float *r, const float *y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) r[i] = r[i] + y[i];
+}
+
+COLI_API int coli_vk_stream_add(const float *y, int D) {
+    if (!g_str.live || !y || D != g_str.D) return 0;
+    if (!host_scratch((void **)&g_str.h_y, &g_str.hy_cap, (size_t)D * 4) ||
+        !scratch((void **)&g_str.d_y, &g_str.dy_cap, (size_t)D * 4))
+        return 0;
+    memcpy(g_str.h_y, y, (size_t)D * 4);
+    const hipError_t e = hipMemcpyAsync(g_str.d_y, g_str.h_y, (size_t)D * 4, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("stream add", e) ? 1 : 0;
+    hipLaunchKernelGGL(vec_add_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), g_str.d_resid, g_str.d_y, D);
+    return sync_stream("stream add") ? 1 : 0;
+}
+
+// the last non-fused route's nrm (host copy), the expert input of c/qwen.c:936-940
+COLI_API const float *coli_vk_stream_nrm(void) { return g_str.live && !g_str.fused_last ? g_str.h_nrm : nullptr; }
+
+COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
+    if (!x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
+    if (!sync_stream("copy resid")) return 0;
+    return hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+}
+
+// c/backend_vulkan.c:2692-2711
+COLI_API int coli_vk_final_norm_weight(const float *w, int D) {
+    if (!ok() || !w || D < 1) return 0;
+    if (!scratch((void **)&g_str.d_fnw, &g_str.fnw_cap, (size_t)D * 4)) return 0;
+    if (!h2d(g_str.d_fnw, w, (size_t)D * 4, "final norm weight")) return 0;
+    g_str.fn_D = D;
+    return 1;
+}
+
+// c/backend_vulkan.c:2713-2782: final RMSNorm of the device residual + lm_head + argmax,
+// only the winner is read back
+COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weights, const float *scales, int fmt,
+                                        int I, int O, int gs, float eps, int *idx, float *val) {
+    if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
+    if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
+    if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, (size_t)I * 4 + 64)) return 0;
+    float *xn = g_str.d_xn;
+    int *d_iv = (int *)(xn + I);
+    if (!rmsnorm_zc(g_str.d_resid, g_str.d_fnw, xn, I, eps, stream())) return 0;
+    TopkOut tk = {1, d_iv, (float *)(d_iv + 8)};
+    if (!gemv(*tensor, xn, nullptr, 1, stream(), &tk)) return 0;
+    int res[16];
+    if (!sync_stream("stream_norm_argmax") || hipMemcpy(res, d_iv, 64, hipMemcpyDeviceToHost) != hipSuccess)
+        return 0;
+    *idx = res[0];
+    if (val) memcpy(val, &res[8], 4);
+    return 1;
+}
+
+COLI_API void coli_vk_route_cache_stats(void) {}
+COLI_API void coli_vk_decode_prof(double decode_ms, int tokens) { (void)decode_ms, (void)tokens; }
+
+// After the block: post_ln, then the fused MoE (device expert table) or the device top-k
+// read back into idx_out / val_out (and nrm into the host cache for stream_nrm).
+static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float eps, int *idx_out, float *val_out) {
+    float *dn = wbuf(W_NRM, g_str.D), *dl = wbuf(W_LOGIT, (size_t)E + 2 * kMaxK);
+    int *dh = hist_dev();
+    if (!dn || !dl || !dh || topk < 1 || topk > kTopK || E > kMaxE) return 0;   // device top-k: K <= 8
+    if (!route_tail(ln_layer, g_str.d_resid, router, E, topk, eps, dn, nullptr, stream())) return 0;
+    if (topk <= kTopK &&
+        moe_decode(ln_layer, router, topk, dn, g_str.d_resid, 1, dh + (size_t)ln_layer * kMaxK, nullptr, stream())) {
+        g_str.fused_last = 1;
+        g_str.pending = 1;
+        g_str.hist_K[ln_layer] = topk;
+        return 1;
+    }
+    if (!ok()) return 0;
+    g_str.fused_last = 0;
+    if (!gemv(router, dn, dl, 1, stream())) return 0;
+    int *di = (int *)(dl + E);
+    float *dv = dl + E + kMaxK;
+    hipLaunchKernelGGL(route_row, dim3(1), dim3(kThreads), 0, stream(), dl, E, topk, di, dv);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("route launch", e) ? 1 : 0;
+    if (!host_scratch((void **)&g_str.h_nrm, &g_str.hnrm_cap, (size_t)(g_str.D + 2 * kMaxK) * 4)) return 0;
+    if (!sync_stream("route read-back") ||
+        hipMemcpy(g_str.h_nrm, dn, (size_t)g_str.D * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(idx_out, di, (size_t)topk * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(val_out, dv, (size_t)topk * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return 0;
+    return 1;
+}
+
+COLI_API int coli_vk_gqa_full_route_pipe(int layer, int D, ColiVkTensor *gq_t, ColiVkTensor *gk_t, ColiVkTensor *gv_t,
+                                         ColiVkTensor *out_t, ColiVkTensor *router, int ln_layer, int *idx_out,
+                                         float *val_out, int topk, int H, int KH, int hd, int rot, int pos_base,
+                                         int max_t, float eps, float theta, int Dout, int E) {
+    if (!ok() || !g_str.live || D != g_str.D || Dout != D || !ln_ok(ln_layer, D) || !router || router->I != D ||
+        router->O != E || !idx_out || !val_out)
+        return 0;
+    const GqaDims d = {H, KH, hd, rot, max_t, eps, theta};
+    if (!gqa_block(layer, g_str.d_resid, g_ln[ln_layer].in_ln, gq_t, gk_t, gv_t, out_t, g_str.d_resid, true, d,
+                   pos_base, stream()))
+        return 0;
+    return pipe_tail(ln_layer, router, E, topk, eps, idx_out, val_out);
+}
+
+COLI_API int coli_vk_gdn_full_route_pipe(int layer, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
+                                         ColiVkTensor *gba_t, ColiVkTensor *gbb_t, ColiVkTensor *out_t,
+                                         ColiVkTensor *router, int ln_layer, int *idx_out, float *val_out, int topk,
+                                         int KH, int KD, int VH, int VD, int conv_dim, int conv_k, float eps, int Dout,
+                                         int E) {
+    if (!ok() || !g_str.live || D != g_str.D || Dout != D || !ln_ok(ln_layer, D) || !router || router->I != D ||
+        router->O != E || !idx_out || !val_out)
+        return 0;
+    const GdnDims d = {KH, KD, VH, VD, conv_dim, conv_k, eps};
+    if (!gdn_block(layer, g_str.d_resid, g_ln[ln_layer].in_ln, nullptr, gqkv_t, gz_t, gba_t, gbb_t, out_t,
+                   g_str.d_resid, true, d, stream()))
+        return 0;
+    return pipe_tail(ln_layer, router, E, topk, eps, idx_out, val_out);
+}
+
+COLI_API int coli_vk_stream_moe_fused(void) { return g_str.live && g_str.fused_last ? 1 : 0; }
+COLI_API int coli_vk_stream_ix_pending(void) { return g_str.pending ? 1 : 0; }
+
+// ids of a fused layer of the last stream (valid after stream_end); returns the count
+COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
+    if (!g_str.pending || g_str.live || layer < 0 || layer >= kMaxLayers || !idx_out) return 0;
+    const int n = g_str.hist_K[layer] < K ? g_str.hist_K[layer] : K;
+    for (int k = 0; k < n; k++) idx_out[k] = g_str.h_hist[layer * kMaxK + k];
+    return n;
+}

@@ -1,5 +1,6 @@
-// moe.hip - the device-indexed top-k MoE block, the expert-group entry points, the expert
-// table and the device residual stream of the drop-in ABI.
+// moe.hip - the device-indexed top-k MoE block, the expert-group entry points (host
+// rows, and the stream form that accumulates into the device residual) and the expert
+// table of the drop-in ABI.
 //
 // Semantics (c/qwen.c:804-928, the --no-vulkan path):
 //   logits = router @ x                                  (f32 router, c/qwen.c:178-189)
@@ -813,34 +814,12 @@ static bool eg_take(float *y) {
     return true;
 }
 
-// ---------------------------------------------------------------- residual stream
-struct StreamState {
-    float *d_resid = nullptr;
-    size_t resid_cap = 0;
-    float *h_y = nullptr;         // pinned staging of stream_add
-    size_t hy_cap = 0;
-    float *d_y = nullptr;
-    size_t dy_cap = 0;
-    float *d_fnw = nullptr;       // final norm weight
-    size_t fnw_cap = 0;
-    int fn_D = 0;
-    float *d_xn = nullptr;        // normed row + argmax result
-    size_t xn_cap = 0;
-    int D = 0, live = 0;
-};
-static StreamState g_str;
-
 __global__ void silu_mul_kernel(const float *g, const float *u, float *h, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
         const float gv = g[i];
         h[i] = gv / (1.f + expf(-gv)) * u[i];
     }
-}
-
-__global__ void vec_add_kernel(float *r, const float *y, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) r[i] = r[i] + y[i];
 }
 
 static void *g_gu_d = nullptr, *g_gu_h = nullptr;
@@ -997,99 +976,77 @@ COLI_API int coli_vk_eg_table_set_shared(int layer, ColiVkTensor *g, ColiVkTenso
     return sync_stream("shared gate upload") ? 1 : 0;
 }
 
-// ---------------------------------------------------------------- ABI: residual stream
-// c/backend_vulkan.h:206-221.  The stream-routed decode (c/qwen.c:1495-1560) also needs
-// the GDN/GQA route_pipe layer blocks, which this library does not provide:
-// stream_available reports 0 so the engine keeps its host-routed flow.  The residual
-// entry points themselves work.
-COLI_API int coli_vk_stream_available(void) { return 0; }
-
-COLI_API int coli_vk_stream_begin(const float *x, int D) {
-    if (!ok() || !x || D < 1) return 0;
-    if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4)) return 0;
-    if (!sync_stream("stream begin")) return 0;
-    const hipError_t e = hipMemcpy(g_str.d_resid, x, (size_t)D * 4, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return fail("stream begin", e) ? 1 : 0;
-    g_str.D = D;
-    g_str.live = 1;
-    return 1;
+// ---------------------------------------------------------------- ABI: expert group (pipe)
+// c/backend_vulkan.h:237-240, c/backend_vulkan.c:3696-3783: the stream-routed expert group
+// of c/qwen.c:934-998.  Every row takes the last route's device nrm as input; the
+// outputs are weighted and added to the device residual in item order:
+//   resid[d] += sum_c weights[c] * y_c[d]
+// (c/shaders/moe_accumulate.comp; the engine lists the routed experts in rank order and
+// the shared expert last, as the CPU path sums them, c/qwen.c:870-877).  Stream-ordered:
+// take_pipe has nothing left to wait for.
+__global__ void eg_accumulate(float *resid, const float *y, const float *w, int n, int D) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= D) return;
+    float acc = 0.f;
+    for (int c = 0; c < n; c++) acc += w[c] * y[(size_t)c * D + d];
+    resid[d] = resid[d] + acc;
 }
 
-COLI_API int coli_vk_stream_end(float *x, int D) {
-    if (!g_str.live || D != g_str.D) return 0;
-    if (!sync_stream("stream end")) return 0;
-    if (x && hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    g_str.live = 0;
-    return 1;
-}
-
-COLI_API int coli_vk_stream_add(const float *y, int D) {
-    if (!g_str.live || !y || D != g_str.D) return 0;
-    if (!host_scratch((void **)&g_str.h_y, &g_str.hy_cap, (size_t)D * 4) ||
-        !scratch((void **)&g_str.d_y, &g_str.dy_cap, (size_t)D * 4))
-        return 0;
-    memcpy(g_str.h_y, y, (size_t)D * 4);
-    const hipError_t e = hipMemcpyAsync(g_str.d_y, g_str.h_y, (size_t)D * 4, hipMemcpyHostToDevice, stream());
-    if (e != hipSuccess) return fail("stream add", e) ? 1 : 0;
-    hipLaunchKernelGGL(vec_add_kernel, dim3((D + 255) / 256), dim3(256), 0, stream(), g_str.d_resid, g_str.d_y, D);
-    return sync_stream("stream add") ? 1 : 0;
-}
-
-COLI_API const float *coli_vk_stream_nrm(void) { return nullptr; }
-
-COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
-    if (!x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
-    if (!sync_stream("copy resid")) return 0;
-    return hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
-}
-
-// c/backend_vulkan.c:2692-2711
-COLI_API int coli_vk_final_norm_weight(const float *w, int D) {
-    if (!ok() || !w || D < 1) return 0;
-    if (!scratch((void **)&g_str.d_fnw, &g_str.fnw_cap, (size_t)D * 4)) return 0;
-    if (!sync_stream("final norm weight")) return 0;
-    if (hipMemcpy(g_str.d_fnw, w, (size_t)D * 4, hipMemcpyHostToDevice) != hipSuccess) return 0;
-    g_str.fn_D = D;
-    return 1;
-}
-
-// c/backend_vulkan.c:2713-2782: final RMSNorm of the device residual + lm_head + argmax,
-// only the winner is read back
-COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weights, const float *scales, int fmt,
-                                        int I, int O, int gs, float eps, int *idx, float *val) {
-    if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
-    if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
-    if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, (size_t)I * 4 + 64)) return 0;
-    float *xn = g_str.d_xn;
-    int *d_iv = (int *)(xn + I);
-    if (!rmsnorm_zc(g_str.d_resid, g_str.d_fnw, xn, I, eps, stream())) return 0;
-    TopkOut tk = {1, d_iv, (float *)(d_iv + 8)};
-    if (!gemv(*tensor, xn, nullptr, 1, stream(), &tk)) return 0;
-    int res[16];
-    if (!sync_stream("stream_norm_argmax") || hipMemcpy(res, d_iv, 64, hipMemcpyDeviceToHost) != hipSuccess)
-        return 0;
-    *idx = res[0];
-    if (val) memcpy(val, &res[8], 4);
-    return 1;
-}
-
-COLI_API void coli_vk_route_cache_stats(void) {}
-COLI_API void coli_vk_decode_prof(double decode_ms, int tokens) { (void)decode_ms, (void)tokens; }
-
-// stream-routed MoE pieces (c/backend_vulkan.h:229-252): they need the route_pipe blocks
 COLI_API int coli_vk_expert_group_issue_pipe(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
                                              ColiVkTensor *const *downs, const int *rows, const float *weights,
                                              int count, int D) {
-    (void)gates, (void)ups, (void)downs, (void)rows, (void)weights, (void)count, (void)D;
-    return 0;
+    float *resid = stream_resid(D);
+    const float *x = stream_nrm_dev(D);
+    if (!ok() || !resid || !x || !weights || g_grp.inflight || count < 1 || count > 64 || !gates || !ups || !downs ||
+        !rows)
+        return 0;
+    MoeGeom m;
+    if (!geom_of(gates[0], downs[0], m) || !geom_supported(m) || m.D != D) return 0;
+    int total = 0;
+    for (int c = 0; c < count; c++) {
+        MoeGeom mc, mu;
+        if (rows[c] < 1 || !geom_of(gates[c], downs[c], mc) || !same_geom(mc, m) || !ups[c] ||
+            !geom_of(ups[c], downs[c], mu) || !same_geom(mu, m))
+            return 0;
+        total += rows[c];
+    }
+    const size_t rec_b = al256((size_t)total * sizeof(ExpertRec)), xrow_b = al256((size_t)total * 4);
+    const size_t w_b = al256((size_t)total * 4), h_b = al256((size_t)total * m.I * 4), y_b = (size_t)total * m.D * 4;
+    if (!scratch(&g_grp.d_buf, &g_grp.d_cap, rec_b + xrow_b + w_b + h_b + al256(y_b))) return 0;
+    if (!host_scratch(&g_grp.h_buf, &g_grp.h_cap, rec_b + xrow_b + w_b)) return 0;
+    if (!sync_stream("expert group pipe")) return 0;   // the pinned staging may still feed a copy
+    uint8_t *hb = (uint8_t *)g_grp.h_buf;
+    ExpertRec *hrec = (ExpertRec *)hb;
+    int *hrow = (int *)(hb + rec_b);
+    float *hw = (float *)(hb + rec_b + xrow_b);
+    for (int c = 0, p = 0; c < count; c++)
+        for (int r = 0; r < rows[c]; r++, p++) {
+            hrec[p] = {gates[c]->w, ups[c]->w, downs[c]->w, gates[c]->sz, ups[c]->sz, downs[c]->sz};
+            hrow[p] = 0;
+            hw[p] = weights[c];
+        }
+    uint8_t *db = (uint8_t *)g_grp.d_buf;
+    EgItems it;
+    memset(&it, 0, sizeof(it));
+    it.rec = (const ExpertRec *)db;
+    it.xrow = (const int *)(db + rec_b);
+    it.x = x;
+    it.h = (float *)(db + rec_b + xrow_b + w_b);
+    it.y = (float *)(db + rec_b + xrow_b + w_b + h_b);
+    it.n = total;
+    it.g = m;
+    hipError_t e = hipMemcpyAsync(db, hb, rec_b + xrow_b + w_b, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("expert group pipe upload", e) ? 1 : 0;
+    if (!dispatch_shape<LaunchEg>(m, it, stream())) return 0;
+    hipLaunchKernelGGL(eg_accumulate, dim3((D + 255) / 256), dim3(256), 0, stream(), resid, it.y,
+                       (const float *)(db + rec_b + xrow_b), total, D);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail("expert group pipe", e) ? 1 : 0;
+    return 1;
 }
-COLI_API int coli_vk_expert_group_take_pipe(void) { return 0; }
-COLI_API int coli_vk_stream_moe_fused(void) { return 0; }
-COLI_API int coli_vk_stream_ix_pending(void) { return 0; }
-COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
-    (void)layer, (void)idx_out, (void)K;
-    return 0;
-}
+
+COLI_API int coli_vk_expert_group_take_pipe(void) { return ok() ? 1 : 0; }
+
 
 // ---------------------------------------------------------------- device-pointer MoE
 // The layer's whole MoE block in one launch on `stream` (NULL = the library's stream):
