@@ -189,6 +189,132 @@ def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
             "frac_bf16_dense_peak": round(flops / (ms * 1e-3) / 2.5e15, 4)}
 
 
+class DecodeStack:
+    """the 40-layer hybrid decode model with random-init weights generated on the
+    device.  Layer i is gated GQA when (i + 1) % 4 == 0 (c/qwen.c:398), GatedDeltaNet
+    otherwise; every layer has its own router and 256 + 1 experts (configs[2] shapes, all
+    resident); lm_head as configs[1].  A step is the engine's stream decode of one token
+    (c/qwen.c:1228-1290, 1392, 1437-1454): stream_begin, the layers' *_full_route_pipe
+    (block + residual add + post_ln + router + device top-8 + fused MoE), then
+    stream_norm_argmax."""
+
+    D, E, K, I, GS, NL = 2048, 256, 8, 512, 128, 40
+    H, KH, HD, ROT, MAX_T, THETA = 16, 2, 256, 64, 4096, 1e7
+    GKH, KD, VH, VD, CK = 16, 128, 32, 128, 4
+    EPS = 1e-6
+
+    def __init__(self, lib, torch, dev, seed=0xC3):
+        import numpy as np
+        D, E, I, GS = self.D, self.E, self.I, self.GS
+        self.lib, self.keep = lib, []
+        self.CD = 2 * self.GKH * self.KD + self.VH * self.VD
+        rng = np.random.default_rng(seed)
+        lib.eg_table_init(self.NL, E, D, I, GS)
+        self.layers = []
+        kvi = gi = 0
+        syn = lambda fmt, i_, o_, tag: lib.tensor_synth(fmt, i_, o_, GS if fmt == 6 else 0, (seed << 32) + tag, 0.02)
+        for L in range(self.NL):
+            tag = (L + 1) << 16
+            for e in range(E + 1):   # gate, up [I, D]; down [D, I]
+                g, u, d = syn(6, D, I, tag + 3 * e), syn(6, D, I, tag + 3 * e + 1), syn(6, I, D, tag + 3 * e + 2)
+                self.keep.append((g, u, d))
+                if e < E:
+                    lib.eg_table_set(L, e, g, u, d)
+                else:
+                    lib.eg_table_set_shared(L, g, u, d, rng.normal(0, 0.02, D).astype(np.float32))
+            router = syn(0, D, E, tag + 4000)
+            if (L + 1) % 4 == 0:
+                H, KH, HD = self.H, self.KH, self.HD
+                t = [syn(6, D, 2 * H * HD, tag + 4001), syn(6, D, KH * HD, tag + 4002),
+                     syn(6, D, KH * HD, tag + 4003), syn(6, H * HD, D, tag + 4004)]
+                lib.kv_ensure(kvi, KH * self.MAX_T, HD, HD)
+                lib.gqa_norm_weight(kvi, rng.normal(0, 0.1, HD).astype(np.float32),
+                                    rng.normal(0, 0.1, HD).astype(np.float32))
+                rows = rng.normal(0, 1, (KH * self.MAX_T, HD)).astype(np.float32)   # a full 4096-row cache
+                lib.kv_load(kvi, 0, rows, rows[::-1].copy())
+                self.layers.append(("gqa", kvi, t, router))
+                kvi += 1
+            else:
+                VH, VD = self.VH, self.VD
+                t = [syn(6, D, self.CD, tag + 4001), syn(6, D, VH * VD, tag + 4002), syn(6, D, VH, tag + 4003),
+                     syn(6, D, VH, tag + 4004), syn(6, VH * VD, D, tag + 4005)]
+                lib.gdn_setup(gi, VH, self.KD, VD, self.CK, self.CD,
+                              rng.normal(0, 0.3, self.CD * self.CK).astype(np.float32),
+                              rng.normal(0, 0.5, VH).astype(np.float32), rng.normal(0, 1, VH).astype(np.float32),
+                              (1 + rng.normal(0, 0.1, VD)).astype(np.float32))
+                self.layers.append(("gdn", gi, t, router))
+                gi += 1
+            lib.layer_norm_weight(L, rng.normal(0, 0.1, D).astype(np.float32),
+                                  rng.normal(0, 0.1, D).astype(np.float32))
+        self.lm = syn(6, D, O_VOCAB, 0xFFFF0)
+        lib.final_norm_weight(rng.normal(0, 0.1, D).astype(np.float32))
+        lib.gdn_reset()
+        self.x0 = rng.normal(0, 1, (16, D)).astype(np.float32)   # embedding rows of the tokens
+        lib.sync()
+
+    def step(self, i, pos):
+        """One token at position pos; returns the argmax id."""
+        lib = self.lib
+        lib.stream_begin(self.x0[i % len(self.x0)])
+        for n, (kind, li, t, router) in enumerate(self.layers):
+            if kind == "gqa":
+                lib.gqa_route_pipe(li, *t, router, n, self.K, self.H, self.KH, self.HD, self.ROT, pos, self.MAX_T,
+                                   self.EPS, self.THETA)
+            else:
+                lib.gdn_route_pipe(li, *t, router, n, self.K, self.GKH, self.KD, self.VH, self.VD, self.CD, self.CK,
+                                   self.EPS)
+        idx, _ = lib.stream_norm_argmax(self.lm, self.EPS)
+        lib.stream_end(self.D, read=False)
+        return idx
+
+    def alg_bytes(self):
+        """HBM bytes one decode step must move (weights as stored + state/cache traffic)."""
+        D, I, GS = self.D, self.I, self.GS
+        q6 = lambda i_, o_: o_ * i_ // 2 + o_ * (i_ // GS) * 8
+        expert = 2 * q6(D, I) + q6(I, D)
+        moe = (self.K + 1) * expert + self.E * D * 4
+        gqa = (q6(D, 2 * self.H * self.HD) + 2 * q6(D, self.KH * self.HD) + q6(self.H * self.HD, D)
+               + 2 * self.KH * self.MAX_T * self.HD * 4)
+        gdn = (q6(D, self.CD) + q6(D, self.VH * self.VD) + 2 * q6(D, self.VH) + q6(self.VH * self.VD, D)
+               + 2 * self.VH * self.KD * self.VD * 4 + 2 * self.CK * self.CD * 4)
+        n_gqa = sum(1 for l in self.layers if l[0] == "gqa")
+        return n_gqa * gqa + (self.NL - n_gqa) * gdn + self.NL * moe + alg_bytes_lmhead()
+
+
+def decode_cfg3(lib, torch, dev, steps, warmup):
+    """full 40-layer decode step, tokens/s from the host wall clock around whole
+    steps (each ends with the argmax read-back, as the engine's token loop)."""
+    t0 = time.perf_counter()
+    m = DecodeStack(lib, torch, dev)
+    setup_s = time.perf_counter() - t0
+    pos = m.MAX_T - 1
+    for i in range(warmup):
+        m.step(i, pos)
+    if lib.moe_error():
+        raise RuntimeError("MoE block reported a device-side error")
+    ext = torch.cuda.ExternalStream(lib.stream())
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ids = []
+    t1 = time.perf_counter()
+    a.record(ext)
+    for i in range(steps):
+        ids.append(m.step(i, pos))
+    b.record(ext)
+    lib.sync()
+    wall = (time.perf_counter() - t1) / steps
+    gpu_ms = a.elapsed_time(b) / steps
+    if lib.moe_error():
+        raise RuntimeError("MoE block reported a device-side error")
+    nbytes = m.alg_bytes()
+    return {"workload": "cfg3: 40-layer decode step (30 GatedDeltaNet + 10 gated GQA at pos 4095 of a 4096 KV "
+                        "cache, MoE 256+1 experts per layer, lm_head 248320 + argmax), random-init fmt6 gs128",
+            "ms_per_token": round(wall * 1e3, 3), "tok_s": round(1.0 / wall, 1),
+            "stream_ms_per_token": round(gpu_ms, 3), "alg_bytes_per_token": nbytes,
+            "achieved_GBs": round(nbytes / wall / 1e9, 1), "frac": round(nbytes / wall / 1e9 / PEAK_GBS, 4),
+            "tok_s_at_hbm_peak": round(PEAK_GBS * 1e9 / nbytes, 1), "setup_s": round(setup_s, 1),
+            "argmax_ids": sorted(set(int(i) for i in ids))[:4]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,6 +322,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the configs[2] MoE block line")
+    ap.add_argument("--no-decode", action="store_true", help="skip the configs[3] 40-layer decode step line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain 256 MiB device copies (the reference point that scales the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -264,6 +391,8 @@ def main():
     if not args.no_moe:
         layer, out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
         out["moe_prefill_cfg4"] = moe_prefill_cfg4(lib, torch, dev, layer, max(args.steps // 10, 5), 2)
+    if not args.no_decode:
+        out["decode_cfg3"] = decode_cfg3(lib, torch, dev, max(args.steps // 10, 5), 3)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

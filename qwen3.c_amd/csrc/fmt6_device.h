@@ -67,69 +67,9 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
     return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
-// Wave-wide maximum of an unsigned value by DPP (no LDS traffic), broadcast to all lanes.
+// max of an unsigned value and its DPP-moved copy (one step of a wave maximum)
 #define COLI_DPP_UMAX(v, ctrl, rmask) \
     max((v), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xF, false))
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
-    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
-    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
-    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
-    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror
-    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15
-    v = COLI_DPP_UMAX(v, 0x143, 0xC);   // row_bcast31
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
-// Wave-wide maximum of 56-bit keys (ordered value, then 0xFFFFFF - row; the launch tag is
-// common to all): two DPP passes.  Returns the key without its tag.
-__device__ __forceinline__ unsigned long long wave_key_max(unsigned long long key) {
-    const uint32_t hi = (uint32_t)(key >> 24), lo = (uint32_t)(key & 0xFFFFFFu);
-    const uint32_t mh = wave_umax(hi);
-    const uint32_t ml = wave_umax(hi == mh ? lo : 0u);
-    return ((unsigned long long)mh << 24) | ml;
-}
-
-// Selection rounds in one wave over per-lane key lists kv[N] (unsorted, tags stripped):
-// round r takes the wave's largest key, the lane holding it drops it.  out[r] = that key
-// (uniform; 0 once the lists are empty) and src[r] = its lane-major index lane * N + q.
-template <int N>
-__device__ __forceinline__ void wave_select(unsigned long long (&kv)[N], int k, unsigned long long (&out)[kTopK],
-                                            int (&src)[kTopK]) {
-    const int lane = threadIdx.x & 63;
-    unsigned long long lm = 0ull;
-    int li = 0;
-#pragma unroll
-    for (int q = 0; q < N; q++)
-        if (kv[q] > lm) {
-            lm = kv[q];
-            li = q;
-        }
-#pragma unroll
-    for (int r = 0; r < kTopK; r++) {
-        out[r] = 0ull;
-        src[r] = -1;
-        if (r >= k) continue;
-        const unsigned long long m = wave_key_max(lm);
-        const unsigned long long who = __ballot(lm == m && lm != 0ull);
-        if (!who) continue;
-        const int wl = __ffsll((long long)who) - 1;
-        out[r] = m;
-        src[r] = __builtin_amdgcn_readlane(li + lane * N, wl);
-        if (lane == wl) {
-#pragma unroll
-            for (int q = 0; q < N; q++)
-                if (q == li) kv[q] = 0ull;
-            lm = 0ull;
-            li = 0;
-#pragma unroll
-            for (int q = 0; q < N; q++)
-                if (kv[q] > lm) {
-                    lm = kv[q];
-                    li = q;
-                }
-        }
-    }
-}
 
 // (value desc, index asc): the order of c/shaders/argmax.comp:28,41 and of the host scan
 // c/qwen.c:1471-1472 (ties resolve to the lowest index).
@@ -336,19 +276,26 @@ __device__ __forceinline__ int group_exp22(const XPrep &P, int g) {
 }
 
 // ---------------------------------------------------------------- per-lane state
-// Buffer loads: out-of-range offsets read 0 (no predication), 32-bit offsets.
+// Buffer loads: out-of-range offsets read 0 (no predication), 32-bit offsets.  Weights are
+// read once per launch, so by default they are loaded nontemporal (cache policy NT: the
+// lines do not displace the activations and partials that are reused); callers whose
+// blocks re-read the same weights pass kCached.
 typedef int coli_v4i __attribute__((ext_vector_type(4)));
 typedef int coli_v2i __attribute__((ext_vector_type(2)));
 constexpr uint32_t kOOB = 0x80000000u;     // added to an offset <= 2^31: always out of range
+constexpr int kStream = 2;                 // buffer-load cache policy: nt
+constexpr int kCached = 0;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
+template <int POL = kStream>
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, POL);
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
+template <int POL = kStream>
 __device__ __forceinline__ float2 buf_load8f(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const coli_v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    const coli_v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, POL);
     return make_float2(__int_as_float(v.x), __int_as_float(v.y));
 }
 

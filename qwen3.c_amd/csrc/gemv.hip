@@ -13,8 +13,8 @@
 // plus one scale recombination per lane, about 35 VALU wave-instructions per KiB of
 // weights.
 //
-// Top-k (fused): each block reduces its rows' candidates and publishes its k best as
-// epoch-tagged 64-bit keys; the last block of the grid merges them in the same launch,
+// Top-k (fused): each wave keeps the k best of its rows in registers and publishes them as
+// epoch-tagged 64-bit keys; the last block of the grid merges the waves in the same launch,
 // polling the tags (agent-scope atomics: no device-scope fences, no second launch).
 #include "fmt6_device.h"
 
@@ -63,22 +63,14 @@ __device__ __forceinline__ unsigned long long aload64(const unsigned long long *
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-constexpr int kFusedGrid = 1024;           // largest grid of a fused top-k launch
-constexpr int kFusedWaves = kFusedGrid * 4;   // wave maxima slots (kWaves waves per block)
-constexpr int kFusedSlots = 64;             // largest per-wave candidate count
+constexpr int kFusedGrid = kThreads;       // largest grid of a fused top-k launch (one list per thread)
+constexpr int kTkBuf = 256;                // row results a wave buffers between selections
 constexpr int kFusedPollLimit = 1 << 20;
 
-// Selection works on keys without the tag: a real key keeps its 56 bits, the padding key
-// (tag only) becomes 1 so that it ranks below every real key but above "no entry" (0).
-__device__ __forceinline__ unsigned long long strip_tag(unsigned long long key) {
-    const unsigned long long v = key & 0x00FFFFFFFFFFFFFFull;
-    return v ? v : (key ? 1ull : 0ull);
-}
-
-// decode a (tag-stripped) key into (row, value); padding and "no entry" -> (INT_MAX, -inf)
+// decode a key into (row, value); the padding key (tag only) -> (INT_MAX, -inf)
 __device__ __forceinline__ void key_decode(unsigned long long key, int *row, float *val) {
     const uint32_t low = (uint32_t)(key & 0xFFFFFFu);
-    if (key <= 1ull || low == 0u) {
+    if ((key & 0x00FFFFFFFFFFFFFFull) == 0ull || low == 0u) {
         *row = INT_MAX;
         *val = -INFINITY;
         return;
@@ -89,88 +81,136 @@ __device__ __forceinline__ void key_decode(unsigned long long key, int *row, flo
     *val = __uint_as_float(u);
 }
 
-// The grid's last block: the k best keys of the launch.  Units are waves: every wave
-// published its largest key (wmax) and one key per slot it owns (cand).  The global top k
-// can only come from the k waves whose maxima rank in the top k (a key of any other wave
-// is beaten by k maxima), so: (1) each of the 4 waves selects the k best maxima of a
-// quarter of the units, (2) wave 0 selects the k best of those 4k, (3) wave 0 selects the
-// k best of the <= k x 64 keys of the chosen waves.  Keys of another launch carry another
-// tag and are polled until overwritten.
-__device__ void topk_final_block(const TopkArgs &tk, int nunits, int per_wave) {
-    __shared__ unsigned long long s_key[kWaves * kTopK];
-    __shared__ int s_unit[kWaves * kTopK];
-    constexpr int kQ = kFusedWaves / kThreads;   // 16 maxima per lane
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, k = tk.k;
-    const unsigned long long tag = (unsigned long long)(tk.epoch & 0xFFu);
-    const unsigned long long *wmax = tk.slots, *cand = tk.slots + kFusedWaves;
-    unsigned long long top[kTopK];
-    int src[kTopK];
-    bool fine = true;
-    {   // (1) wave w: units w * 1024 + lane + 64 q
-        unsigned long long kv[kQ];
-        for (int polls = 0;; polls++) {
-            bool all = true;
-#pragma unroll
-            for (int q = 0; q < kQ; q++) {
-                const int u = wave * (kFusedWaves / kWaves) + lane + 64 * q;
-                kv[q] = u < nunits ? aload64(&wmax[u]) : 0ull;
-                all &= u >= nunits || (kv[q] >> 56) == tag;
-            }
-            if (__all(all)) break;
-            if (polls > kFusedPollLimit) {
-                fine = false;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-#pragma unroll
-        for (int q = 0; q < kQ; q++) kv[q] = strip_tag(kv[q]);
-        wave_select<kQ>(kv, k, top, src);
-#pragma unroll
-        for (int r = 0; r < kTopK; r++)
-            if (lane == r) {   // src = lane' * kQ + q  ->  unit w * 1024 + lane' + 64 q
-                s_key[wave * kTopK + r] = top[r];
-                s_unit[wave * kTopK + r] =
-                    src[r] < 0 ? -1 : wave * (kFusedWaves / kWaves) + src[r] / kQ + 64 * (src[r] % kQ);
-            }
+// out[r] = the key of rank r (r < kTopK) among keys[0, n) in LDS (src[r] = its index
+// when src != NULL), by counting for each key the keys above it.  keys must be 16-byte
+// aligned and hold zeros from n up to the next multiple of 8 (zero is below every key),
+// so the counting loop reads without conditions.  Real keys are unique (the row is part
+// of the key); equal padding keys share a rank, so out is filled with the padding key
+// (and src with -1) first.  All threads of the block call; ends with __syncthreads().
+__device__ __forceinline__ void rank_keys(const unsigned long long *keys, int n, unsigned long long pad,
+                                          unsigned long long *out, int *src = nullptr) {
+    if (threadIdx.x < kTopK) {
+        out[threadIdx.x] = pad;
+        if (src) src[threadIdx.x] = -1;
     }
     __syncthreads();
-    if (wave != 0) return;
-    // (2) the k best of the 4k unit maxima (one per lane)
-    unsigned long long k1[1] = {lane < kWaves * kTopK ? s_key[lane] : 0ull};
-    wave_select<1>(k1, k, top, src);
-    int sel[kTopK];
+    const ulonglong2 *k2 = (const ulonglong2 *)keys;
+    for (int c = threadIdx.x; c < n; c += kThreads) {
+        const unsigned long long me = keys[c];
+        int r = 0;
+        for (int o = 0; o < (n + 7) / 8 * 4; o += 4) {   // 4 x 16-byte broadcast reads in flight
+            ulonglong2 q[4];
 #pragma unroll
-    for (int r = 0; r < kTopK; r++) sel[r] = src[r] < 0 ? -1 : s_unit[src[r]];
-    // (3) the keys of the chosen units: entry q of lane = slot `lane` of unit sel[q]
-    unsigned long long kc[kTopK];
+            for (int u = 0; u < 4; u++) q[u] = k2[o + u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) r += (q[u].x > me ? 1 : 0) + (q[u].y > me ? 1 : 0);
+        }
+        if (r < kTopK) {
+            out[r] = me;
+            if (src && me != pad) src[r] = c;
+        }
+    }
+    __syncthreads();
+}
+
+// Arrival counter of a fused top-k launch: two, used by launch-tag parity, after the keys.
+__device__ __forceinline__ unsigned *topk_counter(const TopkArgs &tk, uint32_t epoch) {
+    return (unsigned *)(tk.slots + (size_t)kFusedGrid * kTopK) + (epoch & 1u);
+}
+
+// Poll the kTopK tagged keys at p until all carry the launch's tag (bounded).
+__device__ __forceinline__ void poll_keys(const unsigned long long *p, unsigned long long tag,
+                                          unsigned long long (&v)[kTopK], int *bad) {
     for (int polls = 0;; polls++) {
         bool all = true;
 #pragma unroll
         for (int q = 0; q < kTopK; q++) {
-            const bool on = sel[q] >= 0 && lane < per_wave;
-            kc[q] = on ? aload64(&cand[(size_t)sel[q] * per_wave + lane]) : 0ull;
-            all &= !on || (kc[q] >> 56) == tag;
+            v[q] = aload64(p + q);
+            all &= (v[q] >> 56) == tag;
         }
-        if (__all(all)) break;
+        if (all) return;
         if (polls > kFusedPollLimit) {
-            fine = false;
-            break;
+            *bad = 1;
+            return;
         }
         __builtin_amdgcn_s_sleep(1);
     }
+}
+
+// Wave-wide maximum of 64-bit keys by DPP (high words, then low words among the lanes
+// holding the highest high word), broadcast to all lanes.
+__device__ __forceinline__ uint32_t wave_umax32(uint32_t v) {
+    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    v = COLI_DPP_UMAX(v, 0x140, 0xF);   // row_mirror
+    v = COLI_DPP_UMAX(v, 0x142, 0xA);   // row_bcast15
+    v = COLI_DPP_UMAX(v, 0x143, 0xC);   // row_bcast31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k) {
+    const uint32_t hi = (uint32_t)(k >> 32), mh = wave_umax32(hi);
+    const uint32_t ml = wave_umax32(hi == mh ? (uint32_t)k : 0u);
+    return ((unsigned long long)mh << 32) | ml;
+}
+
+// compare-exchange of 64-bit keys: a gets the larger
+__device__ __forceinline__ void cx_desc(unsigned long long &a, unsigned long long &b) {
+    const unsigned long long hi = a > b ? a : b, lo = a > b ? b : a;
+    a = hi;
+    b = lo;
+}
+
+// kTopK rounds of a wave maximum over the lanes' sorted lists L (descending, 0 = none):
+// the lane holding the winner moves to its next key.  Returns, in lane r < kTopK, the
+// wave's key of rank r (pad when the lists ran out).
+template <int N>
+__device__ __forceinline__ unsigned long long wave_rounds(unsigned long long (&L)[N], unsigned long long pad) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long out = pad;
 #pragma unroll
-    for (int q = 0; q < kTopK; q++) kc[q] = strip_tag(kc[q]);
-    wave_select<kTopK>(kc, k, top, src);
+    for (int r = 0; r < kTopK; r++) {
+        const unsigned long long m = wave_max_key(L[0]);
+        const int w = __ffsll((long long)__ballot(L[0] == m)) - 1;
+        if (lane == w) {
 #pragma unroll
-    for (int r = 0; r < kTopK; r++)
-        if (lane == r && r < k) {
-            int row;
-            float v;
-            key_decode(top[r], &row, &v);
-            tk.out_i[r] = fine ? row : -1;
-            tk.out_v[r] = v;
+            for (int q = 0; q + 1 < N; q++) L[q] = L[q + 1];
+            L[N - 1] = 0ull;
         }
+        if (lane == r) out = m > pad ? m : pad;
+    }
+    return out;
+}
+
+// The block that arrives last: the k best keys of the launch from the blocks' sorted lists
+// (cand[b * kTopK + e]; nblk <= kThreads).  Thread t polls block t's list; each wave takes
+// kTopK rounds of a wave maximum over its lanes' list heads (the lane whose head wins
+// moves to its next key), and the 4 wave lists are ranked in LDS.  Keys of another launch
+// carry another tag and are polled until overwritten.
+__device__ void topk_final_block(const TopkArgs &tk, int nblk) {
+    __shared__ __attribute__((aligned(16))) unsigned long long s_wl[kWaves * kTopK];
+    __shared__ unsigned long long s_top[kTopK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const unsigned long long tag = (unsigned long long)(tk.epoch & 0xFFu), pad = tag << 56;
+    int bad = 0;
+    unsigned long long L[kTopK];
+    if (tid < nblk) {
+        poll_keys(tk.slots + (size_t)tid * kTopK, tag, L, &bad);
+    } else {
+#pragma unroll
+        for (int q = 0; q < kTopK; q++) L[q] = 0ull;
+    }
+    const unsigned long long wl = wave_rounds<kTopK>(L, pad);   // lane r: the wave's key of rank r
+    if (lane < kTopK) s_wl[wave * kTopK + lane] = wl;
+    bad = __syncthreads_or(bad);
+    rank_keys(s_wl, kWaves * kTopK, pad, s_top);
+    if (tid < tk.k) {
+        int row;
+        float v;
+        key_decode(s_top[tid], &row, &v);
+        tk.out_i[tid] = bad ? -1 : row;
+        tk.out_v[tid] = v;
+    }
 }
 
 // The k best of nblk sorted partial lists (k entries each).  The global top k can only
@@ -259,15 +299,20 @@ __global__ void argmax_reset(unsigned long long *slots) {
 //   MODE 1: also argmax: leader lanes keep their best key, the block reduces it and
 //           atomicMax-es it into slot blockIdx % kArgSlots (no fences: atomics are
 //           coherent, and the reader runs after the kernel).
-//   MODE 2: also top-k, fused: leader lanes store one tagged key per row slot of their
-//           wave (`per_wave` slots, padding keys for slots past the end) and keep the
-//           wave's largest key, which lane 0 publishes; the grid's last block then
-//           merges (topk_final_block).
+//   MODE 2: also top-k, fused: every wave keeps the kTopK best keys of its rows (value
+//           desc, row asc) distributed over lanes 0..kTopK-1; its leader lanes park their
+//           results in LDS, and every kTkBuf rows (and at the end) the wave selects the new
+//           list from them and the old list by kTopK rounds of a wave maximum.  At the end
+//           the block ranks its waves' lists into one list that it stores as tagged keys
+//           and counts itself in; the block that arrives last merges the blocks' lists
+//           (topk_final_block).
+// The grid is persistent with few waves per CU (COLI_GEMV_BPC blocks): with U row steps
+// of every wave in flight that keeps ~8-10 MB of loads outstanding chip-wide, where HBM
+// streams best (more outstanding requests only add DRAM page conflicts).
 template <int LPR, int CU, int U, int MODE>
 __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restrict__ W, const float *__restrict__ SZ,
                                                         const float *__restrict__ x, float *__restrict__ y, int I,
-                                                        int O, int gs, int ng, int nl, int row_bytes, TopkArgs tk,
-                                                        int per_wave) {
+                                                        int O, int gs, int ng, int nl, int row_bytes, TopkArgs tk) {
     __shared__ XPrep P;
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -299,12 +344,51 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
     lane_x<CU>(P, gs, L);
 
     const uint32_t rlim = (uint32_t)((O + RPW - 1) / RPW) * RPW;   // rows the grid walks
-    int slot = 0;                    // MODE 2: next candidate slot of this wave
-    // best key of this lane's rows (MODE 2 starts at the padding key: waves without
-    // rows still publish a tagged maximum)
-    unsigned long long best = MODE == 2 ? (unsigned long long)(tk.epoch & 0xFFu) << 56 : 0ull;
-    unsigned long long *cand = tk.slots + kFusedWaves + (size_t)(blockIdx.x * kWaves + wave) * per_wave;
+    if (MODE == 2 && blockIdx.x == 0 && threadIdx.x == 0)   // the previous launch's counter is free now
+        __hip_atomic_store(topk_counter(tk, tk.epoch + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long best = 0ull;   // MODE 1: best key of this lane's rows
+    // MODE 2: the wave's k best keys (lane q < kTopK: key q); the padding key is the tag
+    // alone, below every real key of the launch
+    const unsigned long long pad = (unsigned long long)(tk.epoch & 0xFFu) << 56;
+    unsigned long long tl = pad;   // lane q < kTopK: the wave's key of rank q so far
+    // MODE 2: leader lanes buffer their row results in LDS (row r of wave step s goes to
+    // entry (s - s0) * RPW + seg); every kWin steps, and at the end, the wave turns them
+    // into keys and offers them to its list, 64 at a time.
+    constexpr int kBuf = RPW * U > kTkBuf ? RPW * U : kTkBuf;
+    constexpr int kWin = kBuf / RPW / U * U;
+    __shared__ float s_tk[MODE == 2 ? kWaves : 1][MODE == 2 ? kBuf : 1];
+    int win = 0, s0 = 0;   // steps buffered, step of entry 0 (wave uniform)
+    auto flush = [&]() {
+        // A wave's LDS operations complete in issue order, so its lanes read what its
+        // lanes wrote; only compiler reordering is fenced (a hardware fence here would wait
+        // for the weight loads in flight).  Lane l takes entries l + 64 q and the list key
+        // of rank l (lanes < kTopK), sorts its 5 keys, and kTopK wave rounds select.
+        asm volatile("" ::: "memory");
+        const int n = win * RPW;
+        constexpr int NQ = kBuf / 64 > 0 ? kBuf / 64 : 1;
+        unsigned long long L[NQ + 1];
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int e = q * 64 + lane;
+            L[q] = 0ull;
+            if (e < n) {
+                const uint32_t r = (uint32_t)((rg0 + (s0 + e / RPW) * nw) * RPW + e % RPW);
+                if (r < (uint32_t)O) L[q] = arg_key(tk.epoch, s_tk[wave][e], r);
+            }
+        }
+        L[NQ] = lane < kTopK ? tl : 0ull;
+#pragma unroll
+        for (int i = 0; i < NQ + 1; i++)   // odd-even transposition sort, descending
+#pragma unroll
+            for (int q = i & 1; q + 1 < NQ + 1; q += 2) cx_desc(L[q], L[q + 1]);
+        tl = wave_rounds<NQ + 1>(L, pad);
+        asm volatile("" ::: "memory");
+        s0 += win;
+        win = 0;
+    };
     for (uint32_t base = (uint32_t)rg0 * RPW; base < rlim; base += rstep) {
+        if constexpr (MODE == 2)
+            if (win + U > kWin) flush();
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const float part = lane_row<CU>(wq[u], sv[u], L);
@@ -314,22 +398,20 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
             sro[u] += sstep;
             lane_load<CU>(rw, rs, min(wro[u], wtot), min(sro[u], stot), L, wq[u], sv[u]);
             const float acc = seg_sum<LPR>(part);
-            if (j == LPR - 1) {
-                const bool valid = r < (uint32_t)O;
-                if (valid) y[r] = acc;
+            const bool lead = j == LPR - 1 && r < (uint32_t)O;
+            if (lead) {
+                y[r] = acc;
                 if constexpr (MODE == 1) {
-                    const unsigned long long key = valid ? arg_key(tk.epoch, acc, r) : 0ull;
-                    best = key > best ? key : best;
-                }
-                if constexpr (MODE == 2) {
-                    const unsigned long long key = valid ? arg_key(tk.epoch, acc, r) : best & (0xFFull << 56);
-                    __hip_atomic_store(&cand[slot + seg], key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long key = arg_key(tk.epoch, acc, r);
                     best = key > best ? key : best;
                 }
             }
-            if constexpr (MODE == 2) slot += RPW;
+            if constexpr (MODE == 2)
+                if (j == LPR - 1) s_tk[wave][(win + u) * RPW + seg] = acc;
         }
+        if constexpr (MODE == 2) win += U;
     }
+    if constexpr (MODE == 2) flush();
     if constexpr (MODE == 1) {
         __shared__ unsigned long long s_best[kWaves];
         best = wave_max_u64(best);
@@ -342,15 +424,20 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
             atomicMax(&tk.slots[blockIdx.x % kArgSlots], b);
         }
     }
-    if constexpr (MODE == 2) {
-        const unsigned long long pad = (unsigned long long)(tk.epoch & 0xFFu) << 56;
-        for (int e = slot + lane; e < per_wave; e += 64)   // slots this wave's rows did not reach
-            __hip_atomic_store(&cand[e], pad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        best = wave_max_u64(best);
-        if (lane == 0)
-            __hip_atomic_store(&tk.slots[blockIdx.x * kWaves + wave], best, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        if (blockIdx.x == gridDim.x - 1) topk_final_block(tk, gridDim.x * kWaves, per_wave);
+    if constexpr (MODE == 2) {   // the block's list: rank the waves' lists in LDS
+        __shared__ __attribute__((aligned(16))) unsigned long long s_wl[kWaves * kTopK];
+        __shared__ unsigned long long s_bl[kTopK];
+        __shared__ int s_last;
+        if (lane < kTopK) s_wl[wave * kTopK + lane] = tl;
+        rank_keys(s_wl, kWaves * kTopK, pad, s_bl);
+        if (threadIdx.x < kTopK)
+            __hip_atomic_store(tk.slots + (size_t)blockIdx.x * kTopK + threadIdx.x, s_bl[threadIdx.x],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0)   // arrival count of this launch (the merge still checks every tag)
+            s_last = __hip_atomic_fetch_add(topk_counter(tk, tk.epoch), 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        __syncthreads();
+        if (s_last) topk_final_block(tk, gridDim.x);
     }
 }
 
@@ -456,7 +543,15 @@ static int pow2_at_least(int n) {
     return l;
 }
 
-constexpr int kU = 4;           // row steps in flight per wave
+// Launch shape of the fmt 6 GEMV (tuned on MI355X: 287 MB lm_head stream).
+#ifndef COLI_GEMV_U
+#define COLI_GEMV_U 4           // row steps in flight per wave
+#endif
+#ifndef COLI_GEMV_BPC
+#define COLI_GEMV_BPC 1         // resident blocks per CU (4 waves each)
+#endif
+constexpr int kU = COLI_GEMV_U;
+constexpr int kGemvBlocksPerCU = COLI_GEMV_BPC;
 constexpr int kMaxBlocksPerCU = 8;
 
 // Resident blocks per CU of one kernel instantiation (queried once).
@@ -485,17 +580,11 @@ static int launch_lanes(const ColiVkTensor *t, const float *x, float *y, hipStre
     const long nrg = (t->O + rpw - 1) / rpw;
     const long work = (nrg + (long)kWaves * kU - 1) / ((long)kWaves * kU);
     auto kern = gemv6_lanes<LPR, CU, kU, MODE>;
-    int nb = grid_size(work, occupancy(kern));
+    const int per = occupancy(kern);
+    int nb = grid_size(work, per < kGemvBlocksPerCU ? per : kGemvBlocksPerCU);
     if (MODE == 2 && nb > kFusedGrid) nb = kFusedGrid;   // the fused merge reads at most kFusedGrid blocks
-    int per_wave = 0;
-    size_t lds = 0;
-    if (MODE == 2) {
-        const long nw = (long)nb * kWaves;
-        per_wave = (int)((nrg + nw * kU - 1) / (nw * kU)) * kU * rpw;   // slots one wave fills
-        if (per_wave > kFusedSlots) return 0;   // more rows than the fused merge reads per wave
-    }
-    hipLaunchKernelGGL(kern, dim3(nb), dim3(kThreads), lds, st, t->w, t->sz, x, y, t->I, t->O, t->gs, t->ng, t->nl,
-                       t->row_bytes, ta, per_wave);
+    hipLaunchKernelGGL(kern, dim3(nb), dim3(kThreads), 0, st, t->w, t->sz, x, y, t->I, t->O, t->gs, t->ng, t->nl,
+                       t->row_bytes, ta);
     return nb;
 }
 
@@ -545,7 +634,7 @@ static size_t g_logits_cap = 0;
 static void *g_slots = nullptr;    // argmax slots (kArgSlots keys)
 static size_t g_slots_cap = 0;
 static uint32_t g_epoch = 0;
-static void *g_keys = nullptr;     // fused top-k keys: wave maxima, then per-slot candidates
+static void *g_keys = nullptr;     // fused top-k: block lists [kFusedGrid][kTopK], then 2 counters
 static size_t g_keys_cap = 0;
 static uint32_t g_tk_epoch = 0;
 
@@ -603,16 +692,15 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
         return true;
     }
     if (want_k && t->layout == kLayoutLanes && t->O < (1 << 24)) {   // fused: one launch
-        const int n = kFusedWaves + kFusedGrid * kWaves * kFusedSlots;
+        const int n = kFusedGrid * kTopK + 1;   // the last word holds the two counters
         if (!scratch(&g_keys, &g_keys_cap, (size_t)n * 8)) return false;
         g_tk_epoch = (g_tk_epoch + 1) & 0xFFu;
-        if (g_tk_epoch == 0) {   // tags wrap: clear the keys so no old key carries the new tag
+        if (g_tk_epoch == 0) {   // tags wrap: clear keys and counters, no old key carries the new tag
             hipLaunchKernelGGL(keys_reset, dim3((n + 255) / 256), dim3(256), 0, st, (unsigned long long *)g_keys, n);
             g_tk_epoch = 1;
         }
         const TopkArgs ta = {tk->k, nullptr, nullptr, (unsigned long long *)g_keys, g_tk_epoch, tk->idx, tk->val};
-        if (launch_lanes_mode<2>(t, d_x, d_y, st, ta)) return true;
-        if (!ok()) return false;   // otherwise (LDS too small) fall through to separate passes
+        return launch_lanes_mode<2>(t, d_x, d_y, st, ta) != 0;
     }
     for (int s = 0; s < S; s++)
         if (!launch_one(t, d_x + (size_t)s * t->I, d_y + (size_t)s * t->O, st)) return false;

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void pf_gemm(PfGemm a) {
             const int h = 4 * g + q;   // host chunk of this lane
             const uint32_t off = arow < a.O ? (uint32_t)(arow * a.rb + ((h & 1) * a.nl + (h >> 1)) * 16) : kOOB;
 #pragma unroll
-            for (int m = 0; m < NM; m++) dst[m] = buf_load16(buf_rsrc(W[m], wtot), g < ng ? off : kOOB);
+            for (int m = 0; m < NM; m++) dst[m] = buf_load16<kCached>(buf_rsrc(W[m], wtot), g < ng ? off : kOOB);
         };
 #pragma unroll
         for (int g = 0; g < kGA; g++) a_load(g, ring[g]);
