@@ -76,9 +76,13 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
 bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t st);
 bool rmsnorm_zc(const float *d_x, const float *d_w, float *d_y, int D, float eps, hipStream_t st);
 
-// the layer's MoE block in one launch (moe.hip): out (+)= sum_k val_k y_k + shgt y_sh
+// the layer's MoE block in one launch (moe.hip): out (+)= sum_k val_k y_k + shgt y_sh.
+// d_xw != NULL: d_x is the residual and the block applies the post-attention RMSNorm
+// (weight d_xw, eps) itself.
 bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
-                int *d_idx, float *d_val, hipStream_t st);
+                int *d_idx, float *d_val, hipStream_t st, const float *d_xw = nullptr, float eps = 0.f);
+// expert table complete for the layer
+bool moe_ready(int layer);
 
 // device residual stream (layer.hip): the residual row of a live stream of width D, and
 // the last non-fused route's normed row (the expert input); NULL when not available

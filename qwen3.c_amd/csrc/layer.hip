@@ -13,13 +13,14 @@
 //   stream / route tail    c/qwen.c:1228-1290 (device residual, device top-k, MoE)
 //
 // Kernels of a layer (all stream-ordered, no host synchronisation inside a layer):
-//   proj_gemv   fmt 6 lanes-layout GEMV over up to 4 tensors that share the input row,
-//               with the input transform fused into the x prologue (in_ln RMSNorm of the
-//               residual, or the GDN per-head gated RMSNorm), the residual add fused into
-//               the store, and (GDN out_proj) the conv-ring shift as a side job.
-//   gdn_core    one block per (v-head, 16-column slice) of the recurrent state: a/b dots,
-//               conv + SiLU of the channels it needs, l2norm, then the delta rule on its
-//               columns.  The state is kept transposed ([VH][VD][KD]) so that a column is
+//   proj_gemv   fmt 6 lanes-layout GEMV over up to 4 tensors that share the input row
+//               (qkv | z | a | b of GDN, q | k | v of GQA), with the input transform fused
+//               into the x prologue (in_ln RMSNorm of the residual, or the GDN per-head
+//               gated RMSNorm) and the residual add fused into the store.
+//   gdn_core    one block per (v-head, 16-column slice) of the recurrent state: decay/beta
+//               from the a/b dots, conv + SiLU of the channels it needs (the conv ring is
+//               circular: the owner of a channel stores this token's input in place), l2norm,
+//               then the delta rule on its columns.  The state is kept transposed ([VH][VD][KD]) so that a column is
 //               contiguous: each wave updates a column with one coalesced load and two
 //               DPP reductions, and blocks own disjoint columns (in-place, race free).
 //   attn_part   one block per (kv head, 32-position chunk): normalises and rotates the
@@ -84,9 +85,6 @@ struct ProjArgs {
     int VD;
     float eps;
     int add;           // 1: y[r] += acc (residual add), 0: y[r] = acc
-    float *ring;       // conv ring [K][CD] to shift (slot K-1 := ring_new), or NULL
-    const float *ring_new;
-    int ring_K, ring_CD;
 };
 
 // XF_NORM: x[i] * r * (1 + w[i]), r = 1/sqrt(mean(x^2) + eps) over the I columns
@@ -200,13 +198,6 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
             }
         }
     }
-    if (a.ring) {   // ring[j] = ring[j+1] (j < K-1), ring[K-1] = new (c/qwen.c:697-700)
-        const int CD = a.ring_CD, K = a.ring_K;
-        for (int ch = blockIdx.x * kThreads + threadIdx.x; ch < CD; ch += gridDim.x * kThreads) {
-            for (int t = 0; t + 1 < K; t++) a.ring[(size_t)t * CD + ch] = a.ring[(size_t)(t + 1) * CD + ch];
-            a.ring[(size_t)(K - 1) * CD + ch] = a.ring_new[ch];
-        }
-    }
 }
 
 // ---------------------------------------------------------------- GatedDeltaNet core
@@ -239,11 +230,14 @@ __device__ __forceinline__ float rowmat_w(const RowMat &m, int r, int i) {
 
 struct GdnArgs {
     const float *qkv;      // [CD] projection of this token (before the conv)
-    const float *ring;     // [K][CD] previous inputs, slot K-1 newest
+    float *ring;           // [K][CD] circular: the previous K - 1 inputs at slots head + 1 ..
+                           // head + K - 1 (mod K), oldest first; this token's input goes to head
+    int head;
     const float *convw;    // [CD][K]
     float *S;              // [VH][VD][KD]
     float *y;              // [VH * VD] recurrence output (before the gated norm)
     const float *params;   // host-packed [decay(VH) | beta(VH) | ...], or NULL: from a/b
+    const float *ab;       // a/b dots [a(VH) | b(VH)] from the projection launch, or NULL
     const float *xin;      // a/b input: the normed row, or NULL: in_ln(resid) here
     const float *resid, *in_ln;
     RowMat a, b;
@@ -276,6 +270,11 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
     if (g.params) {
         decay = g.params[h];
         beta = g.params[g.VH + h];
+    } else if (g.ab) {   // fmt 6 a/b: projected with qkv/z in one launch
+        const float sp_in = g.ab[h] + g.dtb[h];
+        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
+        decay = expf(-expf(g.alog[h]) * sp);
+        beta = 1.f / (1.f + expf(-g.ab[g.VH + h]));
     } else {
         float r = 0.f;
         if (!g.xin) {
@@ -311,18 +310,27 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
     }
 
     // conv1d + SiLU of the channels this block reads (c/qwen.c:697-707): q and k of the
-    // source k-head, v of the block's columns
+    // source k-head, v of the block's columns; the block that owns a channel (the group's
+    // first v-head, first column slice, for q and k; every block for its own v columns)
+    // stores this token's input at the ring head, a slot no block reads for this token
+    const bool owns_qk = h % (g.VH / g.KH) == 0 && c0 == 0;
     for (int t = tid; t < 2 * KD + kGdnCols; t += kThreads) {
         const int ch = t < KD ? src * KD + t : t < 2 * KD ? key_dim + src * KD + (t - KD)
                                                           : 2 * key_dim + h * g.VD + c0 + (t - 2 * KD);
         const float *w = g.convw + (size_t)ch * g.K;
+        const float xn = g.qkv[ch];
         float acc = 0.f;
-        for (int q = 0; q + 1 < g.K; q++) acc += w[q] * g.ring[(size_t)(q + 1) * g.CD + ch];
-        acc += w[g.K - 1] * g.qkv[ch];
+        for (int q = 0; q + 1 < g.K; q++) {
+            int slot = g.head + 1 + q;
+            if (slot >= g.K) slot -= g.K;
+            acc += w[q] * g.ring[(size_t)slot * g.CD + ch];
+        }
+        acc += w[g.K - 1] * xn;
         const float v = silu_f(acc);
         if (t < KD) s_q[t] = v;
         else if (t < 2 * KD) s_k[t - KD] = v;
         else s_v[t - 2 * KD] = v;
+        if (t >= 2 * KD || owns_qk) g.ring[(size_t)g.head * g.CD + ch] = xn;
     }
     __syncthreads();
     // l2norm of q and k (c/qwen.c:713-721)
@@ -378,6 +386,7 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
 constexpr int kAttT = 32;       // positions per chunk (block)
 constexpr int kAttMaxG = 16;    // query heads per kv head
 constexpr int kAttMaxHD = 512;
+constexpr int kAttMaxHR = 64;   // rotary pairs (rot / 2)
 
 struct AttnArgs {
     const float *q;      // [H][2 hd]: q | gate per head (projection output)
@@ -387,13 +396,13 @@ struct AttnArgs {
     float *part;         // [KH][nsplit][G][hd + 2]: ctx, then m, l
     float *ctx;          // [H * hd] merged, gated
     int H, KH, hd, rot, pos, max_t, nsplit;
-    float eps, theta, scale;
+    float eps, scale;
+    float cs[kAttMaxHR], sn[kAttMaxHR];   // rotation at pos (host: c/qwen.c:570-579 in double)
 };
 
 // zero-centred RMSNorm over hd, then partial RoPE at pos (c/qwen.c:326-330, :570-579), of
 // the row src into the LDS row x and, if gdst != NULL, into gdst.  One wave; every output
 // element is written by the lane that computes it from src (no cross-lane LDS reads).
-// The rotation angles are computed in double and rounded to float.
 __device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
     const int lane = threadIdx.x & 63, hr = a.rot / 2;
     double ss = 0;
@@ -409,9 +418,7 @@ __device__ void norm_rope_row(float *x, float *gdst, const float *src, const flo
         if (gdst) gdst[d] = v;
     }
     for (int jj = lane; jj < hr; jj += 64) {
-        const float inv = (float)pow((double)a.theta, (double)(-2.0f * jj / a.rot));
-        const float ang = (float)a.pos * inv;
-        const float cs = (float)cos((double)ang), sn = (float)sin((double)ang);
+        const float cs = a.cs[jj], sn = a.sn[jj];
         const float lo = src[jj] * r * (1.f + w[jj]), hi = src[jj + hr] * r * (1.f + w[jj + hr]);
         const float o0 = lo * cs - hi * sn, o1 = hi * cs + lo * sn;
         x[jj] = o0;
@@ -423,8 +430,14 @@ __device__ void norm_rope_row(float *x, float *gdst, const float *src, const flo
     }
 }
 
+// One block per (kv head, chunk of kAttT positions).  Every K and V element the block
+// needs is loaded at the start (one memory round trip), then the q rows of the group (and
+// the new key row, in the chunk holding pos) are normed and rotated, scores computed,
+// the chunk softmax taken and P.V accumulated.
 template <int DPL>
 __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
+    constexpr int kSteps = kAttT / (kWaves * 4);   // position steps per wave (4 positions each)
+    constexpr int kVPer = kAttMaxHD / kThreads;    // head dims per thread in P.V
     __shared__ __attribute__((aligned(16))) float s_q[kAttMaxG][kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_k[kAttMaxHD];
     __shared__ float s_p[kAttMaxG][kAttT];
@@ -432,8 +445,36 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KH, hd = a.hd;
     const int kh = blockIdx.x / a.nsplit, sp = blockIdx.x % a.nsplit;
-    const int t0 = sp * kAttT, t1 = min(t0 + kAttT, a.pos + 1);
+    const int t0 = sp * kAttT, t1 = min(t0 + kAttT, a.pos + 1), n = t1 - t0;
     const bool owns_pos = a.pos >= t0 && a.pos < t1;
+    // K rows of the score steps (16 lanes per position, DPL dims each) and V columns of
+    // P.V (thread d: dims d + kThreads * i), all in flight together
+    const int pl = lane >> 4, part = lane & 15;
+    float kv[kSteps][DPL];
+#pragma unroll
+    for (int st = 0; st < kSteps; st++) {
+        const int t = t0 + (st * kWaves + wave) * 4 + pl;
+        const bool ld = t < t1 && t != a.pos;
+        const float *kr = a.Kc + ((size_t)kh * a.max_t + (ld ? t : t0)) * hd + part * DPL;
+#pragma unroll
+        for (int e = 0; e < DPL; e += 4) {
+            const float4 v4 = ld ? *(const float4 *)(kr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            kv[st][e] = v4.x;
+            kv[st][e + 1] = v4.y;
+            kv[st][e + 2] = v4.z;
+            kv[st][e + 3] = v4.w;
+        }
+    }
+    float vv[kAttT][kVPer];
+#pragma unroll
+    for (int t = 0; t < kAttT; t++)
+#pragma unroll
+        for (int i = 0; i < kVPer; i++) {
+            const int d = tid + i * kThreads, tt = t0 + t;
+            vv[t][i] = 0.f;
+            if (t < n && d < hd)
+                vv[t][i] = tt == a.pos ? a.v[(size_t)kh * hd + d] : a.Vc[((size_t)kh * a.max_t + tt) * hd + d];
+        }
     for (int gg = wave; gg < G; gg += kWaves)
         norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
     if (owns_pos && wave == kWaves - 1) {   // the new key row and value row (c/qwen.c:605-614)
@@ -443,30 +484,22 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     }
     __syncthreads();
     // scores: 16 lanes per position, 4 positions per wave step
-    const int pl = lane >> 4, part = lane & 15;
-    for (int tb = t0 + wave * 4; tb < t1; tb += kWaves * 4) {
-        const int t = tb + pl;
-        const bool valid = t < t1;
-        const float *kr = (valid && t == a.pos) ? s_k : a.Kc + ((size_t)kh * a.max_t + (valid ? t : t0)) * hd;
-        float kv[DPL];
 #pragma unroll
-        for (int e = 0; e < DPL; e += 4) {
-            const float4 v4 = *(const float4 *)(kr + part * DPL + e);
-            kv[e] = v4.x;
-            kv[e + 1] = v4.y;
-            kv[e + 2] = v4.z;
-            kv[e + 3] = v4.w;
-        }
+    for (int st = 0; st < kSteps; st++) {
+        const int t = t0 + (st * kWaves + wave) * 4 + pl;
+        const bool valid = t < t1;
+        if (valid && t == a.pos)
+#pragma unroll
+            for (int e = 0; e < DPL; e++) kv[st][e] = s_k[part * DPL + e];
         for (int gg = 0; gg < G; gg++) {
             float s = 0.f;
 #pragma unroll
-            for (int e = 0; e < DPL; e++) s = fmaf(s_q[gg][part * DPL + e], kv[e], s);
+            for (int e = 0; e < DPL; e++) s = fmaf(s_q[gg][part * DPL + e], kv[st][e], s);
             s = seg_sum<16>(s);
             if (part == 15 && valid) s_p[gg][t - t0] = s * a.scale;
         }
     }
     __syncthreads();
-    const int n = t1 - t0;
     if (tid < G) {   // chunk max and sum of exp per head
         float m = -INFINITY;
         for (int t = 0; t < n; t++) m = fmaxf(m, s_p[tid][t]);
@@ -482,20 +515,22 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     __syncthreads();
     // P.V: thread d of the head dims, all G heads
     float *pb = a.part + ((size_t)kh * a.nsplit + sp) * G * (hd + 2);
-    for (int d = tid; d < hd; d += kThreads) {
+#pragma unroll
+    for (int i = 0; i < kVPer; i++) {   // guarded bodies, no breaks: the loops unroll fully
+        const int d = tid + i * kThreads;
         float acc[kAttMaxG];
 #pragma unroll
         for (int gg = 0; gg < kAttMaxG; gg++) acc[gg] = 0.f;
-        for (int t = 0; t < n; t++) {
-            const int tt = t0 + t;
-            const float v = tt == a.pos ? a.v[(size_t)kh * hd + d] : a.Vc[((size_t)kh * a.max_t + tt) * hd + d];
+#pragma unroll
+        for (int t = 0; t < kAttT; t++)
+            if (t < n)
+#pragma unroll
+                for (int gg = 0; gg < kAttMaxG; gg++)
+                    if (gg < G) acc[gg] = fmaf(s_p[gg][t], vv[t][i], acc[gg]);
+        if (d < hd)
 #pragma unroll
             for (int gg = 0; gg < kAttMaxG; gg++)
-                if (gg < G) acc[gg] = fmaf(s_p[gg][t], v, acc[gg]);
-        }
-#pragma unroll
-        for (int gg = 0; gg < kAttMaxG; gg++)
-            if (gg < G) pb[(size_t)gg * (hd + 2) + d] = acc[gg];
+                if (gg < G) pb[(size_t)gg * (hd + 2) + d] = acc[gg];
     }
     if (tid < G) {
         pb[(size_t)tid * (hd + 2) + hd] = s_m[tid];
@@ -505,9 +540,13 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
 
 constexpr int kAttMaxSplit = 4096;
 
+// One block per query head: merges the chunks (max, rescaled sums) and applies the
+// sigmoid gate.  Wave w takes chunks w, w + 4, ...; lane l takes dims 4 l .. 4 l + 3 (and
+// + 256 for hd = 512); the 4 wave partials are summed in LDS in wave order.
 __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
     __shared__ float s_w[kAttMaxSplit];
     __shared__ float s_red[kWaves];
+    __shared__ __attribute__((aligned(16))) float s_acc[kWaves][kAttMaxHD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x, G = a.H / a.KH, kh = h / G, gg = h % G, hd = a.hd;
     const int ns = (a.pos + 1 + kAttT - 1) / kAttT;
@@ -533,10 +572,36 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
     l = 0.f;
     for (int w = 0; w < kWaves; w++) l += s_red[w];
     const float inv = 1.f / l;
+    for (int d0 = lane * 4; d0 < hd; d0 += 256) {   // hd % 64 == 0: whole float4s
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        int s = wave;
+        for (; s + 3 * kWaves < ns; s += 4 * kWaves) {   // 4 chunks' loads in flight
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = *(const float4 *)(pb + (size_t)(s + u * kWaves) * stride + d0);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float w = s_w[s + u * kWaves];
+                acc.x = fmaf(v[u].x, w, acc.x);
+                acc.y = fmaf(v[u].y, w, acc.y);
+                acc.z = fmaf(v[u].z, w, acc.z);
+                acc.w = fmaf(v[u].w, w, acc.w);
+            }
+        }
+        for (; s < ns; s += kWaves) {
+            const float4 v = *(const float4 *)(pb + (size_t)s * stride + d0);
+            const float w = s_w[s];
+            acc.x = fmaf(v.x, w, acc.x);
+            acc.y = fmaf(v.y, w, acc.y);
+            acc.z = fmaf(v.z, w, acc.z);
+            acc.w = fmaf(v.w, w, acc.w);
+        }
+        *(float4 *)&s_acc[wave][d0] = acc;
+    }
+    __syncthreads();
     const float *gate = a.q + (size_t)h * 2 * hd + hd;
     for (int d = tid; d < hd; d += kThreads) {
-        float acc = 0.f;
-        for (int s = 0; s < ns; s++) acc = fmaf(pb[s * stride + d], s_w[s], acc);
+        const float acc = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
         a.ctx[(size_t)h * hd + d] = acc * inv * (1.f / (1.f + expf(-gate[d])));
     }
 }
@@ -578,7 +643,8 @@ struct QkNorm {
 struct GdnState {
     float *S = nullptr;      // [VH][VD][KD] (transposed from the reference's [VH][KD][VD])
     int VH = 0, KD = 0, VD = 0;
-    float *ring = nullptr;   // [K][CD], slot K-1 newest
+    float *ring = nullptr;   // [K][CD] circular (see GdnArgs)
+    int head = 0;
     float *convw = nullptr;  // [CD][K]
     int K = 0, CD = 0, convw_set = 0;
     float *alog = nullptr, *dtb = nullptr, *gnorm = nullptr;
@@ -622,7 +688,7 @@ static bool put_vec(float **d, int *have, const float *h, int n, const char *who
 
 // ---------------------------------------------------------------- work buffers
 enum {
-    W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
+    W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_AB, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
     W_HIST, W_COUNT
 };
 struct WorkBuf {
@@ -652,10 +718,6 @@ static bool launch_proj(ProjArgs &a, hipStream_t st) {
     long nb = ((long)a.ngroups + kWaves * kProjU - 1) / (kWaves * kProjU);
     const long cap = (long)n_cu() * per;
     if (nb > cap) nb = cap;
-    if (a.ring) {   // the ring shift wants a few blocks even when the projection is small
-        const long want = ((long)a.ring_CD + kThreads - 1) / kThreads;
-        if (nb < want) nb = want < cap ? want : cap;
-    }
     if (nb < 1) nb = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
     const hipError_t e = hipGetLastError();
@@ -684,7 +746,7 @@ static int pow2_up(int n) {
 
 // y_s = W_s x' for the segments (same I, gs: they share the input row x' = XF(x)).
 static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *xw, const float *z, int VD, float eps,
-                 bool add, float *ring, const float *ring_new, int ring_K, int ring_CD, hipStream_t st) {
+                 bool add, hipStream_t st) {
     if (n < 1 || n > kMaxSeg) return refuse("projection segment count");
     const ColiVkTensor *t0 = segs[0].t;
     for (int i = 0; i < n; i++) {
@@ -715,10 +777,6 @@ static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *
     a.VD = VD;
     a.eps = eps;
     a.add = add ? 1 : 0;
-    a.ring = ring;
-    a.ring_new = ring_new;
-    a.ring_K = ring_K;
-    a.ring_CD = ring_CD;
     if (xf == XF_GATED) {
         const int wph = VD / 8;
         if (VD % 8 || wph < 1 || wph > 64 || (wph & (wph - 1)) || a.I % VD) return refuse("gated norm head size");
@@ -749,7 +807,7 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     if (!kv.K || kv.kd != hd || kv.vd != hd || (long)KH * d.max_t > kv.rows) return refuse("KV mirror not ensured");
     if (!qk.qn || qk.hd != hd) return refuse("q/k norm weights not set");
     if (H < 1 || KH < 1 || H % KH || H / KH > kAttMaxG || hd % 64 || hd > kAttMaxHD || d.rot < 2 || d.rot > hd ||
-        d.rot % 2 || pos < 0 || pos >= d.max_t)
+        d.rot % 2 || d.rot / 2 > kAttMaxHR || pos < 0 || pos >= d.max_t)
         return refuse("attention shape");
     if (!tq || !tk || !tv || !to || tq->O != 2 * H * hd || tk->O != KH * hd || tv->O != KH * hd || to->I != H * hd)
         return refuse("attention projection shapes");
@@ -759,7 +817,7 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     float *ctx = wbuf(W_CTX, (size_t)H * hd), *part = wbuf(W_PART, (size_t)KH * nsplit * G * (hd + 2));
     if (!q || !k || !v || !ctx || !part) return false;
     const SegIn in[3] = {{tq, q}, {tk, k}, {tv, v}};
-    if (!proj(in, 3, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, nullptr, nullptr, 0, 0, st))
+    if (!proj(in, 3, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, st))
         return false;
     AttnArgs a;
     a.q = q;
@@ -779,8 +837,13 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     a.max_t = d.max_t;
     a.nsplit = nsplit;
     a.eps = d.eps;
-    a.theta = d.theta;
     a.scale = 1.f / sqrtf((float)hd);
+    for (int j = 0; j < d.rot / 2; j++) {   // c/qwen.c:572-574, in double, rounded to float
+        const float inv = (float)pow((double)d.theta, (double)(-2.0f * j / d.rot));
+        const float ang = (float)pos * inv;
+        a.cs[j] = (float)cos((double)ang);
+        a.sn[j] = (float)sin((double)ang);
+    }
     switch (hd / 16) {
     case 4: hipLaunchKernelGGL(attn_part<4>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
     case 8: hipLaunchKernelGGL(attn_part<8>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
@@ -792,7 +855,7 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("attention launch", e);
     const SegIn o[1] = {{to, dst}};
-    return proj(o, 1, XF_PLAIN, ctx, nullptr, nullptr, 0, d.eps, add, nullptr, nullptr, 0, 0, st);
+    return proj(o, 1, XF_PLAIN, ctx, nullptr, nullptr, 0, d.eps, add, st);
 }
 
 // ---------------------------------------------------------------- GDN block
@@ -836,14 +899,23 @@ static bool gdn_block(int gi, const float *src, const float *ln, const float *pa
             return refuse("GDN a/b projections");
     }
     float *qkv = wbuf(W_QKV, d.CD), *z = wbuf(W_Z, (size_t)d.VH * d.VD), *y = wbuf(W_Y, (size_t)d.VH * d.VD);
-    if (!qkv || !z || !y) return false;
-    const SegIn in[2] = {{tqkv, qkv}, {tz, z}};
-    if (!proj(in, 2, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, nullptr, nullptr, 0, 0, st))
+    float *ab = wbuf(W_AB, (size_t)2 * d.VH);
+    if (!qkv || !z || !y || !ab) return false;
+    // fmt 6 a/b with the qkv geometry: two more segments of the same launch
+    const auto lanes_like = [&](const ColiVkTensor *t) {
+        return t && t->fmt == 6 && t->layout == kLayoutLanes && t->I == tqkv->I && t->gs == tqkv->gs &&
+               t->nl == tqkv->nl && t->row_bytes == tqkv->row_bytes;
+    };
+    const bool ab_proj = !params && lanes_like(ta) && lanes_like(tb) && lanes_like(tz) && tqkv->fmt == 6;
+    const SegIn in[4] = {{tqkv, qkv}, {tz, z}, {ta, ab}, {tb, ab + d.VH}};
+    if (!proj(in, ab_proj ? 4 : 2, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, st))
         return false;
     GdnArgs g;
     memset(&g, 0, sizeof(g));
     g.qkv = qkv;
     g.ring = G.ring;
+    g.head = G.head;
+    g.ab = ab_proj ? ab : nullptr;
     g.convw = G.convw;
     g.S = G.S;
     g.y = y;
@@ -874,9 +946,10 @@ static bool gdn_block(int gi, const float *src, const float *ln, const float *pa
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("GDN launch", e);
+    G.head = G.head + 1 == G.K ? 0 : G.head + 1;   // the ring advanced by this token
     const float *gnorm = params ? params + 2 * d.VH : G.gnorm;
     const SegIn o[1] = {{tout, dst}};
-    return proj(o, 1, XF_GATED, y, gnorm, z, d.VD, d.eps, add, G.ring, qkv, d.K, d.CD, st);
+    return proj(o, 1, XF_GATED, y, gnorm, z, d.VD, d.eps, add, st);
 }
 
 // ---------------------------------------------------------------- residual stream state
@@ -1064,6 +1137,7 @@ COLI_API void coli_vk_gdn_reset(void) {
         GdnState &G = g_gdn[i];
         if (G.S) (void)hipMemsetAsync(G.S, 0, (size_t)G.VH * G.KD * G.VD * 4, stream());
         if (G.ring) (void)hipMemsetAsync(G.ring, 0, (size_t)G.K * G.CD * 4, stream());
+        G.head = 0;
     }
     (void)sync_stream("gdn reset");
 }
@@ -1081,6 +1155,7 @@ COLI_API int coli_vk_gdn_conv_ensure(int layer, int conv_k, int conv_dim) {
     }
     G.K = conv_k;
     G.CD = conv_dim;
+    G.head = 0;
     const hipError_t e = hipMemsetAsync(G.ring, 0, n * 4, stream());
     if (e != hipSuccess) return fail("gdn conv ring", e) ? 1 : 0;
     return sync_stream("gdn conv ring") ? 1 : 0;
@@ -1165,8 +1240,12 @@ COLI_API int coli_hip_gdn_state_read(int layer, float *ring, float *S) {
     const size_t n = (size_t)G.VH * G.KD * G.VD;
     float *t = (float *)malloc(n * 4);
     if (!t) return 0;
-    int r = hipMemcpy(ring, G.ring, (size_t)G.K * G.CD * 4, hipMemcpyDeviceToHost) == hipSuccess &&
-            hipMemcpy(t, G.S, n * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    int r = hipMemcpy(t, G.S, n * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    for (int j = 0; r && j < G.K; j++) {   // logical slot j (0 = oldest) is physical head + j
+        const int slot = (G.head + j) % G.K;
+        r = hipMemcpy(ring + (size_t)j * G.CD, G.ring + (size_t)slot * G.CD, (size_t)G.CD * 4,
+                      hipMemcpyDeviceToHost) == hipSuccess;
+    }
     for (int h = 0; r && h < G.VH; h++)   // device [h][vd][kd] -> host [h][kd][vd]
         for (int kd = 0; kd < G.KD; kd++)
             for (int vd = 0; vd < G.VD; vd++)
@@ -1336,15 +1415,16 @@ static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float 
     float *dn = wbuf(W_NRM, g_str.D), *dl = wbuf(W_LOGIT, (size_t)E + 2 * kMaxK);
     int *dh = hist_dev();
     if (!dn || !dl || !dh || topk < 1 || topk > kTopK || E > kMaxE) return 0;   // device top-k: K <= 8
-    if (!route_tail(ln_layer, g_str.d_resid, router, E, topk, eps, dn, nullptr, stream())) return 0;
-    if (topk <= kTopK &&
-        moe_decode(ln_layer, router, topk, dn, g_str.d_resid, 1, dh + (size_t)ln_layer * kMaxK, nullptr, stream())) {
+    // fused: the MoE block norms the residual itself (post_ln) and adds into it
+    if (moe_ready(ln_layer) && moe_decode(ln_layer, router, topk, g_str.d_resid, g_str.d_resid, 1,
+                                          dh + (size_t)ln_layer * kMaxK, nullptr, stream(), g_ln[ln_layer].post_ln, eps)) {
         g_str.fused_last = 1;
         g_str.pending = 1;
         g_str.hist_K[ln_layer] = topk;
         return 1;
     }
     if (!ok()) return 0;
+    if (!route_tail(ln_layer, g_str.d_resid, router, E, topk, eps, dn, nullptr, stream())) return 0;
     g_str.fused_last = 0;
     if (!gemv(router, dn, dl, 1, stream())) return 0;
     int *di = (int *)(dl + E);

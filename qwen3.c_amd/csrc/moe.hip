@@ -40,7 +40,10 @@ constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1]
 constexpr int kCounterStride = 64;        // u32 counters 256 bytes apart (one per line)
 
 struct MoeArgs {
-    const float *x;                       // [D] expert input (post-attention RMSNorm)
+    const float *x;                       // [D] expert input (post-attention RMSNorm), or the
+                                          // residual when xw != NULL
+    const float *xw;                      // post-attention norm weight [D] (zero-centred), or NULL
+    float eps;
     const uint8_t *rw;                    // router rows (fmt 0 f32 or fmt 1 int8)
     const float *rs;                      // fmt 1: per-row scales
     int rfmt, rrb, E;
@@ -270,10 +273,26 @@ __device__ __forceinline__ float4 int8x4(uint32_t q) {
     return make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16), (float)(int8_t)(q >> 24));
 }
 
-__device__ void tile_router(const MoeArgs &a, int r0) {
+// rms factor of the residual x (c/qwen.c:326-330: double sum of squares); all threads
+// call, every thread gets the factor
+__device__ float resid_rms(const MoeArgs &a, double *s_red) {
+    const int D = a.g.D;
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += kThreads) ss += (double)a.x[i] * a.x[i];
+    ss = wave_sum_dpp(ss);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double t = 0;
+    for (int w = 0; w < kWaves; w++) t += s_red[w];
+    return 1.f / sqrtf((float)(t / D) + a.eps);
+}
+
+__device__ void tile_router(const MoeArgs &a, int r0, double *s_red) {
     constexpr int kRC = 8;   // float4 per lane and pass: 2048 columns
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.g.D;
     const int r = r0 + wave;
+    const float rr = a.xw ? resid_rms(a, s_red) : 1.f;   // x' = x r (1 + w) (c/qwen.c:329)
     if (r > a.E) return;
     const bool gate = r == a.E;
     const uint8_t *row = gate ? (const uint8_t *)a.sh_gate : a.rw + (size_t)r * a.rrb;
@@ -286,6 +305,11 @@ __device__ void tile_router(const MoeArgs &a, int r0) {
             const int col = c0 + (lane + c * 64) * 4;
             const bool in = col < D;
             xv[c] = in ? *(const float4 *)(a.x + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.xw && in) {
+                const float4 w4 = *(const float4 *)(a.xw + col);
+                xv[c] = make_float4(xv[c].x * rr * (1.f + w4.x), xv[c].y * rr * (1.f + w4.y),
+                                    xv[c].z * rr * (1.f + w4.z), xv[c].w * rr * (1.f + w4.w));
+            }
             w[c] = !in ? make_float4(0.f, 0.f, 0.f, 0.f)
                        : f32 ? *(const float4 *)(row + (size_t)col * 4) : int8x4(*(const uint32_t *)(row + col));
         }
@@ -463,6 +487,7 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     __shared__ int s_e[1];
     __shared__ ExpertRec s_rec[1];
     __shared__ float s_w[kMaxSlots];
+    __shared__ double s_red[kWaves];
     const MoeGeom &g = a.g;
     const int K = a.K;
     // tile list: R router rows | Gs shared gate/up | Dsh shared down | T route |
@@ -482,11 +507,24 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
         const bool gtile = (t >= tGs && t < tDsh) || (t >= tGk && t < tDk);
         if (gtile && !s_xvalid) {   // x digits for the G tiles of this block
             XRegs xr;
-            prep_load(a.x, g.D, g.nlG * kLaneChunks * 32, xr);
-            prep_x(xr, g.gs, g.nlG * kLaneChunks * 32, S.x);
+            const int ncols = g.nlG * kLaneChunks * 32;
+            prep_load(a.x, g.D, ncols, xr);
+            if (a.xw) {   // post-attention norm of the residual (c/qwen.c:326-330)
+                const float rr = resid_rms(a, s_red);
+#pragma unroll
+                for (int k = 0; k < XRegs::kWords; k++) {
+                    const int w = threadIdx.x + k * kThreads;
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        const int i = w * 8 + c;
+                        if (w < ncols / 8 && i < g.D) xr.v[k][c] = xr.v[k][c] * rr * (1.f + a.xw[i]);
+                    }
+                }
+            }
+            prep_x(xr, g.gs, ncols, S.x);
             if (threadIdx.x == 0) s_xvalid = 1;
         }
-        if (t < tGs) tile_router(a, t * kRRows);
+        if (t < tGs) tile_router(a, t * kRRows, s_red);
         else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
         else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
         else if (t == tT) tile_route(a, S.r);
@@ -605,7 +643,7 @@ static bool reject(const char *why) {
 // The layer's MoE block on device pointers (stream-ordered, no sync).  Launches share one
 // scratch area: issue them on one stream.
 bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
-                int *d_idx, float *d_val, hipStream_t st) {
+                int *d_idx, float *d_val, hipStream_t st, const float *d_xw, float eps) {
     EgTable &T = g_eg;
     if (!ok()) return false;
     if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return reject("no expert table for the layer");
@@ -620,10 +658,12 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     const size_t ntag = (size_t)T.E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
     const size_t misc = 256 + (size_t)4 * kMaxSlots * kCounterStride * 4;
     if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, misc)) return false;
-    if (++g_ms.epoch == 0) g_ms.epoch = 1;   // 0 is what fresh scratch holds
+    if (++g_ms.epoch == 0) g_ms.epoch = 2;   // 0 is what fresh scratch holds; keep the parity alternating
     MoeArgs a;
     memset(&a, 0, sizeof(a));
     a.x = d_x;
+    a.xw = d_xw;
+    a.eps = eps;
     a.rw = router->w;
     a.rs = router->sz;
     a.rfmt = router->fmt;
@@ -643,6 +683,14 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.epoch = g_ms.epoch;
     a.g = m;
     return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
+}
+
+bool moe_ready(int layer) {
+    const EgTable &T = g_eg;
+    if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return false;
+    for (int e = 0; e <= T.E; e++)
+        if (!T.valid[(size_t)layer * (T.E + 1) + e]) return false;
+    return true;
 }
 
 bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGeom *geom, int *E) {
