@@ -227,6 +227,33 @@ __device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, in
     }
 }
 
+// x := x r (1 + w) with r = 1 / sqrt(mean(x^2) + eps) over the I columns (zero-centred
+// RMSNorm, c/qwen.c:326-330: double sum of squares; the multiplications in the reference's
+// order).  xr, wr as loaded by prep_load; all threads call (two barriers).
+template <int NT = kThreads>
+__device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr, int I, int ncols, float eps,
+                                           double *s_red) {
+    double ss = 0;
+#pragma unroll
+    for (int k = 0; k < XRegsT<NT>::kWords; k++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];   // zeros past I add 0
+    ss = wave_sum_dpp(ss);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double t = 0;
+    for (int w = 0; w < NT / 64; w++) t += s_red[w];
+    const float r = 1.f / sqrtf((float)(t / I) + eps);
+#pragma unroll
+    for (int k = 0; k < XRegsT<NT>::kWords; k++) {
+        const int w = threadIdx.x + k * NT;
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            if (w < ncols / 8 && w * 8 + c < I) xr.v[k][c] = xr.v[k][c] * r * (1.f + wr.v[k][c]);
+    }
+}
+
 template <int NT = kThreads>
 __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P) {
     const int tid = threadIdx.x;

@@ -89,28 +89,14 @@ struct ProjArgs {
 
 // XF_NORM: x[i] * r * (1 + w[i]), r = 1/sqrt(mean(x^2) + eps) over the I columns
 // (c/qwen.c:326-330, double sum of squares).  XF_GATED: per head of VD columns,
-// y * r_h * gnorm[d] * silu(z) (c/qwen.c:768-772).  Zero columns past I stay zero.
+// y * r_h * gnorm[d] * silu(z) (c/qwen.c:768-772).  Zero columns past I stay zero.  The
+// operands (w; or z and gnorm) were loaded into ar / br together with x.
 template <int XF>
-__device__ __forceinline__ void xf_apply(XRegs &xr, const ProjArgs &a, int ncols) {
+__device__ __forceinline__ void xf_apply(XRegs &xr, const XRegs &ar, const XRegs &br, const ProjArgs &a, int ncols) {
     const int tid = threadIdx.x, nwords = ncols / 8;
     if constexpr (XF == XF_NORM) {
         __shared__ double s_red[kWaves];
-        double ss = 0;
-#pragma unroll
-        for (int k = 0; k < XRegs::kWords; k++)
-#pragma unroll
-            for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];
-        ss = block_sum_d(ss, s_red);
-        const float r = 1.f / sqrtf((float)(ss / a.I) + a.eps);
-#pragma unroll
-        for (int k = 0; k < XRegs::kWords; k++) {
-            const int w = tid + k * kThreads;
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const int i = w * 8 + c;
-                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * (1.f + a.xw[i]);
-            }
-        }
+        norm_apply(xr, ar, a.I, ncols, a.eps, s_red);
     } else if constexpr (XF == XF_GATED) {
         const int wph = a.VD / 8;   // words per head: a power of two <= 64, lane aligned
 #pragma unroll
@@ -124,7 +110,27 @@ __device__ __forceinline__ void xf_apply(XRegs &xr, const ProjArgs &a, int ncols
 #pragma unroll
             for (int c = 0; c < 8; c++) {
                 const int i = w * 8 + c;
-                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * a.xw[i % a.VD] * silu_f(a.z[i]);
+                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * br.v[k][c] * silu_f(ar.v[k][c]);
+            }
+        }
+    }
+}
+
+// the transform operands of the thread's columns: XF_NORM w; XF_GATED z (ar) and the
+// gated-norm weight of the column's head position (br)
+template <int XF>
+__device__ __forceinline__ void xf_load(XRegs &ar, XRegs &br, const ProjArgs &a, int ncols) {
+    if constexpr (XF == XF_NORM) prep_load(a.xw, a.I, ncols, ar);
+    if constexpr (XF == XF_GATED) {
+        prep_load(a.z, a.I, ncols, ar);
+        const int tid = threadIdx.x, nwords = ncols / 8;
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++) {
+            const int w = tid + k * kThreads;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i = w * 8 + c;
+                br.v[k][c] = (w < nwords && i < a.I) ? a.xw[i % a.VD] : 0.f;
             }
         }
     }
@@ -158,8 +164,9 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
     const int j = lane % LPR, sg = lane / LPR;
     const int ncols = a.nl * kLaneChunks * 32;
     const uint32_t srb = (uint32_t)a.ng * 8u;
-    XRegs xr;
+    XRegs xr, ar, br;
     prep_load(a.x, a.I, ncols, xr);
+    if constexpr (XF != XF_PLAIN) xf_load<XF>(ar, br, a, ncols);
     LaneX<CU> L;
     lane_geo<CU>(j, a.nl, a.I, a.gs, L);
     const int nw = gridDim.x * kWaves;
@@ -177,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load(u, gbase + u * nw);
-    if constexpr (XF != XF_PLAIN) xf_apply<XF>(xr, a, ncols);
+    if constexpr (XF != XF_PLAIN) xf_apply<XF>(xr, ar, br, a, ncols);
     prep_x(xr, a.gs, ncols, P);
     lane_x<CU>(P, a.gs, L);
     for (int g0 = gbase; g0 < a.ngroups; g0 += nw * U) {

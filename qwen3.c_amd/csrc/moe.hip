@@ -273,52 +273,73 @@ __device__ __forceinline__ float4 int8x4(uint32_t q) {
     return make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16), (float)(int8_t)(q >> 24));
 }
 
-// rms factor of the residual x (c/qwen.c:326-330: double sum of squares); all threads
-// call, every thread gets the factor
-__device__ float resid_rms(const MoeArgs &a, double *s_red) {
-    const int D = a.g.D;
-    double ss = 0;
-    for (int i = threadIdx.x; i < D; i += kThreads) ss += (double)a.x[i] * a.x[i];
-    ss = wave_sum_dpp(ss);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    double t = 0;
-    for (int w = 0; w < kWaves; w++) t += s_red[w];
-    return 1.f / sqrtf((float)(t / D) + a.eps);
-}
-
-__device__ void tile_router(const MoeArgs &a, int r0, double *s_red) {
+// xn, wn: LDS rows of D floats.  The tile's router rows are loaded first (in flight while
+// the block stages the input row x, normed when a.xw != NULL (c/qwen.c:326-330, x r (1 + w)
+// in the reference's order), into xn); then every wave reads x from LDS.
+__device__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn, float *wn) {
     constexpr int kRC = 8;   // float4 per lane and pass: 2048 columns
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, D = a.g.D;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), D = a.g.D;
     const int r = r0 + wave;
-    const float rr = a.xw ? resid_rms(a, s_red) : 1.f;   // x' = x r (1 + w) (c/qwen.c:329)
-    if (r > a.E) return;
-    const bool gate = r == a.E;
+    const bool live = r <= a.E, gate = r == a.E;   // wave-uniform
     const uint8_t *row = gate ? (const uint8_t *)a.sh_gate : a.rw + (size_t)r * a.rrb;
     const bool f32 = gate || a.rfmt == 0;
+    // buffer loads: columns past D (and rows past E) read 0, no per-lane conditions
+    const __amdgpu_buffer_rsrc_t rr = buf_rsrc(row, !live ? 0u : f32 ? (uint32_t)D * 4u : (uint32_t)D);
+    float4 w[kRC];
+    auto load_row = [&](int c0) {
+        if (f32) {
+#pragma unroll
+            for (int c = 0; c < kRC; c++) {
+                const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rr, (c0 + (lane + c * 64) * 4) * 4, 0, kStream);
+                w[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < kRC; c++)
+                w[c] = int8x4((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, c0 + (lane + c * 64) * 4, 0, kStream));
+        }
+    };
+    load_row(0);
+    if (a.xw) {   // the normed input row into LDS (one block reduction)
+        double ss = 0;
+        for (int i = threadIdx.x; i < D; i += kThreads) {
+            const float v = a.x[i];
+            xn[i] = v;
+            wn[i] = a.xw[i];
+            ss += (double)v * v;
+        }
+        ss = wave_sum_dpp(ss);
+        __syncthreads();
+        if (lane == 0) s_red[wave] = ss;
+        __syncthreads();
+        double t = 0;
+        for (int k = 0; k < kWaves; k++) t += s_red[k];
+        const float rs = 1.f / sqrtf((float)(t / D) + a.eps);
+        for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = xn[i] * rs * (1.f + wn[i]);
+        __syncthreads();
+    }
+    if (!live) return;
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)D * 4u);
     double acc = 0.0;
     for (int c0 = 0; c0 < D; c0 += kRC * 256) {
-        float4 xv[kRC], w[kRC];
+        if (c0) load_row(c0);
+        float4 xq[kRC];
 #pragma unroll
         for (int c = 0; c < kRC; c++) {
             const int col = c0 + (lane + c * 64) * 4;
-            const bool in = col < D;
-            xv[c] = in ? *(const float4 *)(a.x + col) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (a.xw && in) {
-                const float4 w4 = *(const float4 *)(a.xw + col);
-                xv[c] = make_float4(xv[c].x * rr * (1.f + w4.x), xv[c].y * rr * (1.f + w4.y),
-                                    xv[c].z * rr * (1.f + w4.z), xv[c].w * rr * (1.f + w4.w));
+            if (a.xw) {
+                xq[c] = col < D ? *(const float4 *)(xn + col) : make_float4(0.f, 0.f, 0.f, 0.f);   // LDS
+            } else {
+                const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, col * 4, 0, kCached);
+                xq[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
             }
-            w[c] = !in ? make_float4(0.f, 0.f, 0.f, 0.f)
-                       : f32 ? *(const float4 *)(row + (size_t)col * 4) : int8x4(*(const uint32_t *)(row + col));
         }
 #pragma unroll
         for (int c = 0; c < kRC; c++) {
-            acc = fma((double)xv[c].x, (double)w[c].x, acc);
-            acc = fma((double)xv[c].y, (double)w[c].y, acc);
-            acc = fma((double)xv[c].z, (double)w[c].z, acc);
-            acc = fma((double)xv[c].w, (double)w[c].w, acc);
+            acc = fma((double)xq[c].x, (double)w[c].x, acc);
+            acc = fma((double)xq[c].y, (double)w[c].y, acc);
+            acc = fma((double)xq[c].z, (double)w[c].z, acc);
+            acc = fma((double)xq[c].w, (double)w[c].w, acc);
         }
     }
     acc = wave_sum_dpp(acc);
@@ -358,7 +379,11 @@ __device__ void tile_route(const MoeArgs &a, RouteLds &R) {
 }
 
 // ---------------------------------------------------------------- LDS of the kernel
+struct RouterLds {
+    float xn[kLaneMaxI], wn[kLaneMaxI];   // the normed input row, the norm weight
+};
 union MoeLds {
+    RouterLds n;   // R tiles
     XPrep x;       // G tiles
     HPrep h;       // D tiles
     RouteLds r;    // T tile
@@ -506,25 +531,17 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     while (t < total) {
         const bool gtile = (t >= tGs && t < tDsh) || (t >= tGk && t < tDk);
         if (gtile && !s_xvalid) {   // x digits for the G tiles of this block
-            XRegs xr;
+            XRegs xr, wr;
             const int ncols = g.nlG * kLaneChunks * 32;
             prep_load(a.x, g.D, ncols, xr);
             if (a.xw) {   // post-attention norm of the residual (c/qwen.c:326-330)
-                const float rr = resid_rms(a, s_red);
-#pragma unroll
-                for (int k = 0; k < XRegs::kWords; k++) {
-                    const int w = threadIdx.x + k * kThreads;
-#pragma unroll
-                    for (int c = 0; c < 8; c++) {
-                        const int i = w * 8 + c;
-                        if (w < ncols / 8 && i < g.D) xr.v[k][c] = xr.v[k][c] * rr * (1.f + a.xw[i]);
-                    }
-                }
+                prep_load(a.xw, g.D, ncols, wr);
+                norm_apply(xr, wr, g.D, ncols, a.eps, s_red);
             }
             prep_x(xr, g.gs, ncols, S.x);
             if (threadIdx.x == 0) s_xvalid = 1;
         }
-        if (t < tGs) tile_router(a, t * kRRows, s_red);
+        if (t < tGs) tile_router(a, t * kRRows, s_red, S.n.xn, S.n.wn);
         else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
         else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
         else if (t == tT) tile_route(a, S.r);
