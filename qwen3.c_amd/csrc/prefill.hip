@@ -19,18 +19,32 @@
 // product: lane l carries the 16 K positions 16 (l / 16) .. + 15 of the 64-column chunk
 // in the order [0 2 4 6 1 3 5 7 8 10 12 14 9 11 13 15], which is how the weight nibbles
 // fall out of a 32-bit word after masking even and odd nibbles.  The x digit planes are
-// stored in that order (kPerm16).
+// stored in that order (perm16).
+//
+// Launches: pf_logits (router, fp64 split-K partials) -> pf_route (per token: logits,
+// routing, shared gate, x digit planes) -> pf_group (positions per expert) -> pf_gateup
+// (gate/up + SwiGLU) -> pf_digits (h as digit planes) -> pf_down -> pf_combine.
 #include "moe_common.h"
 
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
+
 namespace coli {
 
 typedef int pf_v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kTT = 2;          // 16-row tiles of x per pass (32 rows)
-constexpr int kRowBlk = 64;     // weight rows per block (4 waves x 16)
+constexpr int kGS = 128;               // group size of the MFMA path
+constexpr int kPT = 256;               // threads of the projection kernels (4 waves)
+constexpr int kPW = kPT / 64;
+constexpr int kPR = 32;                // x rows per pass (two 16-row MFMA tiles)
+constexpr int kPitch = kGS + 16;       // LDS bytes per staged row of one group (conflict-free B reads)
+constexpr int kGU = kPW * 16;          // gate/up: h columns per block (64)
+constexpr int kDT = 4;                 // down: 16-row tiles per wave
+constexpr int kDR = kPW * kDT * 16;    // down: output rows per block (256)
+constexpr int kDG = 4;                 // down: groups of h staged at a time (one weight superstep)
+constexpr int kDPitch = kDG * kGS + 16;
 
 // byte position of K offset o (0..15) inside a 16-byte block of digit plane
 __device__ __forceinline__ int perm16(int o) {
@@ -38,346 +52,652 @@ __device__ __forceinline__ int perm16(int o) {
     return h + ((r & 1) ? 4 + (r >> 1) : (r >> 1));
 }
 
-// signed nibbles (stored XOR 8, i.e. the 4-bit two's complement of n - 8) of the 8
-// nibbles of w as int8: even nibbles, then odd nibbles
-__device__ __forceinline__ void nib8(uint32_t w, uint32_t &ev, uint32_t &od) {
-    uint32_t a = w & 0x0F0F0F0Fu, b = (w >> 4) & 0x0F0F0F0Fu;
-    ev = a | ((a & 0x08080808u) * 0x1Eu);   // sign-extend 4 -> 8 bits per byte (no carries)
-    od = b | ((b & 0x08080808u) * 0x1Eu);
+// A operand of one MFMA from 16 nibbles (two words).  A stored nibble (n XOR 8) is the
+// 4-bit two's complement of n' = n - 8, so a nibble in the high half of its byte reads as
+// the int8 16 n'.  Bytes: the low nibbles of w0 (K order 0 2 4 6), its high nibbles
+// (1 3 5 7), then w1's (8 10 12 14, 9 11 13 15).  Products and sums carry the factor 16,
+// which the fold removes exactly through the exponent.
+__device__ __forceinline__ pf_v4i pf_a16(uint32_t w0, uint32_t w1) {
+    return pf_v4i{(int)((w0 << 4) & 0xF0F0F0F0u), (int)(w0 & 0xF0F0F0F0u), (int)((w1 << 4) & 0xF0F0F0F0u),
+                  (int)(w1 & 0xF0F0F0F0u)};
 }
 
-// ---------------------------------------------------------------- router
-// logits[t][e] for e < E (router rows, f32 or int8 * scale) and e = E (shared gate):
-// fp64 accumulation of exact products, rounded once (the reference sums in fp32).
-constexpr int kLT = 8, kLE = 32, kLK = 64;
-__global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, int S, int D, const uint8_t *rw,
-                                                 const float *rs, int rfmt, int rrb, int E,
-                                                 const float *__restrict__ sh_gate, float *__restrict__ logits) {
-    __shared__ float s_x[kLT][kLK];
-    __shared__ float s_w[kLE][kLK + 1];
-    const int tid = threadIdx.x, tt = tid / kLE, ee = tid % kLE;
-    const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE;
-    double acc = 0.0;
-    for (int k0 = 0; k0 < D; k0 += kLK) {
-        for (int q = tid; q < kLT * kLK; q += 256) {
-            const int r = q / kLK, c = q % kLK, t = t0 + r;
-            s_x[r][c] = (t < S && k0 + c < D) ? xs[(size_t)t * D + k0 + c] : 0.f;
+// Block fixed point of 8 consecutive columns (col % 8 == 0) of one row.  The 16 aligned
+// consecutive lanes holding one 128-column group agree on its exponent by shuffles:
+// e = ilogb(max |v|) + 1 (0 for an all-zero group), q = rint(v 2^(22-e)) in balanced
+// base-256 digits d0 + 256 d1 + 65536 d2.  Writes the 8 bytes of each plane at
+// dst + d * pstride (perm16 order) and, from the group's first lane, ge = e - 22 and
+// gsum = 2^(e-22) sum q.  Lanes with valid = false join the shuffles and write nothing.
+__device__ __forceinline__ void digit8(const float (&v)[8], bool valid, int col, int8_t *dst, size_t pstride,
+                                       int *ge, float *gsum) {
+    float m = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(v[c]));
+    uint32_t mu = __float_as_uint(m);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mu = max(mu, (uint32_t)__shfl_xor((int)mu, o));
+    const float mf = __uint_as_float(mu);
+    const int e = mf > 0.f ? ilogbf(mf) + 1 : 0;
+    int qs = 0;
+    uint32_t pl[3][2] = {{0, 0}, {0, 0}, {0, 0}};
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const int q = (int)rintf(ldexpf(v[c], 22 - e));
+        qs += q;
+        const uint32_t u = (uint32_t)(q + 0x808080);   // digits d + 128
+        const int pos = perm16((col + c) & 15) & 7;     // within this 8-byte half
+#pragma unroll
+        for (int d = 0; d < 3; d++) pl[d][pos >> 2] |= ((((u >> (8 * d)) & 255u) ^ 0x80u)) << (8 * (pos & 3));
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) qs += __shfl_xor(qs, o);
+    if (valid) {
+#pragma unroll
+        for (int d = 0; d < 3; d++) *(uint2 *)(dst + d * pstride) = make_uint2(pl[d][0], pl[d][1]);
+        if ((col & (kGS - 1)) == 0) {
+            *ge = e - 22;
+            *gsum = ldexpf((float)qs, e - 22);
         }
-        for (int q = tid; q < kLE * kLK; q += 256) {
-            const int r = q / kLK, c = q % kLK, e = e0 + r, k = k0 + c;
-            float v = 0.f;
-            if (e < E && k < D) v = rfmt == 0 ? ((const float *)(rw + (size_t)e * rrb))[k] : (float)(int8_t)rw[(size_t)e * rrb + k];
-            else if (e == E && k < D) v = sh_gate[k];
-            s_w[r][c] = v;
+    }
+}
+
+// ---------------------------------------------------------------- router logits
+// part[z][t][e] = sum over the z-th Dk-column slice of x[t][k] w[e][k]: fp32 values,
+// exact fp64 products, fp64 accumulation (the reference sums in fp32; pf_route adds the
+// slices in order and rounds once).  64 tokens x 64 experts per block of 256 threads,
+// 4 x 4 per thread; the slice is staged in LDS 32 columns at a time, transposed, double
+// buffered.  Router rows f32 (rfmt 0) or int8 (rfmt 1, scale applied by pf_route).
+constexpr int kLT = 64, kLE = 64, kLC = 32;
+__global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, int S, int D,
+                                                 const uint8_t *__restrict__ rw, int rfmt, int rrb, int E, int Dk,
+                                                 double *__restrict__ part) {
+    __shared__ __attribute__((aligned(16))) float s_x[2][kLC][kLT];
+    __shared__ __attribute__((aligned(16))) float s_w[2][kLC][kLE];
+    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE, kz = blockIdx.z * Dk;
+    float4 rx[2], rv[2];
+    // staging: row r = idx % 64 of the tile, columns 4 (idx / 64) .. + 3, idx = tid + 256 s
+    auto load = [&](int kc) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int idx = tid + 256 * s, r = idx & 63, k = kz + kc + 4 * (idx >> 6);
+            const int t = t0 + r, e = e0 + r;
+            rx[s] = t < S ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e >= E) {
+                rv[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+            } else if (rfmt == 0) {
+                rv[s] = *(const float4 *)(rw + (size_t)e * rrb + 4 * (size_t)k);
+            } else {
+                const char4 c = *(const char4 *)(rw + (size_t)e * rrb + k);
+                rv[s] = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
+            }
         }
-        __syncthreads();
-#pragma unroll 8
-        for (int c = 0; c < kLK; c++) acc = fma((double)s_x[tt][c], (double)s_w[ee][c], acc);
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int idx = tid + 256 * s, r = idx & 63, c = 4 * (idx >> 6);
+            s_x[buf][c][r] = rx[s].x;
+            s_x[buf][c + 1][r] = rx[s].y;
+            s_x[buf][c + 2][r] = rx[s].z;
+            s_x[buf][c + 3][r] = rx[s].w;
+            s_w[buf][c][r] = rv[s].x;
+            s_w[buf][c + 1][r] = rv[s].y;
+            s_w[buf][c + 2][r] = rv[s].z;
+            s_w[buf][c + 3][r] = rv[s].w;
+        }
+    };
+    double acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kc = 0, buf = 0; kc < Dk; kc += kLC, buf ^= 1) {
+        const bool more = kc + kLC < Dk;
+        if (more) load(kc + kLC);
+#pragma unroll 4
+        for (int k = 0; k < kLC; k++) {
+            const float4 a = *(const float4 *)&s_x[buf][k][4 * ty];
+            const float4 b = *(const float4 *)&s_w[buf][k][4 * tx];
+            const double ad[4] = {a.x, a.y, a.z, a.w}, bd[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fma(ad[i], bd[j], acc[i][j]);
+        }
+        if (more) store(buf ^ 1);
         __syncthreads();
     }
-    const int t = t0 + tt, e = e0 + ee;
-    if (t < S && e <= E) {
-        float l = (float)acc;
-        if (e < E && rfmt == 1) l *= rs[e];   // c/qwen.c:237: acc * scale[o]
-        logits[(size_t)t * (E + 1) + e] = l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = t0 + 4 * ty + i;
+        if (t >= S) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = e0 + 4 * tx + j;
+            if (e < E) part[((size_t)blockIdx.z * S + t) * E + e] = acc[i][j];
+        }
     }
 }
 
 // ---------------------------------------------------------------- route per token
-__global__ __launch_bounds__(kThreads) void pf_route(const float *__restrict__ logits, int E, int K, int *tidx,
-                                                    float *tval, float *tshg) {
+// One block per token: the router logits (slices of part added in order, rounded once,
+// times the int8 scale; c/qwen.c:237), the routing (route_select), the shared expert's
+// gate sigmoid(x . sh_gate) (fp64 dot; c/qwen.c:1159), and x's digit planes for the
+// projections ([3][S][D] planes, [S][D/128] exponents and sums).
+__global__ __launch_bounds__(kThreads) void pf_route(const double *__restrict__ part, int KS, const float *__restrict__ xs,
+                                                    int S, int D, const float *__restrict__ rs, int rfmt,
+                                                    const float *__restrict__ sh_gate, int E, int K, int *tidx,
+                                                    float *tval, float *tshg, int8_t *__restrict__ xd,
+                                                    int *__restrict__ xe, float *__restrict__ xsum) {
     __shared__ RouteLds R;
-    const int t = blockIdx.x;
-    const float *lg = logits + (size_t)t * (E + 1);
-    for (int e = threadIdx.x; e <= E; e += kThreads) {
-        if (e < E) R.p[e] = lg[e];
-        else R.gate = lg[e];
+    __shared__ double s_red[kWaves];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += kThreads) {
+        double l = 0.0;
+        for (int z = 0; z < KS; z++) l += part[((size_t)z * S + t) * E + e];
+        float lf = (float)l;
+        if (rfmt == 1) lf *= rs[e];
+        R.p[e] = lf;
+    }
+    const float *x = xs + (size_t)t * D;
+    const int ngD = D / kGS;
+    double g = 0.0;
+    for (int c8 = tid; c8 < D / 8; c8 += kThreads) {   // D / 8 is a multiple of 16: whole groups
+        float v[8];
+        const float4 a = *(const float4 *)(x + 8 * c8), b = *(const float4 *)(x + 8 * c8 + 4);
+        const float4 sa = *(const float4 *)(sh_gate + 8 * c8), sb = *(const float4 *)(sh_gate + 8 * c8 + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        const float sg[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+#pragma unroll
+        for (int c = 0; c < 8; c++) g = fma((double)v[c], (double)sg[c], g);
+        const int gi = (8 * c8) / kGS;
+        digit8(v, true, 8 * c8, xd + (size_t)t * D + 8 * c8, (size_t)S * D, xe + (size_t)t * ngD + gi,
+               xsum + (size_t)t * ngD + gi);
+    }
+    g = wave_sum_dpp(g);
+    if (lane == 0) s_red[wave] = g;
+    __syncthreads();
+    if (tid == 0) {
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) s += s_red[w];
+        R.gate = (float)s;
     }
     route_select(R, E, K);
-    if (threadIdx.x < K) {
-        tidx[t * K + threadIdx.x] = R.idx[threadIdx.x];
-        tval[t * K + threadIdx.x] = R.val[threadIdx.x] / R.vsum;
+    if (tid < K) {
+        tidx[t * K + tid] = R.idx[tid];
+        tval[t * K + tid] = R.val[tid] / R.vsum;
     }
-    if (threadIdx.x == 0) tshg[t] = 1.f / (1.f + expf(-R.gate));
+    if (tid == 0) tshg[t] = 1.f / (1.f + expf(-R.gate));
 }
 
 // ---------------------------------------------------------------- grouping
 // off[e] = first position of expert e's rows, off[E] = S*K; plist[p] = pair index
 // (token * K + slot) at position p; ppos[pair] = its position.  Rows of one expert are
-// independent, so their order within the expert does not change any result.
-__global__ __launch_bounds__(1024) void pf_group(const int *tidx, int npairs, int E, int *cnt, int *off, int *plist,
+// independent, so their order within the expert does not change any result.  E <= 1024.
+__global__ __launch_bounds__(1024) void pf_group(const int *tidx, int npairs, int E, int *off, int *plist,
                                                  int *ppos, int *rank) {
-    extern __shared__ int s_cnt[];   // [E + 1]
-    for (int e = threadIdx.x; e <= E; e += 1024) s_cnt[e] = 0;
+    __shared__ int s_cnt[kMaxE];
+    __shared__ int s_wsum[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 1024) s_cnt[e] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < npairs; i += 1024) rank[i] = atomicAdd(&s_cnt[tidx[i]], 1);
+    for (int i = tid; i < npairs; i += 1024) rank[i] = atomicAdd(&s_cnt[tidx[i]], 1);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; e++) {
-            const int n = s_cnt[e];
-            cnt[e] = n;
-            s_cnt[e] = acc;
-            off[e] = acc;
-            acc += n;
-        }
-        off[E] = acc;
+    // exclusive scan of the counts: inclusive per wave, then the wave totals
+    const int c = tid < E ? s_cnt[tid] : 0;
+    int inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o);
+        if (lane >= o) inc += v;
     }
+    if (lane == 63) s_wsum[wave] = inc;
     __syncthreads();
-    for (int i = threadIdx.x; i < npairs; i += 1024) {
+    int base = 0;
+    for (int w = 0; w < wave; w++) base += s_wsum[w];
+    const int excl = base + inc - c;
+    if (tid < E) {
+        off[tid] = excl;
+        s_cnt[tid] = excl;
+    }
+    if (tid == 1023) off[E] = base + inc;   // the last thread's inclusive sum is the total
+    __syncthreads();
+    for (int i = tid; i < npairs; i += 1024) {
         const int p = s_cnt[tidx[i]] + rank[i];
         plist[p] = i;
         ppos[i] = p;
     }
 }
 
-// ---------------------------------------------------------------- digit planes
-// Rows of n values (x or h) -> planes[3][rows][n] (int8, kPerm16 order inside each
-// 16-column block), ge[rows][ng] = e - 22 and gs_[rows][ng] = 2^(e-22) * sum of q, per
-// group of gs columns: the block fixed point of fmt6_device.h in base 256.  One block of
-// 256 threads per 4 rows; n <= 4096, n % 64 == 0, gs % 64 == 0.
-__global__ __launch_bounds__(256) void pf_digits(const float *__restrict__ src, int rows, int n, int gs,
-                                                 int8_t *__restrict__ planes, int *__restrict__ ge,
-                                                 float *__restrict__ gsum) {
-    __shared__ unsigned s_max[4][64];
-    __shared__ int s_q[4][64];
-    const int sub = threadIdx.x >> 6, lane = threadIdx.x & 63, row = blockIdx.x * 4 + sub;
-    const int ng = n / gs;
-    if (lane < 64) {
-        s_max[sub][lane] = 0u;
-        s_q[sub][lane] = 0;
+// ---------------------------------------------------------------- projections
+struct PfArgs {
+    const ExpertRec *rec;   // [E + 1], the shared expert last
+    const int *off;         // [E + 1] first position per expert (routed)
+    const int *plist;       // position -> pair (token = pair / K)
+    int E, S, K, D, I;
+    int nlG, rbG, nlD, rbD;   // lanes layout: lanes per row, row bytes (gate/up, down)
+    int nsp;                  // shared-expert passes: ceil(S / kPR)
+    const int8_t *xd;         // x digit planes [3][S][D]
+    const int *xe;            // [S][D / 128]
+    const float *xsum;
+    float *h;                 // [P][I] SwiGLU output per position, P = S K + S
+    const int8_t *hd;         // h digit planes [3][P][I]
+    const int *he;            // [P][I / 128]
+    const float *hsum;
+    float *y;                 // [P][D] expert outputs per position
+};
+
+// Block b of a projection launch -> (expert e, unit u, passes [p0, p1)).  Blocks
+// [0, nu nsp) are the shared expert's units, one pass each (u = b % nu); the count is
+// rounded up to a multiple of 8 with idle blocks; the rest are routed (e, u) with all of
+// e's passes, placed so that the nu units of one expert run on one XCD (workgroups are
+// dealt to the 8 XCDs round-robin by index) and share its rows of x in that L2.
+// False for an idle block (or a routed expert without rows).
+__device__ __forceinline__ bool pf_unit(const PfArgs &a, int nu, int &e, int &u, int &p0, int &p1, int &pos0,
+                                        int &n) {
+    const int b = blockIdx.x, nsu = nu * a.nsp, nsu8 = (nsu + 7) & ~7;
+    if (b < nsu) {
+        e = a.E;
+        u = b % nu;
+        p0 = b / nu;
+        p1 = p0 + 1;
+        pos0 = a.S * a.K;
+        n = a.S;
+        return true;
     }
-    __syncthreads();
-    constexpr int kW = 4096 / 8 / 64;   // 8-column words per lane
-    float v[kW][8];
+    if (b < nsu8) return false;
+    const int r = b - nsu8, xcd = r & 7, rest = r >> 3;
+    u = rest % nu;
+    e = 8 * (rest / nu) + xcd;
+    if (e >= a.E) return false;
+    pos0 = a.off[e];
+    n = a.off[e + 1] - pos0;
+    p0 = 0;
+    p1 = (n + kPR - 1) / kPR;
+    return n > 0;
+}
+
+// The fold of one group's three digit sums into the fp32 accumulator of 4 outputs:
+// T = t0 + 256 t1 + 65536 t2 (t0 + 256 t1 exact in int32, t2 * 65536 exact in fp32),
+// v = 2^xe T - (z - 8) xsum, acc += s v.  The sums are 16 times the integer products
+// (pf_a16), so xe is the group's exponent e - 22 minus 4: every step is scaled by an
+// exact power of two and the result is that of the unscaled sums.
+__device__ __forceinline__ void pf_fold(const pf_v4i (&iacc)[3], const float2 (&sz)[4], int xe, float xs,
+                                        float (&acc)[4]) {
 #pragma unroll
-    for (int k = 0; k < kW; k++) {
-        const int w = lane + 64 * k;
-#pragma unroll
-        for (int c = 0; c < 8; c++) v[k][c] = (row < rows && w * 8 < n) ? src[(size_t)row * n + w * 8 + c] : 0.f;
-        float m = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(v[k][c]));
-        if (w * 8 < n) atomicMax(&s_max[sub][(w * 8) / gs], __float_as_uint(m));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kW; k++) {
-        const int w = lane + 64 * k;
-        if (row >= rows || w * 8 >= n) continue;
-        const int g = (w * 8) / gs;
-        const float m = __uint_as_float(s_max[sub][g]);
-        const int e = m > 0.f ? ilogbf(m) + 1 : 0;
-        int qs = 0;
-        uint32_t pl[3][2] = {{0, 0}, {0, 0}, {0, 0}};   // 8 bytes per plane
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int q = (int)rintf(ldexpf(v[k][c], 22 - e));
-            qs += q;
-            const uint32_t u = (uint32_t)(q + 0x808080);   // balanced base-256 digits d + 128
-            const int pos = perm16((w * 8 + c) & 15) & 7;  // within this 8-byte half
-#pragma unroll
-            for (int d = 0; d < 3; d++) {
-                const uint32_t byte = (((u >> (8 * d)) & 255u) ^ 0x80u);   // d as int8
-                pl[d][pos >> 2] |= byte << (8 * (pos & 3));
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < 3; d++)
-            *(uint2 *)(planes + ((size_t)d * rows + row) * n + w * 8) = make_uint2(pl[d][0], pl[d][1]);
-        atomicAdd(&s_q[sub][g], qs);
-    }
-    __syncthreads();
-    if (row < rows && lane < ng) {
-        const float m = __uint_as_float(s_max[sub][lane]);
-        const int e = m > 0.f ? ilogbf(m) + 1 : 0;
-        ge[(size_t)row * ng + lane] = e - 22;
-        gsum[(size_t)row * ng + lane] = ldexpf((float)s_q[sub][lane], e - 22);
+    for (int r = 0; r < 4; r++) {
+        const float lo = (float)(iacc[0][r] + 256 * iacc[1][r]);
+        const float T = fmaf((float)iacc[2][r], 65536.f, lo);
+        const float v = fmaf(-(sz[r].y - 8.f), xs, ldexpf(T, xe));
+        acc[r] = fmaf(sz[r].x, v, acc[r]);
     }
 }
 
-// ---------------------------------------------------------------- grouped GEMM
-// One block (4 waves) per (expert, 64 weight rows, pass of kXRows x-rows); gs = 128.
-// Per group of 128 columns: lane (row i = l % 16, q = l / 16) loads the 16-byte lanes-
-// layout slot of host chunk 4 g + q (32 nibbles: the first 16 feed MFMA half 0, the next
-// 16 half 1); the x digits of the pass's rows for the group are staged in LDS once per
-// block (double buffered) and read as B fragments; weight slots are loaded kGA groups
-// ahead into a register ring.  Scales of the block's rows sit in LDS for the whole pass.
-struct PfGemm {
-    const ExpertRec *rec;   // [E + 1]
-    const int *off;         // [E + 1] first position per expert (routed)
-    int E, S, K;            // experts, tokens, slots
-    int Kdim, O, ng;        // contraction length, weight rows, groups per row (gs = 128)
-    int nl, rb;             // lanes layout: lanes per row, row bytes
-    const int8_t *planes;   // digit planes [3][rows][Kdim]
-    const int *ge;          // [rows][ng]
-    const float *gsum;      // [rows][ng]
-    int prow;               // rows of the planes (tokens for gate/up, positions for down)
-    const int *plist;       // position -> pair (gate/up: row of planes = pair / K)
-    float *out;             // [positions][O] (h for gate/up, y for down)
-    int shared;             // 1: the shared expert over all S tokens (positions S*K + t)
-};
+// Weight slots of 4 consecutive groups (a superstep) for the MFMA A operand.  Lane (q, j)
+// reads 16 bytes at slot 8 S + q and 8 S + 4 + q of each half of row j (lanes layout:
+// even host chunks, then odd), so one load covers 64 contiguous bytes of each of 16 rows;
+// a permlane32 swap of (even, odd) pairs then leaves one group per register across the 4
+// q lanes: register i holds group 4 S + i, lane q host chunk 4 g + kq, kq = [0 2 1 3][q].
+__device__ __forceinline__ void pf_swap(uint4 &a, uint4 &b) {
+    const auto x = __builtin_amdgcn_permlane32_swap(a.x, b.x, false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(a.y, b.y, false, false);
+    const auto z = __builtin_amdgcn_permlane32_swap(a.z, b.z, false, false);
+    const auto w = __builtin_amdgcn_permlane32_swap(a.w, b.w, false, false);
+    a = make_uint4(x[0], y[0], z[0], w[0]);
+    b = make_uint4(x[1], y[1], z[1], w[1]);
+}
+__device__ __forceinline__ void pf_wload(__amdgpu_buffer_rsrc_t r, uint32_t o, uint32_t half, uint4 (&d)[4]) {
+    d[0] = buf_load16<kCached>(r, o);
+    d[1] = buf_load16<kCached>(r, o + half);
+    d[2] = buf_load16<kCached>(r, o + 64);
+    d[3] = buf_load16<kCached>(r, o + half + 64);
+}
+__device__ __forceinline__ void pf_wgroups(uint4 (&d)[4]) {
+    pf_swap(d[0], d[1]);   // groups 4 S, 4 S + 1
+    pf_swap(d[2], d[3]);   // groups 4 S + 2, 4 S + 3
+}
 
-constexpr int kGS = 128;              // group size of the MFMA path
-constexpr int kXRows = 16 * kTT;      // x rows per pass
-constexpr int kXPitch = kGS + 16;     // LDS bytes per staged row (bank-conflict-free B reads)
-constexpr int kGA = 3;                // weight groups loaded ahead
-
-template <int GU>
-__global__ __launch_bounds__(256) void pf_gemm(PfGemm a) {
-    constexpr int NM = GU ? 2 : 1;   // weight matrices: (gate, up) or (down)
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][3][kXRows][kXPitch];
-    __shared__ int sE[2][kXRows];
-    __shared__ float sQ[2][kXRows];
-    extern __shared__ float2 sS[];   // [NM][kRowBlk][ng] scales of the block's rows
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, j = lane & 15;
-    const int nblk = (a.O + kRowBlk - 1) / kRowBlk;
-    const int e = a.shared ? a.E : (int)(blockIdx.x / nblk);
-    const int rbk = blockIdx.x % nblk;
-    const int pos0 = a.shared ? a.S * a.K : a.off[e];
-    const int n = a.shared ? a.S : a.off[e + 1] - a.off[e];
-    if (blockIdx.y * kXRows >= n) return;   // (uniform) no pass for this block
+// Gate/up + SwiGLU.  Unit = 64 columns of h: wave w owns gate and up rows
+// 64 u + 16 w .. + 15.  Per pass of <= 32 rows of x, supersteps of 4 groups: the x digit
+// planes of the pass's rows for the superstep sit in LDS (each thread stages its row's
+// 12 x 16 bytes), the next superstep's x digits and then its weight slots are loaded
+// while this one computes, so the in-order wait for those x digits never covers the
+// weights.  Each (matrix, digit, 16-row tile) is two MFMAs per group, folded in fp32 with
+// the group's scale.  h = silu(gate) * up (c/qwen.c:780-786, silu c/qwen.c:173) goes out
+// as fp32 rows.
+__global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t sB[4][3][kPR][kPitch];
+    __shared__ int sE[4][kPR];
+    __shared__ float sQ[4][kPR];
+    extern __shared__ float4 sS4[];   // [D / 128][2][kGU] float2: scales of the unit's rows
+    float2 *sS = (float2 *)sS4;
+    const int nh = a.I / kGU, ngD = a.D / kGS, nss = (ngD + 3) / 4;
+    int e, u, p0, p1, pos0, n;
+    if (!pf_unit(a, nh, e, u, p0, p1, pos0, n)) return;
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const ExpertRec rec = a.rec[e];
-    const uint8_t *W[2] = {GU ? rec.wg : rec.wd, rec.wu};
-    const float *SZ[2] = {GU ? rec.sg : rec.sd, rec.su};
-    const int ng = a.ng;
-    const uint32_t wtot = (uint32_t)a.O * a.rb;
-    // scales of the block's 64 rows
-    for (int m = 0; m < NM; m++)
-        for (int v = tid; v < kRowBlk * ng; v += 256) {
-            const int r = rbk * kRowBlk + v / ng;
-            sS[(m * kRowBlk) * ng + v] = r < a.O ? ((const float2 *)SZ[m])[(size_t)r * ng + v % ng] : make_float2(0.f, 0.f);
+    {   // scales of rows kGU u .. + kGU - 1 of gate and up, regrouped by group
+        const float2 *sg = (const float2 *)rec.sg + (size_t)u * kGU * ngD, *su = (const float2 *)rec.su + (size_t)u * kGU * ngD;
+        for (int v = tid; v < kGU * ngD; v += kPT) {
+            const int r = v / ngD, g = v - r * ngD;
+            sS[(2 * g) * kGU + r] = sg[v];
+            sS[(2 * g + 1) * kGU + r] = su[v];
         }
-    const int arow = rbk * kRowBlk + wave * 16 + j;   // weight row of this lane's A fragment
-    // staging thread: x row sr = tid / 8 of the pass, 16 columns at 16 * (tid % 8)
-    const int sr = tid >> 3, sc = (tid & 7) * 16;
-    for (int pass = blockIdx.y; pass * kXRows < n; pass += gridDim.y) {
-        int srow;   // planes row staged by this thread
+    }
+    const __amdgpu_buffer_rsrc_t wr[2] = {buf_rsrc(rec.wg, (uint32_t)a.I * a.rbG), buf_rsrc(rec.wu, (uint32_t)a.I * a.rbG)};
+    const uint32_t abase = (uint32_t)((u * kGU + wave * 16 + j) * a.rbG + q * 16), whalf = (uint32_t)a.nlG * 16;
+    auto w_load = [&](int S, uint4 (&d)[2][4]) {
+        const uint32_t o = S < nss ? abase + 128u * S : kOOB;
+        pf_wload(wr[0], o, whalf, d[0]);
+        pf_wload(wr[1], o, whalf, d[1]);
+    };
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xd, (uint32_t)(3u * a.S * a.D));
+    const uint32_t plane = (uint32_t)a.S * a.D;
+    // staging thread: row sr of the pass, 16 columns at sc of every group and plane; the
+    // threads with tid % 8 < 4 also carry exponent and sum of group tid % 8
+    const int sr = tid >> 3, sc = (tid & 7) * 16, sg4 = tid & 7;
+    struct XStage {
+        uint4 v[4][3];
+        int e;
+        float s;
+    };
+    for (int pass = p0; pass < p1; pass++) {
+        const int r0 = pass * kPR, nr = min(kPR, n - r0), ntt = nr > 16 ? 2 : 1;
+        int xrow;
         {
-            const int i = pass * kXRows + sr;
-            const int p = pos0 + (i < n ? i : 0);
-            srow = GU ? (a.shared ? p - a.S * a.K : a.plist[p] / a.K) : p;
+            const int i = r0 + min(sr, nr - 1);
+            xrow = e == a.E ? i : a.plist[pos0 + i] / a.K;
         }
-        auto stage_load = [&](int g, uint4 (&rv)[3], int &re, float &rq) {
+        auto x_load = [&](int S, XStage &st) {
 #pragma unroll
-            for (int d = 0; d < 3; d++)
-                rv[d] = *(const uint4 *)(a.planes + ((size_t)d * a.prow + srow) * a.Kdim + g * kGS + sc);
-            if ((tid & 7) == 0) {
-                re = a.ge[(size_t)srow * ng + g];
-                rq = a.gsum[(size_t)srow * ng + g];
+            for (int gl = 0; gl < 4; gl++) {
+                const int g = 4 * S + gl;
+                const uint32_t o = g < ngD ? (uint32_t)xrow * a.D + g * kGS + sc : kOOB;
+#pragma unroll
+                for (int d = 0; d < 3; d++) st.v[gl][d] = buf_load16<kCached>(xr, o + d * plane);
+            }
+            const int gc = min(4 * S + (sg4 & 3), ngD - 1);
+            st.e = a.xe[(size_t)xrow * ngD + gc];
+            st.s = a.xsum[(size_t)xrow * ngD + gc];
+        };
+        auto x_store = [&](const XStage &st) {
+#pragma unroll
+            for (int gl = 0; gl < 4; gl++)
+#pragma unroll
+                for (int d = 0; d < 3; d++) *(uint4 *)&sB[gl][d][sr][sc] = st.v[gl][d];
+            if (sg4 < 4) {
+                sE[sg4][sr] = st.e - 4;   // the sums carry 16 (pf_a16)
+                sQ[sg4][sr] = st.s;
             }
         };
-        auto stage_store = [&](int buf, const uint4 (&rv)[3], int re, float rq) {
-#pragma unroll
-            for (int d = 0; d < 3; d++) *(uint4 *)&sB[buf][d][sr][sc] = rv[d];
-            if ((tid & 7) == 0) {
-                sE[buf][sr] = re;
-                sQ[buf][sr] = rq;
-            }
-        };
-        uint4 ring[kGA][NM];
-        auto a_load = [&](int g, uint4 (&dst)[NM]) {
-            const int h = 4 * g + q;   // host chunk of this lane
-            const uint32_t off = arow < a.O ? (uint32_t)(arow * a.rb + ((h & 1) * a.nl + (h >> 1)) * 16) : kOOB;
-#pragma unroll
-            for (int m = 0; m < NM; m++) dst[m] = buf_load16<kCached>(buf_rsrc(W[m], wtot), g < ng ? off : kOOB);
-        };
-#pragma unroll
-        for (int g = 0; g < kGA; g++) a_load(g, ring[g]);
-        {
-            uint4 rv[3];
-            int re = 0;
-            float rq = 0.f;
-            stage_load(0, rv, re, rq);
-            stage_store(0, rv, re, rq);
-        }
+        XStage xst;
+        x_load(0, xst);
+        uint4 W[2][4];
+        w_load(0, W);
+        x_store(xst);
         __syncthreads();
-        float facc[NM][kTT][4];
+        // the tile count as a compile-time constant: no branches between the LDS reads
+        // and the MFMAs of a group, so the scheduler can batch them
+        auto run = [&](auto ntc) {
+            constexpr int NT = decltype(ntc)::value;
+            float facc[2][2][4];
 #pragma unroll
-        for (int m = 0; m < NM; m++)
+            for (int m = 0; m < 2; m++)
 #pragma unroll
-            for (int tt = 0; tt < kTT; tt++)
+                for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) facc[m][tt][r] = 0.f;
-        for (int g = 0; g < ng; g++) {
-            const int buf = g & 1;
-            uint4 rv[3];
-            int re = 0;
-            float rq = 0.f;
-            if (g + 1 < ng) stage_load(g + 1, rv, re, rq);   // next group's x digits, in flight
-            uint4 wcur[NM];
+                    for (int r = 0; r < 4; r++) facc[m][tt][r] = 0.f;
+            for (int S = 0; S < nss; S++) {
+                x_load(S + 1, xst);   // zeros past the end
+                uint4 C[2][4];
 #pragma unroll
-            for (int u = 0; u < kGA; u++)
-                if (u == g % kGA)
+                for (int m = 0; m < 2; m++)
 #pragma unroll
-                    for (int m = 0; m < NM; m++) wcur[m] = ring[u][m];
+                    for (int i = 0; i < 4; i++) C[m][i] = W[m][i];
+                w_load(S + 1, W);
+                pf_wgroups(C[0]);
+                pf_wgroups(C[1]);
 #pragma unroll
-            for (int u = 0; u < kGA; u++)   // refill the slot with group g + kGA
-                if (u == g % kGA) a_load(g + kGA, ring[u]);
-            pf_v4i iacc[NM][3][kTT];
+                for (int gl = 0; gl < 4; gl++) {
+                    const int g = 4 * S + gl;
+                    if (g >= ngD) continue;   // uniform
+                    pf_v4i av[2][2];   // [matrix][half]
 #pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int d = 0; d < 3; d++)
-#pragma unroll
-                    for (int tt = 0; tt < kTT; tt++) iacc[m][d][tt] = pf_v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                pf_v4i av[NM];
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    uint32_t e0, o0, e1, o1;
-                    nib8(hh ? wcur[m].z : wcur[m].x, e0, o0);
-                    nib8(hh ? wcur[m].w : wcur[m].y, e1, o1);
-                    av[m] = pf_v4i{(int)e0, (int)o0, (int)e1, (int)o1};
-                }
-#pragma unroll
-                for (int d = 0; d < 3; d++)
-#pragma unroll
-                    for (int tt = 0; tt < kTT; tt++) {
-                        const pf_v4i bv = *(const pf_v4i *)&sB[buf][d][tt * 16 + j][32 * q + 16 * hh];
-#pragma unroll
-                        for (int m = 0; m < NM; m++)
-                            iacc[m][d][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[m], bv, iacc[m][d][tt], 0, 0, 0);
+                    for (int m = 0; m < 2; m++) {
+                        av[m][0] = pf_a16(C[m][gl].x, C[m][gl].y);
+                        av[m][1] = pf_a16(C[m][gl].z, C[m][gl].w);
                     }
+                    pf_v4i iacc[2][2][3];   // [matrix][tile][digit]; one B read serves both matrices
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                        for (int d = 0; d < 3; d++)
+#pragma unroll
+                            for (int tt = 0; tt < 2; tt++)
+                                if (tt < NT) {
+                                    const pf_v4i bv = *(const pf_v4i *)&sB[gl][d][tt * 16 + j][32 * kq + 16 * hh];
+#pragma unroll
+                                    for (int m = 0; m < 2; m++)
+                                        iacc[m][tt][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                            av[m][hh], bv, hh ? iacc[m][tt][d] : pf_v4i{0, 0, 0, 0}, 0, 0, 0);
+                                }
+                    float2 sz[2][4];
+#pragma unroll
+                    for (int m = 0; m < 2; m++) {
+                        const float4 *sz4 = (const float4 *)&sS[(2 * g + m) * kGU + wave * 16 + 4 * q];
+                        const float4 za = sz4[0], zb = sz4[1];
+                        sz[m][0] = make_float2(za.x, za.y);
+                        sz[m][1] = make_float2(za.z, za.w);
+                        sz[m][2] = make_float2(zb.x, zb.y);
+                        sz[m][3] = make_float2(zb.z, zb.w);
+                    }
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++)
+                        if (tt < NT) {
+                            const int xe = sE[gl][tt * 16 + j];
+                            const float xs = sQ[gl][tt * 16 + j];
+#pragma unroll
+                            for (int m = 0; m < 2; m++) pf_fold(iacc[m][tt], sz[m], xe, xs, facc[m][tt]);
+                        }
+                }
+                if (S + 1 < nss) {   // uniform
+                    __syncthreads();   // every wave is done with this superstep's x digits
+                    x_store(xst);
+                    __syncthreads();
+                }
             }
-            // fold the group: T = t0 + 256 t1 + 65536 t2 (t2 * 65536 exact in fp32)
+            // lane holds h columns kGU u + 16 w + 4 q .. + 3 of x row tt * 16 + j
 #pragma unroll
-            for (int tt = 0; tt < kTT; tt++) {
-                const int xe = sE[buf][tt * 16 + j];
-                const float xs = sQ[buf][tt * 16 + j];
-#pragma unroll
-                for (int m = 0; m < NM; m++)
+            for (int tt = 0; tt < 2; tt++) {
+                const int x = tt * 16 + j;
+                if (tt < NT && x < nr) {
+                    float hv[4];
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const float2 sz = sS[(m * kRowBlk + wave * 16 + 4 * q + r) * ng + g];
-                        const float lo = (float)(iacc[m][0][tt][r] + 256 * iacc[m][1][tt][r]);
-                        const float T = fmaf((float)iacc[m][2][tt][r], 65536.f, lo);
-                        const float v = fmaf(-(sz.y - 8.f), xs, ldexpf(T, xe));
-                        facc[m][tt][r] = fmaf(sz.x, v, facc[m][tt][r]);
+                        const float gv = facc[0][tt][r];
+                        hv[r] = gv / (1.f + expf(-gv)) * facc[1][tt][r];
                     }
-            }
-            if (g + 1 < ng) stage_store(buf ^ 1, rv, re, rq);
-            __syncthreads();
-        }
-        // epilogue: lane holds rows 4 q + r of the wave tile for x row j of each tile
-#pragma unroll
-        for (int tt = 0; tt < kTT; tt++) {
-            const int i = pass * kXRows + tt * 16 + j;
-            if (i >= n) continue;
-            const size_t p = (size_t)pos0 + i;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int orow = rbk * kRowBlk + wave * 16 + 4 * q + r;
-                if (orow >= a.O) continue;
-                float v;
-                if (GU) {   // c/qwen.c:780-786, silu c/qwen.c:173
-                    const float gv = facc[0][tt][r];
-                    v = gv / (1.f + expf(-gv)) * facc[NM - 1][tt][r];
-                } else {
-                    v = facc[0][tt][r];
+                    *(float4 *)&a.h[(size_t)(pos0 + r0 + x) * a.I + u * kGU + wave * 16 + 4 * q] =
+                        make_float4(hv[0], hv[1], hv[2], hv[3]);
                 }
-                a.out[p * a.O + orow] = v;
+            }
+        };
+        if (ntt == 2) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
+        __syncthreads();   // the next pass restages sB
+    }
+}
+
+// Rows of n values (n % 128 == 0) -> digit planes [3][rows][n], ge / gsum [rows][n / 128]:
+// one thread per 8 columns.
+__global__ __launch_bounds__(256) void pf_digits(const float *__restrict__ src, int rows, int n,
+                                                 int8_t *__restrict__ planes, int *__restrict__ ge,
+                                                 float *__restrict__ gsum) {
+    const int per = n / 8, i = blockIdx.x * 256 + threadIdx.x, row = i / per, c8 = i - row * per;
+    const bool valid = row < rows;
+    float v[8];
+    if (valid) {
+        const float4 a = *(const float4 *)(src + (size_t)row * n + 8 * c8),
+                     b = *(const float4 *)(src + (size_t)row * n + 8 * c8 + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) v[c] = 0.f;
+    }
+    const int ng = n / kGS, gi = (8 * c8) / kGS;
+    const size_t r = valid ? row : 0;
+    digit8(v, valid, 8 * c8, planes + r * n + 8 * c8, (size_t)rows * n, ge + r * ng + gi, gsum + r * ng + gi);
+}
+
+// Down projection.  Unit = 256 output rows: wave w owns rows 256 u + 64 w + 16 t .. + 15
+// (t < 4).  Per pass of <= 32 positions, h's digit planes are staged in LDS 4 groups
+// (512 columns) at a time with the matching scales; the lane's weight slots of those
+// groups (one superstep per tile) are loaded at once and kept across passes when one
+// chunk covers I.
+__global__ __launch_bounds__(kPT, 2) void pf_down(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t sH[3][kPR][kDPitch];
+    __shared__ int sE[kPR][kDG];
+    __shared__ float sQ[kPR][kDG];
+    __shared__ __attribute__((aligned(16))) float2 sS[kDG][kDR];
+    const int nq = (a.D + kDR - 1) / kDR, ngI = a.I / kGS, nch = (ngI + kDG - 1) / kDG;
+    int e, u, p0, p1, pos0, n;
+    if (!pf_unit(a, nq, e, u, p0, p1, pos0, n)) return;
+    const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const ExpertRec rec = a.rec[e];
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(rec.wd, (uint32_t)a.D * a.rbD);
+    const int P = a.S * a.K + a.S;
+    const __amdgpu_buffer_rsrc_t hr = buf_rsrc(a.hd, (uint32_t)(3u * P * a.I));
+    const int rbase = u * kDR + wave * 64;   // first row of the wave
+    constexpr int kHS = 3 * kPR * kDG * kGS / 16 / kPT;   // 16-byte staging chunks per thread (12)
+    uint4 wv[kDT][kDG];
+    for (int pass = p0; pass < p1; pass++) {
+        const int r0 = pass * kPR, nr = min(kPR, n - r0), ntt = nr > 16 ? 2 : 1;
+        // staging chunk k = tid + kPT i of the 3 x 32 x 32 16-byte chunks: plane k / 1024,
+        // row (k / 32) % 32 = (tid / 32 + 8 i) % 32, columns 16 (k % 32)
+        int hrow[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) hrow[i] = pos0 + r0 + min(((tid >> 5) + 8 * i) & 31, nr - 1);
+        float facc[kDT][2][4];
+#pragma unroll
+        for (int t = 0; t < kDT; t++)
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) facc[t][tt][r] = 0.f;
+        for (int ch = 0; ch < nch; ch++) {
+            const int gb = ch * kDG;
+            uint4 hv[kHS];
+#pragma unroll
+            for (int i = 0; i < kHS; i++) {
+                const int k = tid + kPT * i, col = gb * kGS + 16 * (k & 31);
+                hv[i] = buf_load16<kCached>(hr, col < a.I ? (uint32_t)((k >> 10) * P + hrow[i & 3]) * a.I + col : kOOB);
+            }
+            int re = 0;
+            float rq = 0.f;
+            if (tid < kPR * kDG) {
+                const int g = min(gb + (tid & 3), ngI - 1);
+                const size_t o = (size_t)(pos0 + r0 + min(tid >> 2, nr - 1)) * ngI + g;
+                re = a.he[o];
+                rq = a.hsum[o];
+            }
+            float2 sv[kDG];
+#pragma unroll
+            for (int i = 0; i < kDG; i++) {   // scales: entry v = tid + kPT i -> row v / 4, group v % 4
+                const int v = tid + kPT * i, row = u * kDR + (v >> 2), g = gb + (v & 3);
+                sv[i] = row < a.D && g < ngI ? ((const float2 *)rec.sd)[(size_t)row * ngI + g] : make_float2(0.f, 0.f);
+            }
+            if (nch > 1 || pass == p0) {   // the superstep ch of each tile's rows
+#pragma unroll
+                for (int t = 0; t < kDT; t++) {
+                    const int row = rbase + 16 * t + j;
+                    pf_wload(wr, row < a.D ? (uint32_t)(row * a.rbD + q * 16 + 128 * ch) : kOOB, (uint32_t)a.nlD * 16, wv[t]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kHS; i++) {
+                const int k = tid + kPT * i;
+                *(uint4 *)&sH[k >> 10][(k >> 5) & 31][16 * (k & 31)] = hv[i];
+            }
+            if (tid < kPR * kDG) {
+                sE[tid >> 2][tid & 3] = re - 4;   // the sums carry 16 (pf_a16)
+                sQ[tid >> 2][tid & 3] = rq;
+            }
+#pragma unroll
+            for (int i = 0; i < kDG; i++) {
+                const int v = tid + kPT * i;
+                sS[v & 3][v >> 2] = sv[i];
+            }
+            __syncthreads();
+            if (nch > 1 || pass == p0)
+#pragma unroll
+                for (int t = 0; t < kDT; t++) pf_wgroups(wv[t]);   // once per load; kept for later passes
+            constexpr int TP = 2;   // two row tiles share each B read
+#pragma unroll
+            for (int tp = 0; tp < kDT / TP; tp++) {
+#pragma unroll
+                for (int gl = 0; gl < kDG; gl++) {
+                    if (gb + gl >= ngI) continue;   // uniform
+                    pf_v4i av[TP][2];   // [tile][half]
+#pragma unroll
+                    for (int i = 0; i < TP; i++) {
+                        av[i][0] = pf_a16(wv[TP * tp + i][gl].x, wv[TP * tp + i][gl].y);
+                        av[i][1] = pf_a16(wv[TP * tp + i][gl].z, wv[TP * tp + i][gl].w);
+                    }
+                    pf_v4i iacc[TP][2][3];   // [tile][x tile][digit]
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                        for (int d = 0; d < 3; d++)
+#pragma unroll
+                            for (int tt = 0; tt < 2; tt++) {
+                                if (tt >= ntt) continue;   // uniform
+                                const pf_v4i bv =
+                                    *(const pf_v4i *)&sH[d][tt * 16 + j][gl * kGS + 32 * kq + 16 * hh];
+#pragma unroll
+                                for (int i = 0; i < TP; i++)
+                                    iacc[i][tt][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                        av[i][hh], bv, hh ? iacc[i][tt][d] : pf_v4i{0, 0, 0, 0}, 0, 0, 0);
+                            }
+                    float2 sz[TP][4];
+#pragma unroll
+                    for (int i = 0; i < TP; i++) {
+                        const float4 *sz4 = (const float4 *)&sS[gl][wave * 64 + 16 * (TP * tp + i) + 4 * q];
+                        const float4 za = sz4[0], zb = sz4[1];
+                        sz[i][0] = make_float2(za.x, za.y);
+                        sz[i][1] = make_float2(za.z, za.w);
+                        sz[i][2] = make_float2(zb.x, zb.y);
+                        sz[i][3] = make_float2(zb.z, zb.w);
+                    }
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++) {
+                        if (tt >= ntt) continue;
+                        const int xe = sE[tt * 16 + j][gl];
+                        const float xs = sQ[tt * 16 + j][gl];
+#pragma unroll
+                        for (int i = 0; i < TP; i++) pf_fold(iacc[i][tt], sz[i], xe, xs, facc[TP * tp + i][tt]);
+                    }
+                }
+            }
+            __syncthreads();   // the staging buffers are refilled by the next chunk or pass
+        }
+        // y rows rbase + 16 t + 4 q .. + 3 of position r0 + 16 tt + j
+#pragma unroll
+        for (int t = 0; t < kDT; t++) {
+            const int row = rbase + 16 * t + 4 * q;
+            if (row >= a.D) continue;
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                const int x = tt * 16 + j;
+                if (tt < ntt && x < nr)
+                    *(float4 *)&a.y[(size_t)(pos0 + r0 + x) * a.D + row] =
+                        make_float4(facc[t][tt][0], facc[t][tt][1], facc[t][tt][2], facc[t][tt][3]);
             }
         }
     }
@@ -385,9 +705,10 @@ __global__ __launch_bounds__(256) void pf_gemm(PfGemm a) {
 
 // ---------------------------------------------------------------- combine
 // out[t] = sum over t's K experts in ascending expert id of w * y[pos] + shgt * y_sh[t]
+// (c/qwen.c:1144, 1159-1161); float4 columns, all K + 1 rows in flight.
 __global__ __launch_bounds__(256) void pf_combine(const float *__restrict__ y, const int *tidx, const float *tval,
                                                   const float *tshg, const int *ppos, int S, int K, int D,
-                                                  float *out) {
+                                                  float *__restrict__ out) {
     const int t = blockIdx.x;
     int ord[kTopK];
     int nk = 0;
@@ -399,15 +720,33 @@ __global__ __launch_bounds__(256) void pf_combine(const float *__restrict__ y, c
         }
         ord[j] = k;
     }
+    const float *row[kTopK];
+    float w[kTopK];
+#pragma unroll
+    for (int i = 0; i < kTopK; i++) {
+        const int k = i < K ? ord[i] : 0;
+        row[i] = y + (size_t)ppos[t * K + k] * D;
+        w[i] = tval[t * K + k];
+    }
     const float shg = tshg[t];
     const float *ysh = y + (size_t)(S * K + t) * D;
-    for (int c = threadIdx.x; c < D; c += 256) {
-        float acc = 0.f;
-        for (int i = 0; i < K; i++) {
-            const int k = ord[i];
-            acc = acc + tval[t * K + k] * y[(size_t)ppos[t * K + k] * D + c];
-        }
-        out[(size_t)t * D + c] = acc + shg * ysh[c];
+    for (int c = 4 * threadIdx.x; c < D; c += 4 * 256) {
+        float4 v[kTopK];
+#pragma unroll
+        for (int i = 0; i < kTopK; i++)
+            if (i < K) v[i] = *(const float4 *)(row[i] + c);
+        const float4 s = *(const float4 *)(ysh + c);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < kTopK; i++)
+            if (i < K) {
+                acc.x = acc.x + w[i] * v[i].x;
+                acc.y = acc.y + w[i] * v[i].y;
+                acc.z = acc.z + w[i] * v[i].z;
+                acc.w = acc.w + w[i] * v[i].w;
+            }
+        *(float4 *)(out + (size_t)t * D + c) =
+            make_float4(acc.x + shg * s.x, acc.y + shg * s.y, acc.z + shg * s.z, acc.w + shg * s.w);
     }
 }
 
@@ -431,8 +770,14 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     if (K < 1 || K > kTopK || K > E || E > kMaxE) return false;
     if (router->I != m.D || router->O != E || (router->fmt != 0 && router->fmt != 1) || router->layout != kLayoutRows)
         return false;
+    if (router->row_bytes % (router->fmt == 0 ? 16 : 4)) return false;
     if (m.gs != kGS || m.D % kGS || m.I % kGS || m.D > 4096 || m.I > 4096) return false;
-    const int D = m.D, I = m.I, np = S * K, P = np + S, ngD = D / m.gs, ngI = I / m.gs;
+    const int D = m.D, I = m.I, np = S * K, P = np + S, ngD = D / kGS, ngI = I / kGS;
+    if ((size_t)3 * S * D >= (1u << 31) || (size_t)3 * P * I >= (1u << 31) || (size_t)P * D >= (1u << 31)) return false;
+    // router split-K: slices of Dk columns (a multiple of 32) until about 512 blocks
+    const int tiles = ((S + kLT - 1) / kLT) * ((E + kLE - 1) / kLE);
+    int KS = 1;
+    while (KS < 8 && D % (2 * KS * kLC) == 0 && tiles * KS < 512) KS *= 2;
     // scratch layout
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -440,67 +785,55 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
         o += al256(bytes);
         return at;
     };
-    const size_t o_lg = take((size_t)S * (E + 1) * 4), o_ti = take((size_t)np * 4), o_tv = take((size_t)np * 4),
-                 o_sh = take((size_t)S * 4), o_cnt = take((size_t)(E + 1) * 4), o_off = take((size_t)(E + 1) * 4),
-                 o_pl = take((size_t)np * 4), o_pp = take((size_t)np * 4), o_rk = take((size_t)np * 4),
-                 o_xd = take((size_t)3 * S * D), o_xe = take((size_t)S * ngD * 4), o_xs = take((size_t)S * ngD * 4),
-                 o_h = take((size_t)P * I * 4), o_hd = take((size_t)3 * P * I), o_he = take((size_t)P * ngI * 4),
-                 o_hs = take((size_t)P * ngI * 4), o_y = take((size_t)P * D * 4);
+    const size_t o_pt = take((size_t)KS * S * E * 8), o_ti = take((size_t)np * 4), o_tv = take((size_t)np * 4),
+                 o_sh = take((size_t)S * 4), o_off = take((size_t)(E + 1) * 4), o_pl = take((size_t)np * 4),
+                 o_pp = take((size_t)np * 4), o_rk = take((size_t)np * 4), o_xd = take((size_t)3 * S * D),
+                 o_xe = take((size_t)S * ngD * 4), o_xs = take((size_t)S * ngD * 4), o_h = take((size_t)P * I * 4),
+                 o_hd = take((size_t)3 * P * I),
+                 o_he = take((size_t)P * ngI * 4), o_hs = take((size_t)P * ngI * 4), o_y = take((size_t)P * D * 4);
     if (!scratch(&g_pf.buf, &g_pf.cap, o)) return false;
     uint8_t *b = (uint8_t *)g_pf.buf;
-    float *lg = (float *)(b + o_lg), *tv = d_val ? d_val : (float *)(b + o_tv), *tsh = (float *)(b + o_sh);
-    int *ti = d_idx ? d_idx : (int *)(b + o_ti), *cnt = (int *)(b + o_cnt), *off = (int *)(b + o_off);
+    double *part = (double *)(b + o_pt);
+    float *tv = d_val ? d_val : (float *)(b + o_tv), *tsh = (float *)(b + o_sh);
+    int *ti = d_idx ? d_idx : (int *)(b + o_ti), *off = (int *)(b + o_off);
     int *pl = (int *)(b + o_pl), *pp = (int *)(b + o_pp), *rk = (int *)(b + o_rk);
-    int8_t *xd = (int8_t *)(b + o_xd), *hd = (int8_t *)(b + o_hd);
-    int *xe = (int *)(b + o_xe), *he = (int *)(b + o_he);
-    float *xsum = (float *)(b + o_xs), *hsum = (float *)(b + o_hs), *h = (float *)(b + o_h), *y = (float *)(b + o_y);
 
-    hipLaunchKernelGGL(pf_logits, dim3((S + kLT - 1) / kLT, (E + 1 + kLE - 1) / kLE), dim3(256), 0, st, d_xs, S, D,
-                       router->w, router->sz, router->fmt, router->row_bytes, E, shg, lg);
-    hipLaunchKernelGGL(pf_route, dim3(S), dim3(kThreads), 0, st, lg, E, K, ti, tv, tsh);
-    hipLaunchKernelGGL(pf_group, dim3(1), dim3(1024), (size_t)(E + 1) * 4, st, ti, np, E, cnt, off, pl, pp, rk);
-    hipLaunchKernelGGL(pf_digits, dim3((S + 3) / 4), dim3(256), 0, st, d_xs, S, D, m.gs, xd, xe, xsum);
-    PfGemm gu;
-    memset(&gu, 0, sizeof(gu));
-    gu.rec = rec;
-    gu.off = off;
-    gu.E = E;
-    gu.S = S;
-    gu.K = K;
-    gu.Kdim = D;
-    gu.O = I;
-    gu.ng = ngD;
-    gu.nl = m.nlG;
-    gu.rb = m.rbG;
-    gu.planes = xd;
-    gu.ge = xe;
-    gu.gsum = xsum;
-    gu.prow = S;
-    gu.plist = pl;
-    gu.out = h;
-    const int nbu = (I + kRowBlk - 1) / kRowBlk, nbd = (D + kRowBlk - 1) / kRowBlk;
-    const int passes_sh = (S + 16 * kTT - 1) / (16 * kTT);
-    const size_t lds_gu = (size_t)2 * kRowBlk * ngD * sizeof(float2), lds_dn = (size_t)kRowBlk * ngI * sizeof(float2);
-    hipLaunchKernelGGL(pf_gemm<1>, dim3(E * nbu, 2), dim3(256), lds_gu, st, gu);
-    gu.shared = 1;
-    hipLaunchKernelGGL(pf_gemm<1>, dim3(nbu, passes_sh), dim3(256), lds_gu, st, gu);
-    hipLaunchKernelGGL(pf_digits, dim3((P + 3) / 4), dim3(256), 0, st, h, P, I, m.gs, hd, he, hsum);
-    PfGemm dn = gu;
-    dn.shared = 0;
-    dn.Kdim = I;
-    dn.O = D;
-    dn.ng = ngI;
-    dn.nl = m.nlD;
-    dn.rb = m.rbD;
-    dn.planes = hd;
-    dn.ge = he;
-    dn.gsum = hsum;
-    dn.prow = P;
-    dn.out = y;
-    hipLaunchKernelGGL(pf_gemm<0>, dim3(E * nbd, 2), dim3(256), lds_dn, st, dn);
-    dn.shared = 1;
-    hipLaunchKernelGGL(pf_gemm<0>, dim3(nbd, passes_sh), dim3(256), lds_dn, st, dn);
-    hipLaunchKernelGGL(pf_combine, dim3(S), dim3(256), 0, st, y, ti, tv, tsh, pp, S, K, D, d_out);
+    hipLaunchKernelGGL(pf_logits, dim3((S + kLT - 1) / kLT, (E + kLE - 1) / kLE, KS), dim3(256), 0, st, d_xs, S, D,
+                       router->w, router->fmt, router->row_bytes, E, D / KS, part);
+    PfArgs a;
+    memset(&a, 0, sizeof(a));
+    a.rec = rec;
+    a.off = off;
+    a.plist = pl;
+    a.E = E;
+    a.S = S;
+    a.K = K;
+    a.D = D;
+    a.I = I;
+    a.nlG = m.nlG;
+    a.rbG = m.rbG;
+    a.nlD = m.nlD;
+    a.rbD = m.rbD;
+    a.nsp = (S + kPR - 1) / kPR;
+    a.xd = (const int8_t *)(b + o_xd);
+    a.xe = (const int *)(b + o_xe);
+    a.xsum = (const float *)(b + o_xs);
+    a.h = (float *)(b + o_h);
+    a.hd = (const int8_t *)(b + o_hd);
+    a.he = (const int *)(b + o_he);
+    a.hsum = (const float *)(b + o_hs);
+    a.y = (float *)(b + o_y);
+    hipLaunchKernelGGL(pf_route, dim3(S), dim3(kThreads), 0, st, part, KS, d_xs, S, D, router->sz, router->fmt, shg, E,
+                       K, ti, tv, tsh, (int8_t *)(b + o_xd), (int *)(b + o_xe), (float *)(b + o_xs));
+    hipLaunchKernelGGL(pf_group, dim3(1), dim3(1024), 0, st, ti, np, E, off, pl, pp, rk);
+    const int E8 = (E + 7) & ~7;
+    auto blocks = [&](int nu) { return ((nu * a.nsp + 7) & ~7) + nu * E8; };
+    const int nh = I / kGU, nq = (D + kDR - 1) / kDR;
+    hipLaunchKernelGGL(pf_gateup, dim3(blocks(nh)), dim3(kPT), (size_t)ngD * 2 * kGU * sizeof(float2), st, a);
+    hipLaunchKernelGGL(pf_digits, dim3((P * (I / 8) + 255) / 256), dim3(256), 0, st, a.h, P, I, (int8_t *)(b + o_hd),
+                       (int *)(b + o_he), (float *)(b + o_hs));
+    hipLaunchKernelGGL(pf_down, dim3(blocks(nq)), dim3(kPT), 0, st, a);
+    hipLaunchKernelGGL(pf_combine, dim3(S), dim3(256), 0, st, a.y, ti, tv, tsh, pp, S, K, D, d_out);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail("moe prefill launch", err);
     return true;

@@ -39,7 +39,7 @@ def check(orc, L, K, xs, S, got):
     assert worst <= TOL, worst
 
 
-@pytest.mark.parametrize("S,K", [(1, 4), (37, 4), (64, 8)])
+@pytest.mark.parametrize("S,K", [(1, 4), (37, 4), (64, 8), (200, 8)])
 def test_prefill_small(lib, orc, gen, torch_dev, S, K):
     import torch
     L = Layer(lib, gen, 0x9F1, 256, 128, 32, 128)
