@@ -111,16 +111,17 @@ constexpr int kLT = 64, kLE = 64, kLC = 32;
 __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, int S, int D,
                                                  const uint8_t *__restrict__ rw, int rfmt, int rrb, int E, int Dk,
                                                  double *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) float s_x[2][kLC][kLT];
-    __shared__ __attribute__((aligned(16))) float s_w[2][kLC][kLE];
+    __shared__ __attribute__((aligned(16))) float s_x[2][kLC][kLT + 4];   // +4: fewer conflicts on the transposed stores
+    __shared__ __attribute__((aligned(16))) float s_w[2][kLC][kLE + 4];
     const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
     const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE, kz = blockIdx.z * Dk;
     float4 rx[2], rv[2];
-    // staging: row r = idx % 64 of the tile, columns 4 (idx / 64) .. + 3, idx = tid + 256 s
+    // staging: row r = idx / 8 of the tile, columns 4 (idx % 8) .. + 3, idx = tid + 256 s
+    // (8 lanes read 128 contiguous bytes of a row)
     auto load = [&](int kc) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int idx = tid + 256 * s, r = idx & 63, k = kz + kc + 4 * (idx >> 6);
+            const int idx = tid + 256 * s, r = idx >> 3, k = kz + kc + 4 * (idx & 7);
             const int t = t0 + r, e = e0 + r;
             rx[s] = t < S ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
             if (e >= E) {
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, i
     auto store = [&](int buf) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int idx = tid + 256 * s, r = idx & 63, c = 4 * (idx >> 6);
+            const int idx = tid + 256 * s, r = idx >> 3, c = 4 * (idx & 7);
             s_x[buf][c][r] = rx[s].x;
             s_x[buf][c + 1][r] = rx[s].y;
             s_x[buf][c + 2][r] = rx[s].z;
@@ -299,7 +300,7 @@ struct PfArgs {
 // dealt to the 8 XCDs round-robin by index) and share its rows of x in that L2.
 // False for an idle block (or a routed expert without rows).
 __device__ __forceinline__ bool pf_unit(const PfArgs &a, int nu, int &e, int &u, int &p0, int &p1, int &pos0,
-                                        int &n) {
+                                        int &n, ExpertRec &rec) {
     const int b = blockIdx.x, nsu = nu * a.nsp, nsu8 = (nsu + 7) & ~7;
     if (b < nsu) {
         e = a.E;
@@ -308,6 +309,7 @@ __device__ __forceinline__ bool pf_unit(const PfArgs &a, int nu, int &e, int &u,
         p1 = p0 + 1;
         pos0 = a.S * a.K;
         n = a.S;
+        rec = a.rec[e];
         return true;
     }
     if (b < nsu8) return false;
@@ -315,6 +317,7 @@ __device__ __forceinline__ bool pf_unit(const PfArgs &a, int nu, int &e, int &u,
     u = rest % nu;
     e = 8 * (rest / nu) + xcd;
     if (e >= a.E) return false;
+    rec = a.rec[e];   // loaded with the offsets: one round trip
     pos0 = a.off[e];
     n = a.off[e + 1] - pos0;
     p0 = 0;
@@ -378,18 +381,19 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
     float2 *sS = (float2 *)sS4;
     const int nh = a.I / kGU, ngD = a.D / kGS, nss = (ngD + 3) / 4;
     int e, u, p0, p1, pos0, n;
-    if (!pf_unit(a, nh, e, u, p0, p1, pos0, n)) return;
+    ExpertRec rec;
+    if (!pf_unit(a, nh, e, u, p0, p1, pos0, n, rec)) return;
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const ExpertRec rec = a.rec[e];
-    {   // scales of rows kGU u .. + kGU - 1 of gate and up, regrouped by group
-        const float2 *sg = (const float2 *)rec.sg + (size_t)u * kGU * ngD, *su = (const float2 *)rec.su + (size_t)u * kGU * ngD;
-        for (int v = tid; v < kGU * ngD; v += kPT) {
-            const int r = v / ngD, g = v - r * ngD;
-            sS[(2 * g) * kGU + r] = sg[v];
-            sS[(2 * g + 1) * kGU + r] = su[v];
-        }
-    }
+    // scales of rows kGU u .. + kGU - 1 of gate and up, regrouped by group in LDS: the first
+    // kSV entries per thread are loaded with the first pass's x row and weights
+    const float2 *sgp = (const float2 *)rec.sg + (size_t)u * kGU * ngD, *sup = (const float2 *)rec.su + (size_t)u * kGU * ngD;
+    constexpr int kSV = 2;
+    auto s_store = [&](int v, float2 gv, float2 uv) {
+        const int r = v / ngD, g = v - r * ngD;
+        sS[(2 * g) * kGU + r] = gv;
+        sS[(2 * g + 1) * kGU + r] = uv;
+    };
     const __amdgpu_buffer_rsrc_t wr[2] = {buf_rsrc(rec.wg, (uint32_t)a.I * a.rbG), buf_rsrc(rec.wu, (uint32_t)a.I * a.rbG)};
     const uint32_t abase = (uint32_t)((u * kGU + wave * 16 + j) * a.rbG + q * 16), whalf = (uint32_t)a.nlG * 16;
     auto w_load = [&](int S, uint4 (&d)[2][4]) {
@@ -409,11 +413,21 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
     };
     for (int pass = p0; pass < p1; pass++) {
         const int r0 = pass * kPR, nr = min(kPR, n - r0), ntt = nr > 16 ? 2 : 1;
-        int xrow;
-        {
-            const int i = r0 + min(sr, nr - 1);
-            xrow = e == a.E ? i : a.plist[pos0 + i] / a.K;
-        }
+        // issue order: this thread's row of x (the dependent chain), the first weights,
+        // the scales (first pass), then the x digits once the row is known
+        const int xi = r0 + min(sr, nr - 1);
+        const int xpair = e == a.E ? xi : a.plist[pos0 + xi];
+        uint4 W[2][4];
+        w_load(0, W);
+        float2 sv[kSV][2];
+        if (pass == p0)
+#pragma unroll
+            for (int i = 0; i < kSV; i++) {
+                const int v = tid + kPT * i;
+                sv[i][0] = v < kGU * ngD ? sgp[v] : make_float2(0.f, 0.f);
+                sv[i][1] = v < kGU * ngD ? sup[v] : make_float2(0.f, 0.f);
+            }
+        const int xrow = e == a.E ? xpair : xpair / a.K;
         auto x_load = [&](int S, XStage &st) {
 #pragma unroll
             for (int gl = 0; gl < 4; gl++) {
@@ -436,10 +450,14 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
                 sQ[sg4][sr] = st.s;
             }
         };
+        if (pass == p0) {   // the scales arrive with the x row: storing them first costs no wait
+#pragma unroll
+            for (int i = 0; i < kSV; i++)
+                if (tid + kPT * i < kGU * ngD) s_store(tid + kPT * i, sv[i][0], sv[i][1]);
+            for (int v = tid + kPT * kSV; v < kGU * ngD; v += kPT) s_store(v, sgp[v], sup[v]);   // D > 2048
+        }
         XStage xst;
         x_load(0, xst);
-        uint4 W[2][4];
-        w_load(0, W);
         x_store(xst);
         __syncthreads();
         // the tile count as a compile-time constant: no branches between the LDS reads
@@ -567,10 +585,10 @@ __global__ __launch_bounds__(kPT, 2) void pf_down(PfArgs a) {
     __shared__ __attribute__((aligned(16))) float2 sS[kDG][kDR];
     const int nq = (a.D + kDR - 1) / kDR, ngI = a.I / kGS, nch = (ngI + kDG - 1) / kDG;
     int e, u, p0, p1, pos0, n;
-    if (!pf_unit(a, nq, e, u, p0, p1, pos0, n)) return;
+    ExpertRec rec;
+    if (!pf_unit(a, nq, e, u, p0, p1, pos0, n, rec)) return;
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const ExpertRec rec = a.rec[e];
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(rec.wd, (uint32_t)a.D * a.rbD);
     const int P = a.S * a.K + a.S;
     const __amdgpu_buffer_rsrc_t hr = buf_rsrc(a.hd, (uint32_t)(3u * P * a.I));
@@ -774,10 +792,10 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     if (m.gs != kGS || m.D % kGS || m.I % kGS || m.D > 4096 || m.I > 4096) return false;
     const int D = m.D, I = m.I, np = S * K, P = np + S, ngD = D / kGS, ngI = I / kGS;
     if ((size_t)3 * S * D >= (1u << 31) || (size_t)3 * P * I >= (1u << 31) || (size_t)P * D >= (1u << 31)) return false;
-    // router split-K: slices of Dk columns (a multiple of 32) until about 512 blocks
+    // router split-K: slices of Dk columns (a multiple of 32) until about 1024 blocks
     const int tiles = ((S + kLT - 1) / kLT) * ((E + kLE - 1) / kLE);
     int KS = 1;
-    while (KS < 8 && D % (2 * KS * kLC) == 0 && tiles * KS < 512) KS *= 2;
+    while (KS < 16 && D % (2 * KS * kLC) == 0 && tiles * KS < 1024) KS *= 2;
     // scratch layout
     size_t o = 0;
     auto take = [&](size_t bytes) {
