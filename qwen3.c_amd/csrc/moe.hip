@@ -15,9 +15,9 @@
 //   T  softmax / top-k / renorm / shared gate -> route (tagged)
 //   Gk routed gate/up rows  -> h[k]   (wait for route)
 //   D  down rows of all K+1 experts + weighted combine -> out   (wait for route, then h)
-// Block b runs tile b; when the grid is smaller than the tile list, finished blocks take
-// further tiles from an atomic counter.  A tile only waits for tiles of smaller index,
-// which blocks of smaller index hold (workgroups are dispatched in index order).
+// Block b runs tile b, one block per tile.  A tile only waits for tiles of smaller index,
+// which blocks of smaller index hold (workgroups are dispatched in index order), so the
+// launch makes progress however many blocks are resident at once.
 //
 // Cross-block data are 64-bit words {epoch, value} written and read with agent-scope
 // atomics (single-copy atomic, coherent across the XCDs' L2s): a consumer polls until the
@@ -57,7 +57,6 @@ struct MoeArgs {
     unsigned long long *tagv;             // logits [E + 1] | route [kRouteReps][kRouteStride] |
                                           // h [(K + 1) * I] | y [(K + 1) * D]
                                           // (logit E = the shared-expert gate dot)
-    unsigned *tickets;                    // [2]
     unsigned *done;                       // [2][2][kMaxSlots] G, then D tiles finished per slot, by
                                           // launch parity; kCounterStride apart
     int *err;
@@ -508,7 +507,6 @@ __device__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
 template <int LPRG, int TPRD>
 __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     __shared__ MoeLds S;
-    __shared__ int s_ticket, s_xvalid;
     __shared__ int s_e[1];
     __shared__ ExpertRec s_rec[1];
     __shared__ float s_w[kMaxSlots];
@@ -520,43 +518,31 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     const int nR = (a.E + 1 + kRRows - 1) / kRRows;
     const int tGs = nR, tDsh = tGs + a.nG, tT = tDsh + a.nD, tGk = tT + 1, tDk = tGk + K * a.nG;
     const int tC = tDk + K * a.nD, total = tC + a.nC;
-    if (blockIdx.x == 0 && threadIdx.x == 0)   // the previous launch's ticket counter is free now
-        __hip_atomic_store(&a.tickets[(a.epoch + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (blockIdx.x == 0 && threadIdx.x < 2 * kMaxSlots)   // and so are its per-slot counters
+    if (blockIdx.x == 0 && threadIdx.x < 2 * kMaxSlots)   // the previous launch's per-slot counters are free now
         __hip_atomic_store(counter(a, a.epoch + 1, threadIdx.x / kMaxSlots, threadIdx.x % kMaxSlots), 0u,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) s_xvalid = 0;
-    __syncthreads();
-    int t = blockIdx.x;
-    while (t < total) {
-        const bool gtile = (t >= tGs && t < tDsh) || (t >= tGk && t < tDk);
-        if (gtile && !s_xvalid) {   // x digits for the G tiles of this block
-            XRegs xr, wr;
-            const int ncols = g.nlG * kLaneChunks * 32;
-            prep_load(a.x, g.D, ncols, xr);
-            if (a.xw) {   // post-attention norm of the residual (c/qwen.c:326-330)
-                prep_load(a.xw, g.D, ncols, wr);
-                norm_apply(xr, wr, g.D, ncols, a.eps, s_red);
-            }
-            prep_x(xr, g.gs, ncols, S.x);
-            if (threadIdx.x == 0) s_xvalid = 1;
+    // One block per tile (the host launches exactly that many): straight-line code, so
+    // nothing tile-specific is computed up front and kept live across the other tile kinds.
+    const int t = blockIdx.x;
+    if (t >= total) return;
+    const bool gtile = (t >= tGs && t < tDsh) || (t >= tGk && t < tDk);
+    if (gtile) {   // x digits for the G tiles
+        XRegs xr, wr;
+        const int ncols = g.nlG * kLaneChunks * 32;
+        prep_load(a.x, g.D, ncols, xr);
+        if (a.xw) {   // post-attention norm of the residual (c/qwen.c:326-330)
+            prep_load(a.xw, g.D, ncols, wr);
+            norm_apply(xr, wr, g.D, ncols, a.eps, s_red);
         }
-        if (t < tGs) tile_router(a, t * kRRows, s_red, S.n.xn, S.n.wn);
-        else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
-        else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
-        else if (t == tT) tile_route(a, S.r);
-        else if (t < tDk) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
-        else if (t < tC) tile_dslot<TPRD>(a, S.h, (t - tDk) / a.nD, ((t - tDk) % a.nD) * kDRows, s_rec);
-        else tile_combine(a, (t - tC) * kCRows, s_w);
-        if ((int)gridDim.x >= total) break;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            s_ticket = (int)gridDim.x + (int)atomicAdd(&a.tickets[a.epoch & 1], 1u);
-            if (!gtile) s_xvalid = 0;   // the LDS union was reused
-        }
-        __syncthreads();
-        t = s_ticket;
+        prep_x(xr, g.gs, ncols, S.x);
     }
+    if (t < tGs) tile_router(a, t * kRRows, s_red, S.n.xn, S.n.wn);
+    else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
+    else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
+    else if (t == tT) tile_route(a, S.r);
+    else if (t < tDk) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
+    else if (t < tC) tile_dslot<TPRD>(a, S.h, (t - tDk) / a.nD, ((t - tDk) % a.nD) * kDRows, s_rec);
+    else tile_combine(a, (t - tC) * kCRows, s_w);
 }
 
 // ---------------------------------------------------------------- expert table
@@ -575,7 +561,7 @@ static EgTable g_eg;
 struct MoeScratch {
     void *tag = nullptr;
     size_t tag_cap = 0;
-    void *misc = nullptr;         // tickets [2] at 0, err at 64, per-slot counters from 256
+    void *misc = nullptr;         // err at 64, per-slot counters from 256
     size_t misc_cap = 0;
     uint32_t epoch = 0;
 };
@@ -633,16 +619,9 @@ struct LaunchMoe {
         a.nG = (a.g.I + a.gRows - 1) / a.gRows;
         a.nD = (a.g.D + kDRows - 1) / kDRows;
         a.nC = (a.g.D + kCRows - 1) / kCRows;
-        static int per = 0;
-        if (!per) {
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, kThreads, 0) != hipSuccess || per < 1)
-                per = 1;
-        }
         const int nR = (a.E + 1 + kRRows - 1) / kRRows;
         const long tiles = nR + (long)(a.K + 1) * (a.nG + a.nD) + 1 + a.nC;
-        long nb = (long)n_cu() * per;
-        if (nb > tiles) nb = tiles;
-        hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kThreads), 0, st, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail("moe launch", e);
         return true;
@@ -694,7 +673,6 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.idx_out = d_idx;
     a.val_out = d_val;
     a.tagv = (unsigned long long *)g_ms.tag;
-    a.tickets = (unsigned *)g_ms.misc;
     a.err = (int *)((uint8_t *)g_ms.misc + 64);
     a.done = (unsigned *)((uint8_t *)g_ms.misc + 256);
     a.epoch = g_ms.epoch;
