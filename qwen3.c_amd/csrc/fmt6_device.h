@@ -196,6 +196,16 @@ __device__ void block_topk_merge(float (&tv)[K], int (&ti)[K], int k, float *out
 }
 
 // ---------------------------------------------------------------- x -> digit planes
+// Workgroup barrier for LDS traffic: orders this block's LDS accesses only.  A
+// __syncthreads() carries a workgroup fence over all address spaces, which on gfx950 also
+// waits for every global load in flight; the x preparation runs while the weight loads
+// issued before it are still outstanding, so its barriers must not wait for them.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct XPrep {
     uint32_t limb[kLaneMaxI / 8][kLimbs];   // [word][digit]
     int qsum[kLaneMaxI / 32];               // per 32-column chunk: sum of q
@@ -205,7 +215,7 @@ struct XPrep {
 // ncols: columns to prepare (a multiple of 32 covering every lane's chunks, <= kLaneMaxI);
 // columns at or past I are zero.  Each thread owns whole 8-column words: it loads its
 // x values once (all loads in flight together), publishes one max per word, then turns
-// them into digit planes.  NT = threads of the block.  Ends with __syncthreads().
+// them into digit planes.  NT = threads of the block.  Ends with an LDS barrier.
 template <int NT>
 struct XRegsT {
     static constexpr int kWords = (kLaneMaxI / 8 + NT - 1) / NT;   // words per thread
@@ -213,23 +223,27 @@ struct XRegsT {
 };
 using XRegs = XRegsT<kThreads>;
 // Issue the x loads (split from prep_x so that they can go out before other loads).
+// Buffer loads with out-of-range offsets for the missing columns: no branches, so the
+// compiler can wait for exactly these loads and not for the weight loads issued after.
 template <int NT = kThreads>
 __device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, int ncols, XRegsT<NT> &xr) {
     const int tid = threadIdx.x, nwords = ncols / 8;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x), (short)0, I * 4, 0x00020000);
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
             const int i = w * 8 + c;
-            xr.v[k][c] = (w < nwords && i < I) ? x[i] : 0.f;
+            xr.v[k][c] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(r, w < nwords ? i * 4 : (int)0x80000000, 0, 0));
         }
     }
 }
 
 // x := x r (1 + w) with r = 1 / sqrt(mean(x^2) + eps) over the I columns (zero-centred
 // RMSNorm, c/qwen.c:326-330: double sum of squares; the multiplications in the reference's
-// order).  xr, wr as loaded by prep_load; all threads call (two barriers).
+// order).  xr, wr as loaded by prep_load; all threads call (two LDS barriers).
 template <int NT = kThreads>
 __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr, int I, int ncols, float eps,
                                            double *s_red) {
@@ -239,9 +253,9 @@ __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr,
 #pragma unroll
         for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];   // zeros past I add 0
     ss = wave_sum_dpp(ss);
-    __syncthreads();
+    lds_barrier();
     if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
-    __syncthreads();
+    lds_barrier();
     double t = 0;
     for (int w = 0; w < NT / 64; w++) t += s_red[w];
     const float r = 1.f / sqrtf((float)(t / I) + eps);
@@ -261,7 +275,7 @@ __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P)
     const auto &xv = xr.v;
     for (int g = tid; g < ngrp; g += NT) P.gmax[g] = 0u;
     for (int c = tid; c < nch; c += NT) P.qsum[c] = 0;
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
@@ -270,7 +284,7 @@ __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P)
         for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(xv[k][c]));
         if (w < nwords) atomicMax(&P.gmax[(w * 8) / gs], __float_as_uint(m));
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
@@ -294,7 +308,7 @@ __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P)
         }
         atomicAdd(&P.qsum[w >> 2], qs);
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 __device__ __forceinline__ int group_exp22(const XPrep &P, int g) {

@@ -124,13 +124,15 @@ __device__ __forceinline__ void xf_load(XRegs &ar, XRegs &br, const ProjArgs &a,
     if constexpr (XF == XF_GATED) {
         prep_load(a.z, a.I, ncols, ar);
         const int tid = threadIdx.x, nwords = ncols / 8;
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(a.xw, (uint32_t)a.VD * 4);
 #pragma unroll
-        for (int k = 0; k < XRegs::kWords; k++) {
+        for (int k = 0; k < XRegs::kWords; k++) {   // unconditional loads, as prep_load
             const int w = tid + k * kThreads;
 #pragma unroll
             for (int c = 0; c < 8; c++) {
                 const int i = w * 8 + c;
-                br.v[k][c] = (w < nwords && i < a.I) ? a.xw[i % a.VD] : 0.f;
+                br.v[k][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           r, (w < nwords && i < a.I) ? (i % a.VD) * 4 : (int)kOOB, 0, 0));
             }
         }
     }
@@ -173,14 +175,13 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
     const int gbase = blockIdx.x * kWaves + wave;
     uint4 wq[U][kLaneChunks];
     float2 sv[U][LaneX<CU>::NU];
-    auto load = [&](int u, int g) {
-        if (g < a.ngroups) {
-            const SegSel s = seg_of(a, g);
-            const uint32_t r = (uint32_t)((g - s.g0) * RPW + sg);
-            const uint32_t wtot = (uint32_t)s.O * (uint32_t)a.row_bytes, stot = (uint32_t)s.O * srb;
-            lane_load<CU>(buf_rsrc(s.w, wtot), buf_rsrc(s.sz, stot), min(r * (uint32_t)a.row_bytes, wtot),
-                          min(r * srb, stot), L, wq[u], sv[u]);
-        }
+    auto load = [&](int u, int g) {   // unconditional: out-of-range offsets past the last group
+        const bool on = g < a.ngroups;
+        const SegSel s = seg_of(a, on ? g : a.ngroups - 1);
+        const uint32_t r = (uint32_t)((on ? g - s.g0 : 0) * RPW + sg);
+        const uint32_t wtot = (uint32_t)s.O * (uint32_t)a.row_bytes, stot = (uint32_t)s.O * srb;
+        lane_load<CU>(buf_rsrc(s.w, wtot), buf_rsrc(s.sz, stot), on ? min(r * (uint32_t)a.row_bytes, wtot) : kOOB,
+                      on ? min(r * srb, stot) : kOOB, L, wq[u], sv[u]);
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load(u, gbase + u * nw);
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     constexpr int kVPer = kAttMaxHD / kThreads;    // head dims per thread in P.V
     __shared__ __attribute__((aligned(16))) float s_q[kAttMaxG][kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_k[kAttMaxHD];
-    __shared__ float s_p[kAttMaxG][kAttT];
+    __shared__ __attribute__((aligned(16))) float s_p[kAttMaxG][kAttT];
     __shared__ float s_m[kAttMaxG], s_l[kAttMaxG];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.H / a.KH, hd = a.hd;
@@ -490,34 +491,54 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
         for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
     }
     __syncthreads();
-    // scores: 16 lanes per position, 4 positions per wave step
+    // scores: 16 lanes per position, 4 positions per wave step; each q fragment is read
+    // from LDS once for all the wave's steps
 #pragma unroll
     for (int st = 0; st < kSteps; st++) {
         const int t = t0 + (st * kWaves + wave) * 4 + pl;
-        const bool valid = t < t1;
-        if (valid && t == a.pos)
+        if (t < t1 && t == a.pos)
 #pragma unroll
             for (int e = 0; e < DPL; e++) kv[st][e] = s_k[part * DPL + e];
-        for (int gg = 0; gg < G; gg++) {
-            float s = 0.f;
+    }
+    for (int gg = 0; gg < G; gg++) {
+        float qf[DPL];
 #pragma unroll
-            for (int e = 0; e < DPL; e++) s = fmaf(s_q[gg][part * DPL + e], kv[st][e], s);
-            s = seg_sum<16>(s);
-            if (part == 15 && valid) s_p[gg][t - t0] = s * a.scale;
+        for (int e = 0; e < DPL; e += 4) {
+            const float4 q4 = *(const float4 *)&s_q[gg][part * DPL + e];
+            qf[e] = q4.x;
+            qf[e + 1] = q4.y;
+            qf[e + 2] = q4.z;
+            qf[e + 3] = q4.w;
+        }
+#pragma unroll
+        for (int st = 0; st < kSteps; st++) {
+            const int t = t0 + (st * kWaves + wave) * 4 + pl;
+            float sc = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) sc = fmaf(qf[e], kv[st][e], sc);
+            sc = seg_sum<16>(sc);
+            if (part == 15 && t < t1) s_p[gg][t - t0] = sc * a.scale;
         }
     }
     __syncthreads();
-    if (tid < G) {   // chunk max and sum of exp per head
-        float m = -INFINITY;
-        for (int t = 0; t < n; t++) m = fmaxf(m, s_p[tid][t]);
-        float l = 0.f;
-        for (int t = 0; t < n; t++) {
-            const float p = expf(s_p[tid][t] - m);
-            s_p[tid][t] = p;
-            l += p;
+    // chunk max and sum of exp per head: 32 lanes per head, lane = position; positions past
+    // the chunk get p = 0
+    static_assert(kAttT == 32, "one position per lane of a half wave");
+    for (int gg = tid >> 5; gg < G; gg += kThreads / 32) {
+        const int t = tid & 31;
+        const float sc = t < n ? s_p[gg][t] : -INFINITY;
+        float m = sc;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float pv = t < n ? expf(sc - m) : 0.f;
+        float l = pv;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        s_p[gg][t] = pv;
+        if (t == 0) {
+            s_m[gg] = m;
+            s_l[gg] = l;
         }
-        s_m[tid] = m;
-        s_l[tid] = l;
     }
     __syncthreads();
     // P.V: thread d of the head dims, all G heads
@@ -525,19 +546,19 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < kVPer; i++) {   // guarded bodies, no breaks: the loops unroll fully
         const int d = tid + i * kThreads;
-        float acc[kAttMaxG];
+        if (i * kThreads >= hd) continue;   // uniform
+        for (int gg = 0; gg < G; gg++) {   // p as float4 broadcasts, positions in order
+            float acc = 0.f;
 #pragma unroll
-        for (int gg = 0; gg < kAttMaxG; gg++) acc[gg] = 0.f;
-#pragma unroll
-        for (int t = 0; t < kAttT; t++)
-            if (t < n)
-#pragma unroll
-                for (int gg = 0; gg < kAttMaxG; gg++)
-                    if (gg < G) acc[gg] = fmaf(s_p[gg][t], vv[t][i], acc[gg]);
-        if (d < hd)
-#pragma unroll
-            for (int gg = 0; gg < kAttMaxG; gg++)
-                if (gg < G) pb[(size_t)gg * (hd + 2) + d] = acc[gg];
+            for (int t4 = 0; t4 < kAttT; t4 += 4) {
+                const float4 p = *(const float4 *)&s_p[gg][t4];
+                acc = fmaf(p.x, vv[t4][i], acc);
+                acc = fmaf(p.y, vv[t4 + 1][i], acc);
+                acc = fmaf(p.z, vv[t4 + 2][i], acc);
+                acc = fmaf(p.w, vv[t4 + 3][i], acc);
+            }
+            if (d < hd) pb[(size_t)gg * (hd + 2) + d] = acc;
+        }
     }
     if (tid < G) {
         pb[(size_t)tid * (hd + 2) + hd] = s_m[tid];
