@@ -19,26 +19,32 @@ class Layer:
                            lib.tensor(d[0], d[1], 6, I, D, gs)))
         self.router = lib.tensor(self.mw.router, None, 0, D, E)
 
+    def int8_router(self, lib, gen, base):
+        """An int8 (fmt 1) router [E, D] uploaded, and its exact f32 equivalent q * s
+        (_util.int8_rows)."""
+        q, s, f = _util.int8_rows(gen, base, self.E, self.D)
+        return lib.tensor(q.view(np.uint8).reshape(-1), s, 1, self.D, self.E), f
+
     def register(self, lib, layer):
         for e in range(self.E):
             lib.eg_table_set(layer, e, *self.t[e])
         lib.eg_table_set_shared(layer, *self.t[self.E], self.mw.sh_gate)
 
-    def oracle(self, orc, x, K):
+    def oracle(self, orc, x, K, router=None):
         out = np.empty(self.D, np.float32)
         idx = np.empty(K, np.int32)
         val = np.empty(K, np.float32)
         shgt = np.empty(1, np.float32)
-        orc.orc_moe_decode(P(x), P(self.mw.router), eptr(self.ex), eptr(self.ex, self.E), P(self.mw.sh_gate),
+        orc.orc_moe_decode(P(x), P(self.mw.router if router is None else router), eptr(self.ex), eptr(self.ex, self.E), P(self.mw.sh_gate),
                            self.D, self.I, self.E, K, self.gs, P(out), P(idx), P(val), P(shgt), None)
         return out, idx, val, float(shgt[0])
 
-    def oracle_prefill(self, orc, xs, S, K):
+    def oracle_prefill(self, orc, xs, S, K, router=None):
         """moe_batch_from_logits (c/qwen.c:1050-1183) restated: out [S, D], ids/weights [S, K]."""
         out = np.empty(S * self.D, np.float32)
         tidx = np.empty(S * K, np.int32)
         tval = np.empty(S * K, np.float32)
-        orc.orc_moe_prefill(P(xs), S, P(self.mw.router), eptr(self.ex), eptr(self.ex, self.E), P(self.mw.sh_gate),
+        orc.orc_moe_prefill(P(xs), S, P(self.mw.router if router is None else router), eptr(self.ex), eptr(self.ex, self.E), P(self.mw.sh_gate),
                             self.D, self.I, self.E, K, self.gs, P(out), P(tidx), P(tval))
         return out, tidx, tval
 

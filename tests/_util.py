@@ -135,6 +135,19 @@ def expert_seed(gen, base, layer, eid):
     return gen.stream(base, 1000 + layer * 4096 + eid)
 
 
+def int8_rows(gen, base, O, I, sigma=0.02):
+    """int8 rows q [O, I] with per-row power-of-two scales s, and f = q * s as f32 [O*I].
+    With s = 2^-k the fmt-1 product (sum x*q, then * s, c/qwen.c:230-238) equals the f32
+    dot with rows q * s bit for bit: scaling by a power of two commutes with every rounding
+    of the sum (nothing overflows or underflows at these magnitudes), so an f32 oracle pins
+    an int8 path."""
+    s = np.ldexp(np.ones(O, np.float32), -(11 + np.arange(O) % 3)).astype(np.float32)
+    w = gen.normal(O * I, gen.stream(base, 30), sigma).reshape(O, I)
+    q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
+    f = (q.astype(np.float32) * s[:, None]).astype(np.float32).reshape(-1)
+    return q, s, f
+
+
 class MoeWeights:
     """One MoE layer: f32 router [E, D], E fmt-6 experts + shared, f32 sh_gate [D]."""
 

@@ -20,13 +20,13 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def run_moe(lib, torch, dev, layer, L, K, x, accumulate=False, resid=None):
+def run_moe(lib, torch, dev, layer, L, K, x, accumulate=False, resid=None, router=None):
     dx = torch.from_numpy(x).to(dev)
     dout = torch.from_numpy(resid.copy()).to(dev) if resid is not None else torch.full((L.D,), np.nan, device=dev)
     didx = torch.full((K,), -1, dtype=torch.int32, device=dev)
     dval = torch.zeros(K + 1, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
-    lib.moe_decode_dev(layer, L.router, K, dx.data_ptr(), dout.data_ptr(), accumulate, didx.data_ptr(),
+    lib.moe_decode_dev(layer, L.router if router is None else router, K, dx.data_ptr(), dout.data_ptr(), accumulate, didx.data_ptr(),
                        dval.data_ptr())
     lib.sync()
     return dout.cpu().numpy(), didx.cpu().numpy(), dval.cpu().numpy()
@@ -53,8 +53,8 @@ def moe_f64(L, x, idx, val, shgt):
     return out
 
 
-def check(orc, L, K, x, got, tol=TOL, f64=False):
-    out, idx, val, shgt = L.oracle(orc, x, K)
+def check(orc, L, K, x, got, tol=TOL, f64=False, router=None):
+    out, idx, val, shgt = L.oracle(orc, x, K, router)
     gout, gidx, gval = got
     assert np.array_equal(gidx, idx), (gidx, idx)
     np.testing.assert_allclose(gval[:K], val, rtol=1e-5, atol=1e-7)
@@ -134,6 +134,19 @@ def test_moe_router_ties(lib, orc, gen, torch_dev):
         x = gen.normal(D, 0x400 + t)
         got = run_moe(lib, torch, torch_dev, 0, L, K, x)
         check(orc, L, K, x, got)
+    assert lib.moe_error() == 0
+
+
+@pytest.mark.parametrize("K", [4, 8])
+def test_moe_router_int8(lib, orc, gen, torch_dev, small, K):
+    """fmt 1 router (int8 rows, per-row scale applied after the dot, c/qwen.c:230-238), the
+    format the reference uploads for the router when it quantises to int8."""
+    import torch
+    L = small.activate()[0]
+    rt, rf = L.int8_router(lib, gen, 0x1A8)
+    for t in range(6):
+        x = gen.normal(L.D, 0x1A9 + t)
+        check(orc, L, K, x, run_moe(lib, torch, torch_dev, 0, L, K, x, router=rt), router=rf)
     assert lib.moe_error() == 0
 
 

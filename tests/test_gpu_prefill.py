@@ -18,19 +18,19 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def run_prefill(lib, torch, dev, L, K, xs, S):
+def run_prefill(lib, torch, dev, L, K, xs, S, router=None):
     dxs = torch.from_numpy(xs).to(dev)
     dout = torch.full((S * L.D,), np.nan, device=dev)
     didx = torch.full((S * K,), -1, dtype=torch.int32, device=dev)
     dval = torch.zeros(S * K, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
-    lib.moe_prefill_dev(0, L.router, K, dxs.data_ptr(), S, dout.data_ptr(), didx.data_ptr(), dval.data_ptr())
+    lib.moe_prefill_dev(0, L.router if router is None else router, K, dxs.data_ptr(), S, dout.data_ptr(), didx.data_ptr(), dval.data_ptr())
     lib.sync()
     return dout.cpu().numpy(), didx.cpu().numpy(), dval.cpu().numpy()
 
 
-def check(orc, L, K, xs, S, got):
-    out, tidx, tval = L.oracle_prefill(orc, xs, S, K)
+def check(orc, L, K, xs, S, got, router=None):
+    out, tidx, tval = L.oracle_prefill(orc, xs, S, K, router)
     gout, gidx, gval = got
     assert np.array_equal(gidx, tidx), np.nonzero(gidx != tidx)[0][:10]
     np.testing.assert_allclose(gval, tval, rtol=1e-5, atol=1e-7)
@@ -46,6 +46,17 @@ def test_prefill_small(lib, orc, gen, torch_dev, S, K):
     Table(lib, [L]).activate()
     xs = gen.normal(S * L.D, 0x9F2 + S)
     check(orc, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S))
+
+
+@pytest.mark.parametrize("S", [1, 64, 200])
+def test_prefill_router_int8(lib, orc, gen, torch_dev, S):
+    """fmt 1 router: int8 rows, the per-row scale applied after the dot (c/qwen.c:230-238)."""
+    import torch
+    L = Layer(lib, gen, 0x9F1, 256, 128, 32, 128)
+    Table(lib, [L]).activate()
+    rt, rf = L.int8_router(lib, gen, 0x9F3)
+    xs = gen.normal(S * L.D, 0x9F4 + S)
+    check(orc, L, 8, xs, S, run_prefill(lib, torch, torch_dev, L, 8, xs, S, router=rt), router=rf)
 
 
 @pytest.fixture(scope="module")
@@ -65,3 +76,12 @@ def test_prefill_cfg4(lib, orc_omp, gen, torch_dev, cfg4):
     check(orc_omp, L, K, xs, S, got)
     counts = np.bincount(got[1], minlength=L.E)
     assert counts.max() > 8 and (counts == 0).sum() < L.E   # ragged groups
+
+
+def test_prefill_cfg4_router_int8(lib, orc_omp, gen, torch_dev, cfg4):
+    """configs[4] shape with an int8 (fmt 1) router: the split-K router pass over int8 rows."""
+    import torch
+    L, K, S = cfg4.activate()[0], 8, 64
+    rt, rf = L.int8_router(lib, gen, 0xC0F6)
+    xs = gen.normal(S * L.D, 0xC0F7)
+    check(orc_omp, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S, router=rt), router=rf)

@@ -8,7 +8,7 @@ a swapped nibble order, a wrong group index, ties resolved to the higher index) 
 import numpy as np
 import pytest
 
-from _util import P, brute_fmt6, eptr, maxrel, normrel
+from _util import P, brute_fmt6, eptr, int8_rows, maxrel, normrel
 
 
 def gemv(orc, q, sz, x, I, O, gs):
@@ -126,6 +126,26 @@ def route(orc, logits, K):
     val = np.empty(K, np.float32)
     orc.orc_route_topk(P(pr), pr.size, K, P(idx), P(val))
     return idx, val, pr
+
+
+def test_int8_pow2_scale_equals_f32(orc, gen):
+    """The GPU tests check an int8 (fmt 1) router against the f32 oracle on rows q * s
+    with s = 2^-k: the two products must agree bit for bit, and a scale applied to the
+    wrong row or dropped must not."""
+    E, D, S = 32, 256, 4
+    q, s, f = int8_rows(gen, 0x1A8, E, D)
+    assert len(set(s.tolist())) == 3
+    for t in range(S):
+        x = gen.normal(D, 0x1B0 + t)
+        y8, yf = np.empty(E, np.float32), np.empty(E, np.float32)
+        orc.orc_matmul_q8(P(y8), P(x), P(q.view(np.uint8)), P(s), D, E)
+        orc.orc_matmul_f32(P(yf), P(x), P(f), 1, D, E)
+        assert np.array_equal(y8, yf)
+        y64 = (q.astype(np.float64) @ x.astype(np.float64)) * s
+        assert maxrel(y8, y64) < 1e-4
+        ys = np.empty(E, np.float32)
+        orc.orc_matmul_q8(P(ys), P(x), P(q.view(np.uint8)), P(np.roll(s, 1)), D, E)
+        assert not np.allclose(ys, yf, rtol=1e-3)
 
 
 def test_route_invariants(orc, gen):
