@@ -14,8 +14,8 @@
 // weights.
 //
 // Top-k (fused): each wave keeps the k best of its rows in registers and publishes them as
-// epoch-tagged 64-bit keys; the last block of the grid merges the waves in the same launch,
-// polling the tags (agent-scope atomics: no device-scope fences, no second launch).
+// epoch-tagged 64-bit keys; the first block of the grid to finish merges them in the same
+// launch, polling the tags (agent-scope atomics: no device-scope fences, no second launch).
 #include "fmt6_device.h"
 
 #include <stdio.h>
@@ -154,6 +154,13 @@ __device__ __forceinline__ unsigned long long wave_max_key(unsigned long long k)
     return ((unsigned long long)mh << 32) | ml;
 }
 
+// lane l's 64-bit value, wave uniform
+__device__ __forceinline__ unsigned long long readlane64(unsigned long long v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 // compare-exchange of 64-bit keys: a gets the larger
 __device__ __forceinline__ void cx_desc(unsigned long long &a, unsigned long long &b) {
     const unsigned long long hi = a > b ? a : b, lo = a > b ? b : a;
@@ -170,8 +177,19 @@ __device__ __forceinline__ unsigned long long wave_rounds(unsigned long long (&L
     unsigned long long out = pad;
 #pragma unroll
     for (int r = 0; r < kTopK; r++) {
-        const unsigned long long m = wave_max_key(L[0]);
-        const int w = __ffsll((long long)__ballot(L[0] == m)) - 1;
+        // the head with the largest value bits (key bits 55:24) wins; only when several
+        // heads share them does the full 64-bit maximum (row order) decide
+        const uint32_t h = (uint32_t)(L[0] >> 24);
+        const uint32_t mh = wave_umax32(h);
+        const unsigned long long tied = __ballot(h == mh);
+        int w;
+        if (__popcll(tied) == 1) {
+            w = __ffsll((long long)tied) - 1;
+        } else {
+            const unsigned long long mt = wave_max_key(h == mh ? L[0] : 0ull);
+            w = __ffsll((long long)__ballot(L[0] == mt)) - 1;
+        }
+        const unsigned long long m = readlane64(L[0], w);
         if (lane == w) {
 #pragma unroll
             for (int q = 0; q + 1 < N; q++) L[q] = L[q + 1];
@@ -182,8 +200,11 @@ __device__ __forceinline__ unsigned long long wave_rounds(unsigned long long (&L
     return out;
 }
 
-// The block that arrives last: the k best keys of the launch from the blocks' sorted lists
-// (cand[b * kTopK + e]; nblk <= kThreads).  Thread t polls block t's list; each wave takes
+// The block that arrives first: the k best keys of the launch from the blocks' sorted lists
+// (cand[b * kTopK + e]; nblk <= kThreads).  Thread t polls block t's list until its keys
+// carry the launch's tag, so the merge ends soon after the last block's keys land (a last
+// block that merged would first wait for its arrival count to return); the other blocks
+// wait on nothing, so every list arrives.  Each wave takes
 // kTopK rounds of a wave maximum over its lanes' list heads (the lane whose head wins
 // moves to its next key), and the 4 wave lists are ranked in LDS.  Keys of another launch
 // carry another tag and are polled until overwritten.
@@ -304,8 +325,8 @@ __global__ void argmax_reset(unsigned long long *slots) {
 //           results in LDS, and every kTkBuf rows (and at the end) the wave selects the new
 //           list from them and the old list by kTopK rounds of a wave maximum.  At the end
 //           the block ranks its waves' lists into one list that it stores as tagged keys
-//           and counts itself in; the block that arrives last merges the blocks' lists
-//           (topk_final_block).
+//           and counts itself in; the block that arrives first merges the blocks' lists
+//           as they land (topk_final_block).
 // The grid is persistent with few waves per CU (COLI_GEMV_BPC blocks): with U row steps
 // of every wave in flight that keeps ~8-10 MB of loads outstanding chip-wide, where HBM
 // streams best (more outstanding requests only add DRAM page conflicts).
@@ -427,17 +448,17 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
     if constexpr (MODE == 2) {   // the block's list: rank the waves' lists in LDS
         __shared__ __attribute__((aligned(16))) unsigned long long s_wl[kWaves * kTopK];
         __shared__ unsigned long long s_bl[kTopK];
-        __shared__ int s_last;
+        __shared__ int s_merge;
         if (lane < kTopK) s_wl[wave * kTopK + lane] = tl;
         rank_keys(s_wl, kWaves * kTopK, pad, s_bl);
         if (threadIdx.x < kTopK)
             __hip_atomic_store(tk.slots + (size_t)blockIdx.x * kTopK + threadIdx.x, s_bl[threadIdx.x],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0)   // arrival count of this launch (the merge still checks every tag)
-            s_last = __hip_atomic_fetch_add(topk_counter(tk, tk.epoch), 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+        if (threadIdx.x == 0)   // arrival count of this launch: the first block merges
+            s_merge = __hip_atomic_fetch_add(topk_counter(tk, tk.epoch), 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) == 0;
         __syncthreads();
-        if (s_last) topk_final_block(tk, gridDim.x);
+        if (s_merge) topk_final_block(tk, gridDim.x);
     }
 }
 
