@@ -206,8 +206,17 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Digit plane l holds the digit-l nibbles of x word w (8 columns) at xprep_pos(w): the
+// words of host chunk h (4 each) sit in slot h % kLaneChunks of lane h / kLaneChunks, the
+// lanes of one slot side by side, so lane_x's 16-byte reads of consecutive lanes are
+// consecutive in LDS (a word-major layout, 96 bytes per chunk, put 8-16 lanes on one bank).
+constexpr int kXLanes = kLaneMaxI / (32 * kLaneChunks);   // lanes of a row, at most
+__device__ __forceinline__ int xprep_pos(int w) {
+    const int h = w >> 2;
+    return ((h % kLaneChunks) * kXLanes + h / kLaneChunks) * 4 + (w & 3);
+}
 struct XPrep {
-    uint32_t limb[kLaneMaxI / 8][kLimbs];   // [word][digit]
+    __attribute__((aligned(16))) uint32_t limb[kLimbs][kLaneMaxI / 8];   // [digit][xprep_pos(word)]
     int qsum[kLaneMaxI / 32];               // per 32-column chunk: sum of q
     unsigned gmax[kLaneMaxI / 32];          // per group (gs >= 32): bits of max |x|
 };
@@ -304,7 +313,7 @@ __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P)
             uint32_t lw = 0;
 #pragma unroll
             for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
-            P.limb[w][l] = lw ^ 0x88888888u;   // (d + 8) ^ 8 == d mod 16
+            P.limb[l][xprep_pos(w)] = lw ^ 0x88888888u;   // (d + 8) ^ 8 == d mod 16
         }
         atomicAdd(&P.qsum[w >> 2], qs);
     }
@@ -371,10 +380,17 @@ __device__ __forceinline__ void lane_geo(int j, int nl, int I, int gs, LaneX<CU>
 
 template <int CU>
 __device__ __forceinline__ void lane_x(const XPrep &P, int gs, LaneX<CU> &L) {
+    const int j = L.ch0 / kLaneChunks;
 #pragma unroll
-    for (int w = 0; w < kLaneWords; w++)
+    for (int c = 0; c < kLaneChunks; c++)
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) L.lm[w][l] = P.limb[L.ch0 * 4 + w][l];
+        for (int l = 0; l < kLimbs; l++) {
+            const uint4 v = *(const uint4 *)&P.limb[l][(c * kXLanes + j) * 4];
+            L.lm[c * 4 + 0][l] = v.x;
+            L.lm[c * 4 + 1][l] = v.y;
+            L.lm[c * 4 + 2][l] = v.z;
+            L.lm[c * 4 + 3][l] = v.w;
+        }
 #pragma unroll
     for (int q = 0; q < LaneX<CU>::NU; q++) {
         const int ch = L.ch0 + q * CU;

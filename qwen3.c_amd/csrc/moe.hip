@@ -74,8 +74,11 @@ __device__ __forceinline__ void tag_put(unsigned long long *p, uint32_t epoch, f
     __hip_atomic_store(p, ((unsigned long long)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
+// The error flag is read on every 16th poll only: each read is one more memory round trip
+// between a poll and the next.
 __device__ __forceinline__ bool poll_give_up(int *err, int polls) {
-    if (polls > kPollLimit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    if (polls > kPollLimit ||
+        ((polls & 15) == 15 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     }
@@ -108,39 +111,44 @@ __device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t e
 
 // ---------------------------------------------------------------- h -> digit planes
 // The down projection uses the same integer-dot arithmetic as the GEMV (fmt6_device.h)
-// with h in place of x: per slot s, limb[s * I/8 + word][digit], qsum[s * I/32 + chunk],
-// gmax[s * ngI + group] (the down tiles prepare one slot, s = 0).
+// with h (one slot) in place of x: digit planes limb[digit][hprep_pos(word)], qsum[chunk],
+// gmax[group].  hprep_pos puts host chunk h = 2 jj + c (the chunk a down thread reads, see
+// down_thread) at slot c, lane jj, lanes of a slot side by side: the 16-byte reads of a
+// row's threads are consecutive in LDS.
+constexpr int kHLanes = kMoeMaxI / 64;
+__device__ __forceinline__ int hprep_pos(int w) {
+    const int h = w >> 2;
+    return ((h & 1) * kHLanes + (h >> 1)) * 4 + (w & 3);
+}
 struct HPrep {
-    uint32_t limb[kMoeMaxI / 8][kLimbs];
+    __attribute__((aligned(16))) uint32_t limb[kLimbs][kMoeMaxI / 8];
     int qsum[kMoeMaxI / 32];
     unsigned gmax[kMoeMaxI / 64];
 };
 constexpr int kHWords = (kMoeMaxI / 8 + kThreads - 1) / kThreads;
 
-// v: the thread's words q = tid + k * kThreads (8 columns each) of the NS x I values.
+// v: the thread's words q = tid + k * kThreads (8 columns each) of the I values.
 // Ends with __syncthreads().
-__device__ void prep_h(const float (&v)[kHWords][8], int NS, int I, int gs, int ngI, HPrep &H) {
-    const int tid = threadIdx.x, wpr = I / 8, nw = NS * wpr;
-    for (int i = tid; i < NS * ngI; i += kThreads) H.gmax[i] = 0u;
-    for (int i = tid; i < NS * (I / 32); i += kThreads) H.qsum[i] = 0;
+__device__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
+    const int tid = threadIdx.x, nw = I / 8;
+    for (int i = tid; i < I / gs; i += kThreads) H.gmax[i] = 0u;
+    for (int i = tid; i < I / 32; i += kThreads) H.qsum[i] = 0;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kHWords; k++) {
         const int q = tid + k * kThreads;
         if (q >= nw) continue;
-        const int s = q / wpr, w = q - s * wpr;
         float m = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(v[k][c]));
-        atomicMax(&H.gmax[s * ngI + (w * 8) / gs], __float_as_uint(m));
+        atomicMax(&H.gmax[(q * 8) / gs], __float_as_uint(m));
     }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kHWords; k++) {
         const int q = tid + k * kThreads;
         if (q >= nw) continue;
-        const int s = q / wpr, w = q - s * wpr;
-        const float m = __uint_as_float(H.gmax[s * ngI + (w * 8) / gs]);
+        const float m = __uint_as_float(H.gmax[(q * 8) / gs]);
         const int e = m > 0.f ? ilogbf(m) + 1 : 0;
         uint32_t u[8];
         int qs = 0;
@@ -155,9 +163,9 @@ __device__ void prep_h(const float (&v)[kHWords][8], int NS, int I, int gs, int 
             uint32_t lw = 0;
 #pragma unroll
             for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
-            H.limb[q][l] = lw ^ 0x88888888u;
+            H.limb[l][hprep_pos(q)] = lw ^ 0x88888888u;
         }
-        atomicAdd(&H.qsum[s * (I / 32) + w / 4], qs);
+        atomicAdd(&H.qsum[q / 4], qs);
     }
     __syncthreads();
 }
@@ -183,22 +191,26 @@ __device__ __forceinline__ DownThread down_thread(const MoeGeom &g) {
     return d;
 }
 
-// partial of one chunk: s * (2^(e-22) T - (z - 8) sum(h~)) over its 32 columns of slot s
-__device__ __forceinline__ float down_chunk(const HPrep &H, int s, int I, int gs, int ngI, const DownThread &d,
-                                            const uint4 &w, const float2 &sz) {
-    const uint32_t *lb = H.limb[s * (I / 8) + d.h * 4];
+// partial of one chunk: s * (2^(e-22) T - (z - 8) sum(h~)) over its 32 columns
+__device__ __forceinline__ float down_chunk(const HPrep &H, int gs, const DownThread &d, const uint4 &w,
+                                            const float2 &sz) {
+    const int pos = ((d.h & 1) * kHLanes + (d.h >> 1)) * 4;
     const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
     int t[kLimbs] = {0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int l = 0; l < kLimbs; l++) t[l] = __builtin_amdgcn_sdot8((int)wv[q], (int)lb[q * kLimbs + l], t[l], false);
+    for (int l = 0; l < kLimbs; l++) {
+        const uint4 hv = *(const uint4 *)&H.limb[l][pos];
+        t[l] = __builtin_amdgcn_sdot8((int)wv[0], (int)hv.x, t[l], false);
+        t[l] = __builtin_amdgcn_sdot8((int)wv[1], (int)hv.y, t[l], false);
+        t[l] = __builtin_amdgcn_sdot8((int)wv[2], (int)hv.z, t[l], false);
+        t[l] = __builtin_amdgcn_sdot8((int)wv[3], (int)hv.w, t[l], false);
+    }
     const int lo = t[0] + 16 * t[1] + 256 * t[2];
     const int hi = t[3] + 16 * t[4] + 256 * t[5];
     const float T = fmaf((float)hi, 4096.f, (float)lo);
-    const float m = __uint_as_float(H.gmax[s * ngI + (d.h * 32) / gs]);
+    const float m = __uint_as_float(H.gmax[(d.h * 32) / gs]);
     const int ue = (m > 0.f ? ilogbf(m) + 1 : 0) - 22;
-    const float ucs = ldexpf((float)H.qsum[s * (I / 32) + d.h], ue);
+    const float ucs = ldexpf((float)H.qsum[d.h], ue);
     return sz.x * fmaf(-(sz.y - 8.f), ucs, ldexpf(T, ue));
 }
 
@@ -225,11 +237,11 @@ __device__ __forceinline__ void down_slot(const MoeGeom &g, const ExpertRec &rec
     }
     float hv[kHWords][8];
     gather(hv);
-    prep_h(hv, 1, g.I, g.gs, g.ngI, H);
+    prep_h(hv, g.I, g.gs, H);
 #pragma unroll
     for (int p = 0; p < P; p++) {
         const int r = r0 + (p * kWaves + wave) * RPW + seg;
-        const float y = seg_sum<TPR>(down_chunk(H, 0, g.I, g.gs, g.ngI, d, wq[p], sv[p]));
+        const float y = seg_sum<TPR>(down_chunk(H, g.gs, d, wq[p], sv[p]));
         if (t == TPR - 1 && r < g.D) emit(r, y);
     }
 }
