@@ -225,6 +225,22 @@ struct XPrep {
 // columns at or past I are zero.  Each thread owns whole 8-column words: it loads its
 // x values once (all loads in flight together), publishes one max per word, then turns
 // them into digit planes.  NT = threads of the block.  Ends with an LDS barrier.
+// v[0..8) = the 8 floats at byte offset off of buffer r (two 16-byte loads; dwords out of
+// the buffer's range read 0)
+__device__ __forceinline__ void load8f(__amdgpu_buffer_rsrc_t r, int off, float (&v)[8]) {
+    typedef int v4i_t __attribute__((ext_vector_type(4)));
+    const v4i_t a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    const v4i_t b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+    v[0] = __int_as_float(a.x);
+    v[1] = __int_as_float(a.y);
+    v[2] = __int_as_float(a.z);
+    v[3] = __int_as_float(a.w);
+    v[4] = __int_as_float(b.x);
+    v[5] = __int_as_float(b.y);
+    v[6] = __int_as_float(b.z);
+    v[7] = __int_as_float(b.w);
+}
+
 template <int NT>
 struct XRegsT {
     static constexpr int kWords = (kLaneMaxI / 8 + NT - 1) / NT;   // words per thread
@@ -234,6 +250,8 @@ using XRegs = XRegsT<kThreads>;
 // Issue the x loads (split from prep_x so that they can go out before other loads).
 // Buffer loads with out-of-range offsets for the missing columns: no branches, so the
 // compiler can wait for exactly these loads and not for the weight loads issued after.
+// A thread's word is two 16-byte loads.  Raw buffer loads check the range per dword, so the
+// columns at or past I read 0 also inside a partly covered load.
 template <int NT = kThreads>
 __device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, int ncols, XRegsT<NT> &xr) {
     const int tid = threadIdx.x, nwords = ncols / 8;
@@ -241,12 +259,8 @@ __device__ __forceinline__ void prep_load(const float *__restrict__ x, int I, in
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int i = w * 8 + c;
-            xr.v[k][c] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(r, w < nwords ? i * 4 : (int)0x80000000, 0, 0));
-        }
+        const int off = w < nwords ? w * 32 : (int)0x80000000;
+        load8f(r, off, xr.v[k]);
     }
 }
 

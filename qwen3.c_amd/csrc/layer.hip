@@ -126,14 +126,9 @@ __device__ __forceinline__ void xf_load(XRegs &ar, XRegs &br, const ProjArgs &a,
         const int tid = threadIdx.x, nwords = ncols / 8;
         const __amdgpu_buffer_rsrc_t r = buf_rsrc(a.xw, (uint32_t)a.VD * 4);
 #pragma unroll
-        for (int k = 0; k < XRegs::kWords; k++) {   // unconditional loads, as prep_load
-            const int w = tid + k * kThreads;
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const int i = w * 8 + c;
-                br.v[k][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                           r, (w < nwords && i < a.I) ? (i % a.VD) * 4 : (int)kOOB, 0, 0));
-            }
+        for (int k = 0; k < XRegs::kWords; k++) {   // unconditional loads, as prep_load; VD % 8 == 0,
+            const int w = tid + k * kThreads;          // so a word lies within one head
+            load8f(r, (w < nwords && w * 8 < a.I) ? ((w * 8) % a.VD) * 4 : (int)kOOB, br.v[k]);
         }
     }
 }
