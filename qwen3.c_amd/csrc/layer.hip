@@ -87,6 +87,17 @@ struct ProjArgs {
     int add;           // 1: y[r] += acc (residual add), 0: y[r] = acc
 };
 
+// Sum over aligned groups of n lanes (n a power of two <= 64, wave uniform), in every lane
+// of the group: the xor butterfly's pairing, by DPP within rows of 16 lanes.
+__device__ __forceinline__ double seg_sum_d(double v, int n) {
+    if (n >= 2) v += dpp_d<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    if (n >= 4) v += dpp_d<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    if (n >= 8) v += dpp_d<0x141, 0xF>(v);   // row_half_mirror: the other quad of the 8
+    if (n >= 16) v += dpp_d<0x140, 0xF>(v);  // row_mirror: the other 8 of the row
+    for (int off = 16; off < n; off <<= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
 // XF_NORM: x[i] * r * (1 + w[i]), r = 1/sqrt(mean(x^2) + eps) over the I columns
 // (c/qwen.c:326-330, double sum of squares).  XF_GATED: per head of VD columns,
 // y * r_h * gnorm[d] * silu(z) (c/qwen.c:768-772).  Zero columns past I stay zero.  The
@@ -105,12 +116,13 @@ __device__ __forceinline__ void xf_apply(XRegs &xr, const XRegs &ar, const XRegs
             double ss = 0;
 #pragma unroll
             for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];
-            for (int off = 1; off < wph; off <<= 1) ss += __shfl_xor(ss, off);
+            ss = seg_sum_d(ss, wph);
             const float r = 1.f / sqrtf((float)(ss / a.VD) + a.eps);
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
+            for (int c = 0; c < 8; c++) {   // silu(z) with a hardware reciprocal (< 2 ulp)
                 const int i = w * 8 + c;
-                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * br.v[k][c] * silu_f(ar.v[k][c]);
+                const float z = ar.v[k][c], sz = z * __builtin_amdgcn_rcpf(1.f + expf(-z));
+                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * br.v[k][c] * sz;
             }
         }
     }
