@@ -14,15 +14,16 @@
 //   Gs shared gate/up rows  -> h[K]   (independent of routing: overlaps R and T)
 //   T  softmax / top-k / renorm / shared gate -> route (tagged)
 //   Gk routed gate/up rows  -> h[k]   (wait for route)
-//   D  down rows of all K+1 experts + weighted combine -> out   (wait for route, then h)
+//   D  down rows of one slot -> y[k]   (wait for route, then h)
+//   C  weighted combine of the K+1 y rows -> out   (wait for y)
 // Block b runs tile b, one block per tile.  A tile only waits for tiles of smaller index,
 // which blocks of smaller index hold (workgroups are dispatched in index order), so the
 // launch makes progress however many blocks are resident at once.
 //
 // Cross-block data are 64-bit words {epoch, value} written and read with agent-scope
 // atomics (single-copy atomic, coherent across the XCDs' L2s): a consumer polls until the
-// tag equals the launch epoch.  No counters need ordering, so no device-scope fences (an
-// L2 write-back each on gfx950) are issued.  Polls are bounded: past the limit they set an
+// tag equals the launch epoch.  There are no counters to order, so no device-scope fences
+// (an L2 write-back each on gfx950) are issued.  Polls are bounded: past the limit they set an
 // error flag and give up, so every wave always exits.
 #include "moe_common.h"
 
@@ -37,7 +38,6 @@ constexpr int kGSteps = 2;                // gate/up row steps per tile
 constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
 constexpr int kRouteReps = 16;            // copies of the route block (readers spread over them)
 constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1], K <= 8
-constexpr int kCounterStride = 64;        // u32 counters 256 bytes apart (one per line)
 
 struct MoeArgs {
     const float *x;                       // [D] expert input (post-attention RMSNorm), or the
@@ -57,8 +57,6 @@ struct MoeArgs {
     unsigned long long *tagv;             // logits [E + 1] | route [kRouteReps][kRouteStride] |
                                           // h [(K + 1) * I] | y [(K + 1) * D]
                                           // (logit E = the shared-expert gate dot)
-    unsigned *done;                       // [2][2][kMaxSlots] G, then D tiles finished per slot, by
-                                          // launch parity; kCounterStride apart
     int *err;
     uint32_t epoch;
     int gRows, nG;                        // gate/up rows per tile, tiles per expert
@@ -96,10 +94,6 @@ __device__ __forceinline__ unsigned long long *h_of(const MoeArgs &a, int slot) 
 }
 __device__ __forceinline__ unsigned long long *y_of(const MoeArgs &a, int slot) {
     return h_of(a, a.K + 1) + (size_t)slot * a.g.D;
-}
-// per-slot counters of this launch: which 0 = G tiles done, 1 = D tiles done
-__device__ __forceinline__ unsigned *counter(const MoeArgs &a, uint32_t epoch, int which, int slot) {
-    return a.done + ((size_t)((epoch & 1) * 2 + which) * kMaxSlots + slot) * kCounterStride;
 }
 __device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t epoch, int *err) {
     for (int polls = 0;; polls++) {
@@ -422,16 +416,15 @@ __device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, 
     unsigned long long *hs = h_of(a, slot);
     const uint32_t ep = a.epoch;
     gateup_rows<LPR, CU>(L, rec, g, r0, [&](int r, float h) { tag_put(&hs[r], ep, h); });
-    __syncthreads();
-    if (threadIdx.x == 0)   // a hint for the D tiles (they still check every tag)
-        __hip_atomic_fetch_add(counter(a, a.epoch, 0, slot), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- D and C tiles
-// D: y_s[r] = down_s row r . h_s for one slot and kDRows rows.  The slot's G tiles count
-// themselves when done; the tile waits for that count, then reads the tagged h (words not
-// yet of this launch are read again).  C: out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt
-// y_sh, the reference's order (c/qwen.c:870-877, :917).
+// D: y_s[r] = down_s row r . h_s for one slot and kDRows rows.  The tile polls one h word
+// of each of the slot's G tiles (its last row) until all carry the launch's tag, then reads
+// the whole tagged h (words not yet of this launch are read again): a cheap wait without
+// counters, whose read-modify-writes and polls each added a memory round trip.  C:
+// out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt y_sh, the reference's order
+// (c/qwen.c:870-877, :917), polling its rows' tagged y of every slot directly.
 template <int TPR>
 __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertRec *s_rec) {
     const int tid = threadIdx.x, K = a.K;
@@ -451,15 +444,13 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
     const int nw = a.g.I / 8;
     const uint32_t ep = a.epoch;
     int *err = a.err;
-    const unsigned *done = counter(a, a.epoch, 0, slot);
-    const unsigned nG = (unsigned)a.nG;
     auto gather = [&](float (&hv)[kHWords][8]) {
-        if (tid == 0)
+        if (tid < a.nG) {   // one word per G tile: the tile's last row
+            const int r = min((tid + 1) * a.gRows, a.g.I) - 1;
             for (int polls = 0;; polls++)
-                if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nG ||
-                    poll_give_up(err, polls))
-                    break;
-        __syncthreads();
+                if ((uint32_t)(aload(hs + r) >> 32) == ep || poll_give_up(err, polls)) break;
+        }
+        lds_barrier();   // no wait for the weight loads in flight
         for (int polls = 0;; polls++) {
             bool all = true;
 #pragma unroll
@@ -476,9 +467,6 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
         }
     };
     down_slot<TPR>(a.g, s_rec[0], H, r0, gather, [&](int r, float y) { tag_put(&ys[r], ep, y); });
-    __syncthreads();
-    if (tid == 0)   // a hint for the C tiles (they still check every tag)
-        __hip_atomic_fetch_add(counter(a, a.epoch, 1, slot), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr int kCRows = 64;   // combine tile rows (one thread each)
@@ -486,14 +474,7 @@ __device__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
     const int tid = threadIdx.x, K = a.K, NS = K + 1, D = a.g.D;
     const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
     const unsigned long long *ys = y_of(a, 0);
-    if (tid < NS) {   // the weights, then wait until every slot's D tiles have counted
-        s_w[tid] = tag_get(&route[K + tid], a.epoch, a.err);   // val[0..K), then shgt at K
-        const unsigned *dd = counter(a, a.epoch, 1, tid);
-        for (int polls = 0;; polls++)
-            if (__hip_atomic_load(dd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (unsigned)a.nD ||
-                poll_give_up(a.err, polls))
-                break;
-    }
+    if (tid < NS) s_w[tid] = tag_get(&route[K + tid], a.epoch, a.err);   // val[0..K), then shgt at K
     __syncthreads();
     const int r = r0 + tid;
     if (tid >= kCRows || r >= D) return;
@@ -530,9 +511,6 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     const int nR = (a.E + 1 + kRRows - 1) / kRRows;
     const int tGs = nR, tDsh = tGs + a.nG, tT = tDsh + a.nD, tGk = tT + 1, tDk = tGk + K * a.nG;
     const int tC = tDk + K * a.nD, total = tC + a.nC;
-    if (blockIdx.x == 0 && threadIdx.x < 2 * kMaxSlots)   // the previous launch's per-slot counters are free now
-        __hip_atomic_store(counter(a, a.epoch + 1, threadIdx.x / kMaxSlots, threadIdx.x % kMaxSlots), 0u,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // One block per tile (the host launches exactly that many): straight-line code, so
     // nothing tile-specific is computed up front and kept live across the other tile kinds.
     const int t = blockIdx.x;
@@ -573,7 +551,7 @@ static EgTable g_eg;
 struct MoeScratch {
     void *tag = nullptr;
     size_t tag_cap = 0;
-    void *misc = nullptr;         // err at 64, per-slot counters from 256
+    void *misc = nullptr;         // err at 64
     size_t misc_cap = 0;
     uint32_t epoch = 0;
 };
@@ -664,7 +642,7 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
         if (!T.valid[(size_t)layer * (T.E + 1) + e]) return reject("expert table slot not set");
     const MoeGeom &m = T.geom;
     const size_t ntag = (size_t)T.E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
-    const size_t misc = 256 + (size_t)4 * kMaxSlots * kCounterStride * 4;
+    const size_t misc = 256;
     if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, misc)) return false;
     if (++g_ms.epoch == 0) g_ms.epoch = 2;   // 0 is what fresh scratch holds; keep the parity alternating
     MoeArgs a;
@@ -686,7 +664,6 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.val_out = d_val;
     a.tagv = (unsigned long long *)g_ms.tag;
     a.err = (int *)((uint8_t *)g_ms.misc + 64);
-    a.done = (unsigned *)((uint8_t *)g_ms.misc + 256);
     a.epoch = g_ms.epoch;
     a.g = m;
     return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
