@@ -71,6 +71,22 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
 #define COLI_DPP_UMAX(v, ctrl, rmask) \
     max((v), (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xF, false))
 
+// Maximum over aligned runs of n lanes (n a power of two <= 16, wave uniform), in every
+// lane of the run.  All lanes must be active.
+__device__ __forceinline__ uint32_t run_umax(uint32_t v, int n) {
+    if (n >= 2) v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    if (n >= 4) v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    if (n >= 8) v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    if (n >= 16) v = COLI_DPP_UMAX(v, 0x140, 0xF);  // row_mirror
+    return v;
+}
+// Sum over aligned quads of lanes, in every lane of the quad.  All lanes must be active.
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
 // (value desc, index asc): the order of c/shaders/argmax.comp:28,41 and of the host scan
 // c/qwen.c:1471-1472 (ties resolve to the lowest index).
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
@@ -294,25 +310,33 @@ __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr,
 template <int NT = kThreads>
 __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P) {
     const int tid = threadIdx.x;
-    const int nwords = ncols / 8, nch = ncols / 32, ngrp = (ncols + gs - 1) / gs;
+    const int nwords = ncols / 8, ngrp = (ncols + gs - 1) / gs, wpg = gs / 8;
+    // Word w sits in lane w % 64, so a group of wpg <= 16 words (a power of two) is an
+    // aligned run of lanes: its maximum comes by DPP, and a chunk's q sum (4 words) by a
+    // quad sum, with no LDS round trip.  Other group sizes use LDS atomics.
+    const bool runs = wpg <= 16 && (wpg & (wpg - 1)) == 0;
     const auto &xv = xr.v;
-    for (int g = tid; g < ngrp; g += NT) P.gmax[g] = 0u;
-    for (int c = tid; c < nch; c += NT) P.qsum[c] = 0;
-    lds_barrier();
+    if (!runs) {
+        for (int g = tid; g < ngrp; g += NT) P.gmax[g] = 0u;
+        lds_barrier();
+    }
+    uint32_t mb[XRegsT<NT>::kWords];
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
         float m = 0.f;
 #pragma unroll
-        for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(xv[k][c]));
-        if (w < nwords) atomicMax(&P.gmax[(w * 8) / gs], __float_as_uint(m));
+        for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(xv[k][c]));   // words past ncols hold zeros
+        mb[k] = __float_as_uint(m);
+        if (runs) mb[k] = run_umax(mb[k], wpg);
+        else if (w < nwords) atomicMax(&P.gmax[(w * 8) / gs], mb[k]);
     }
-    lds_barrier();
+    if (!runs) lds_barrier();
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = tid + k * NT;
-        if (w >= nwords) continue;
-        const float m = __uint_as_float(P.gmax[(w * 8) / gs]);
+        const bool on = w < nwords;
+        const float m = runs ? __uint_as_float(mb[k]) : on ? __uint_as_float(P.gmax[(w * 8) / gs]) : 0.f;
         const int e = m > 0.f ? ilogbf(m) + 1 : 0;    // m < 2^e
         uint32_t u[8];
         int qs = 0;
@@ -322,14 +346,18 @@ __device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P)
             qs += q;
             u[c] = (uint32_t)(q + 0x888888);   // balanced digits d -> unsigned nibbles d + 8
         }
+        if (on) {
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-            uint32_t lw = 0;
+            for (int l = 0; l < kLimbs; l++) {
+                uint32_t lw = 0;
 #pragma unroll
-            for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
-            P.limb[l][xprep_pos(w)] = lw ^ 0x88888888u;   // (d + 8) ^ 8 == d mod 16
+                for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
+                P.limb[l][xprep_pos(w)] = lw ^ 0x88888888u;   // (d + 8) ^ 8 == d mod 16
+            }
         }
-        atomicAdd(&P.qsum[w >> 2], qs);
+        qs = quad_sum(qs);
+        if (on && (w & 3) == 0) P.qsum[w >> 2] = qs;
+        if (runs && on && (w & (wpg - 1)) == 0) P.gmax[(w * 8) / gs] = mb[k];
     }
     lds_barrier();
 }

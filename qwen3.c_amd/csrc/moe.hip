@@ -121,28 +121,32 @@ struct HPrep {
 };
 constexpr int kHWords = (kMoeMaxI / 8 + kThreads - 1) / kThreads;
 
-// v: the thread's words q = tid + k * kThreads (8 columns each) of the I values.
-// Ends with __syncthreads().
+// v: the thread's words q = tid + k * kThreads (8 columns each) of the I values (zeros
+// past I).  Group maxima and chunk q sums as in prep_x.  Ends with __syncthreads().
 __device__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
-    const int tid = threadIdx.x, nw = I / 8;
-    for (int i = tid; i < I / gs; i += kThreads) H.gmax[i] = 0u;
-    for (int i = tid; i < I / 32; i += kThreads) H.qsum[i] = 0;
-    __syncthreads();
+    const int tid = threadIdx.x, nw = I / 8, wpg = gs / 8;
+    const bool runs = wpg <= 16 && (wpg & (wpg - 1)) == 0;
+    if (!runs) {
+        for (int i = tid; i < I / gs; i += kThreads) H.gmax[i] = 0u;
+        __syncthreads();
+    }
+    uint32_t mb[kHWords];
 #pragma unroll
     for (int k = 0; k < kHWords; k++) {
         const int q = tid + k * kThreads;
-        if (q >= nw) continue;
         float m = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; c++) m = fmaxf(m, fabsf(v[k][c]));
-        atomicMax(&H.gmax[(q * 8) / gs], __float_as_uint(m));
+        mb[k] = __float_as_uint(m);
+        if (runs) mb[k] = run_umax(mb[k], wpg);
+        else if (q < nw) atomicMax(&H.gmax[(q * 8) / gs], mb[k]);
     }
-    __syncthreads();
+    if (!runs) __syncthreads();
 #pragma unroll
     for (int k = 0; k < kHWords; k++) {
         const int q = tid + k * kThreads;
-        if (q >= nw) continue;
-        const float m = __uint_as_float(H.gmax[(q * 8) / gs]);
+        const bool on = q < nw;
+        const float m = runs ? __uint_as_float(mb[k]) : on ? __uint_as_float(H.gmax[(q * 8) / gs]) : 0.f;
         const int e = m > 0.f ? ilogbf(m) + 1 : 0;
         uint32_t u[8];
         int qs = 0;
@@ -152,14 +156,18 @@ __device__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
             qs += qv;
             u[c] = (uint32_t)(qv + 0x888888);
         }
+        if (on) {
 #pragma unroll
-        for (int l = 0; l < kLimbs; l++) {
-            uint32_t lw = 0;
+            for (int l = 0; l < kLimbs; l++) {
+                uint32_t lw = 0;
 #pragma unroll
-            for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
-            H.limb[l][hprep_pos(q)] = lw ^ 0x88888888u;
+                for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
+                H.limb[l][hprep_pos(q)] = lw ^ 0x88888888u;
+            }
         }
-        atomicAdd(&H.qsum[q / 4], qs);
+        qs = quad_sum(qs);
+        if (on && (q & 3) == 0) H.qsum[q / 4] = qs;
+        if (runs && on && (q & (wpg - 1)) == 0) H.gmax[(q * 8) / gs] = mb[k];
     }
     __syncthreads();
 }
