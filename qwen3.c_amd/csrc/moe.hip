@@ -157,13 +157,10 @@ __device__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
             u[c] = (uint32_t)(qv + 0x888888);
         }
         if (on) {
+            uint32_t lw[kLimbs];
+            digit_planes(u, lw);
 #pragma unroll
-            for (int l = 0; l < kLimbs; l++) {
-                uint32_t lw = 0;
-#pragma unroll
-                for (int c = 0; c < 8; c++) lw |= ((u[c] >> (4 * l)) & 15u) << (4 * c);
-                H.limb[l][hprep_pos(q)] = lw ^ 0x88888888u;
-            }
+            for (int l = 0; l < kLimbs; l++) H.limb[l][hprep_pos(q)] = lw[l];
         }
         qs = quad_sum(qs);
         if (on && (q & 3) == 0) H.qsum[q / 4] = qs;
