@@ -741,23 +741,38 @@ struct SegIn {
     float *y;
 };
 
-constexpr int kProjU = 4;
+// Row steps per wave, all loaded before the first is reduced: the smallest of 2..8 that
+// covers the rows with one block per CU, so every CU streams and no CU runs a second block
+// behind the first (a launch is latency-bound: its x preparation and first loads dominate).
+// Larger projections take 8 and loop.
+static int proj_u(int ngroups) {
+    const long per_step = (long)kWaves * n_cu();
+    const long need = (ngroups + per_step - 1) / per_step;
+    return need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : need <= 5 ? 5 : need <= 6 ? 6 : 8;
+}
 
-template <int LPR, int CU, int XF>
-static bool launch_proj(ProjArgs &a, hipStream_t st) {
-    auto kern = proj_gemv<LPR, CU, kProjU, XF>;
-    static int per = 0;
-    if (!per) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, kThreads, 0) != hipSuccess || per < 1) per = 1;
-    }
-    long nb = ((long)a.ngroups + kWaves * kProjU - 1) / (kWaves * kProjU);
-    const long cap = (long)n_cu() * per;
-    if (nb > cap) nb = cap;
+template <int LPR, int CU, int U, int XF>
+static bool launch_proj_u(ProjArgs &a, hipStream_t st) {
+    auto kern = proj_gemv<LPR, CU, U, XF>;
+    long nb = ((long)a.ngroups + kWaves * U - 1) / (kWaves * U);
+    if (nb > n_cu()) nb = n_cu();
     if (nb < 1) nb = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("projection launch", e);
     return true;
+}
+
+template <int LPR, int CU, int XF>
+static bool launch_proj(ProjArgs &a, hipStream_t st) {
+    switch (proj_u(a.ngroups)) {
+    case 2: return launch_proj_u<LPR, CU, 2, XF>(a, st);
+    case 3: return launch_proj_u<LPR, CU, 3, XF>(a, st);
+    case 4: return launch_proj_u<LPR, CU, 4, XF>(a, st);
+    case 5: return launch_proj_u<LPR, CU, 5, XF>(a, st);
+    case 6: return launch_proj_u<LPR, CU, 6, XF>(a, st);
+    default: return launch_proj_u<LPR, CU, 8, XF>(a, st);
+    }
 }
 
 template <int CU, int XF>
