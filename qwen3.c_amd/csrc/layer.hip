@@ -419,28 +419,58 @@ struct AttnArgs {
 // the row src into the LDS row x and, if gdst != NULL, into gdst.  One wave; every output
 // element is written by the lane that computes it from src (no cross-lane LDS reads).
 __device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
-    const int lane = threadIdx.x & 63, hr = a.rot / 2;
+    constexpr int kPer = kAttMaxHD / 64, kPairs = (kAttMaxHR + 63) / 64;
+    const int lane = threadIdx.x & 63, hd = a.hd, hr = a.rot / 2;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, (uint32_t)hd * 4), rw = buf_rsrc(w, (uint32_t)hd * 4);
+    auto ld = [](__amdgpu_buffer_rsrc_t r, bool on, int i) {   // unconditional: out of range reads 0
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? i * 4 : (int)kOOB, 0, 0));
+    };
+    // every load first, one memory round trip: the row and its norm weight at lane + 64 q,
+    // and the lane's rotation pairs (jj, jj + hr) with their weights and cos/sin
+    float v[kPer], wv[kPer], lo[kPairs], hi[kPairs], wl[kPairs], wh[kPairs], cs[kPairs], sn[kPairs];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int d = lane + 64 * q;
+        v[q] = ld(rs, d < hd, d);
+        wv[q] = ld(rw, d < hd, d);
+    }
+#pragma unroll
+    for (int p = 0; p < kPairs; p++) {
+        const int jj = lane + 64 * p, jc = jj < kAttMaxHR ? jj : kAttMaxHR - 1;
+        const bool on = jj < hr;
+        lo[p] = ld(rs, on, jj);
+        hi[p] = ld(rs, on, jj + hr);
+        wl[p] = ld(rw, on, jj);
+        wh[p] = ld(rw, on, jj + hr);
+        cs[p] = a.cs[jc];
+        sn[p] = a.sn[jc];
+    }
     double ss = 0;
-    for (int d = lane; d < a.hd; d += 64) {
-        const float v = src[d];
-        ss += (double)v * v;
-    }
+#pragma unroll
+    for (int q = 0; q < kPer; q++) ss += (double)v[q] * v[q];   // zeros past hd add 0
     ss = wave_sum_d(ss);
-    const float r = 1.f / sqrtf((float)(ss / a.hd) + a.eps);
-    for (int d = a.rot + lane; d < a.hd; d += 64) {
-        const float v = src[d] * r * (1.f + w[d]);
-        x[d] = v;
-        if (gdst) gdst[d] = v;
+    const float r = 1.f / sqrtf((float)(ss / hd) + a.eps);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int d = lane + 64 * q;
+        if (d >= a.rot && d < hd) {
+            const float o = v[q] * r * (1.f + wv[q]);
+            x[d] = o;
+            if (gdst) gdst[d] = o;
+        }
     }
-    for (int jj = lane; jj < hr; jj += 64) {
-        const float cs = a.cs[jj], sn = a.sn[jj];
-        const float lo = src[jj] * r * (1.f + w[jj]), hi = src[jj + hr] * r * (1.f + w[jj + hr]);
-        const float o0 = lo * cs - hi * sn, o1 = hi * cs + lo * sn;
-        x[jj] = o0;
-        x[jj + hr] = o1;
-        if (gdst) {
-            gdst[jj] = o0;
-            gdst[jj + hr] = o1;
+#pragma unroll
+    for (int p = 0; p < kPairs; p++) {
+        const int jj = lane + 64 * p;
+        if (jj < hr) {
+            const float l = lo[p] * r * (1.f + wl[p]), h = hi[p] * r * (1.f + wh[p]);
+            const float o0 = l * cs[p] - h * sn[p], o1 = h * cs[p] + l * sn[p];
+            x[jj] = o0;
+            x[jj + hr] = o1;
+            if (gdst) {
+                gdst[jj] = o0;
+                gdst[jj + hr] = o1;
+            }
         }
     }
 }
@@ -464,31 +494,40 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     const bool owns_pos = a.pos >= t0 && a.pos < t1;
     // K rows of the score steps (16 lanes per position, DPL dims each) and V columns of
     // P.V (thread d: dims d + kThreads * i), all in flight together
+    // (branch-free buffer loads: out-of-range offsets read 0, so no load waits behind a
+    // data-dependent branch)
     const int pl = lane >> 4, part = lane & 15;
+    const uint32_t cache_b = (uint32_t)a.max_t * (uint32_t)hd * 4u;
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.Kc + (size_t)kh * a.max_t * hd, cache_b);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.Vc + (size_t)kh * a.max_t * hd, cache_b);
+    const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.v + (size_t)kh * hd, (uint32_t)hd * 4u);
     float kv[kSteps][DPL];
 #pragma unroll
     for (int st = 0; st < kSteps; st++) {
         const int t = t0 + (st * kWaves + wave) * 4 + pl;
         const bool ld = t < t1 && t != a.pos;
-        const float *kr = a.Kc + ((size_t)kh * a.max_t + (ld ? t : t0)) * hd + part * DPL;
 #pragma unroll
         for (int e = 0; e < DPL; e += 4) {
-            const float4 v4 = ld ? *(const float4 *)(kr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            kv[st][e] = v4.x;
-            kv[st][e + 1] = v4.y;
-            kv[st][e + 2] = v4.z;
-            kv[st][e + 3] = v4.w;
+            const coli_v4i v4 = __builtin_amdgcn_raw_buffer_load_b128(
+                rk, ld ? (t * hd + part * DPL + e) * 4 : (int)kOOB, 0, 0);
+            kv[st][e] = __int_as_float(v4.x);
+            kv[st][e + 1] = __int_as_float(v4.y);
+            kv[st][e + 2] = __int_as_float(v4.z);
+            kv[st][e + 3] = __int_as_float(v4.w);
         }
     }
-    float vv[kAttT][kVPer];
+    float vv[kAttT][kVPer];   // the cached row, or this token's v at pos (the other load reads 0)
 #pragma unroll
     for (int t = 0; t < kAttT; t++)
 #pragma unroll
         for (int i = 0; i < kVPer; i++) {
             const int d = tid + i * kThreads, tt = t0 + t;
-            vv[t][i] = 0.f;
-            if (t < n && d < hd)
-                vv[t][i] = tt == a.pos ? a.v[(size_t)kh * hd + d] : a.Vc[((size_t)kh * a.max_t + tt) * hd + d];
+            const bool on = t < n && d < hd;
+            const float c = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rv, on && tt != a.pos ? (tt * hd + d) * 4 : (int)kOOB, 0, 0));
+            const float nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           rn, on && tt == a.pos ? d * 4 : (int)kOOB, 0, 0));
+            vv[t][i] = c + nv;
         }
     for (int gg = wave; gg < G; gg += kWaves)
         norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
