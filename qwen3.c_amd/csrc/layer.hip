@@ -219,6 +219,7 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
 constexpr int kGdnCols = 16;            // state columns per block (4 per wave)
 constexpr int kGdnColsPerWave = kGdnCols / kWaves;
 constexpr int kGdnMaxKD = 256;
+constexpr int kGdnMaxK = 4;             // conv taps of the one-round-trip path (others loop)
 
 // A small projection row (GDN a/b: [VH, D]) in any device layout: element i of row r.
 struct RowMat {
@@ -329,6 +330,51 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
     // first v-head, first column slice, for q and k; every block for its own v columns)
     // stores this token's input at the ring head, a slot no block reads for this token
     const bool owns_qk = h % (g.VH / g.KH) == 0 && c0 == 0;
+    auto channel = [&](int t) {
+        return t < KD ? src * KD + t : t < 2 * KD ? key_dim + src * KD + (t - KD) : 2 * key_dim + h * g.VD + c0 + (t - 2 * KD);
+    };
+    if (g.K <= kGdnMaxK) {   // every load of the conv first (one memory round trip), branch-free
+        constexpr int kCh = (2 * kGdnMaxKD + kGdnCols + kThreads - 1) / kThreads;
+        const int nch = 2 * KD + kGdnCols, K = g.K;
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(g.qkv, (uint32_t)g.CD * 4u);
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(g.convw, (uint32_t)g.CD * (uint32_t)K * 4u);
+        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(g.ring, (uint32_t)K * (uint32_t)g.CD * 4u);
+        auto ld = [](__amdgpu_buffer_rsrc_t r, bool on, int i) {
+            return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? i * 4 : (int)kOOB, 0, 0));
+        };
+        float xin[kCh], wlast[kCh], cw[kCh][kGdnMaxK - 1], rg[kCh][kGdnMaxK - 1];
+#pragma unroll
+        for (int i = 0; i < kCh; i++) {
+            const int t = tid + i * kThreads;
+            const bool on = t < nch;
+            const int ch = on ? channel(t) : 0;
+            xin[i] = ld(rx, on, ch);
+            wlast[i] = ld(rw, on, ch * K + K - 1);
+#pragma unroll
+            for (int q = 0; q + 1 < kGdnMaxK; q++) {
+                int slot = g.head + 1 + q;
+                if (slot >= K) slot -= K;
+                cw[i][q] = ld(rw, on && q + 1 < K, ch * K + q);
+                rg[i][q] = ld(rr, on && q + 1 < K, slot * g.CD + ch);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kCh; i++) {
+            const int t = tid + i * kThreads;
+            if (t >= nch) continue;
+            const int ch = channel(t);
+            float acc = 0.f;   // the reference's order: older inputs first, this token last
+#pragma unroll
+            for (int q = 0; q + 1 < kGdnMaxK; q++)
+                if (q + 1 < K) acc += cw[i][q] * rg[i][q];
+            acc += wlast[i] * xin[i];
+            const float v = silu_f(acc);
+            if (t < KD) s_q[t] = v;
+            else if (t < 2 * KD) s_k[t - KD] = v;
+            else s_v[t - 2 * KD] = v;
+            if (t >= 2 * KD || owns_qk) g.ring[(size_t)g.head * g.CD + ch] = xin[i];
+        }
+    } else
     for (int t = tid; t < 2 * KD + kGdnCols; t += kThreads) {
         const int ch = t < KD ? src * KD + t : t < 2 * KD ? key_dim + src * KD + (t - KD)
                                                           : 2 * key_dim + h * g.VD + c0 + (t - 2 * KD);
