@@ -364,10 +364,26 @@ __device__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn, 
 // c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate.
 __device__ void tile_route(const MoeArgs &a, RouteLds &R) {
     const int tid = threadIdx.x, E = a.E, K = a.K;
-    for (int e = tid; e <= E; e += kThreads) {   // logit E is the shared-expert gate dot
-        const float l = tag_get(&a.tagv[e], a.epoch, a.err);
+    // the thread's logits e = tid + q kThreads <= E (logit E is the shared-expert gate dot),
+    // all polled together: one round trip per poll however many a thread holds
+    constexpr int kPer = (kMaxE + 1 + kThreads - 1) / kThreads;
+    unsigned long long v[kPer];
+    for (int polls = 0;; polls++) {
+        bool all = true;
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            const int e = tid + q * kThreads;
+            v[q] = aload(&a.tagv[e <= E ? e : E]);
+            all &= e > E || (uint32_t)(v[q] >> 32) == a.epoch;
+        }
+        if (all || poll_give_up(a.err, polls)) break;
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int e = tid + q * kThreads;
+        const float l = __uint_as_float((uint32_t)v[q]);
         if (e < E) R.p[e] = l;
-        else R.gate = l;
+        else if (e == E) R.gate = l;
     }
     route_select(R, E, K);
     // thread (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
