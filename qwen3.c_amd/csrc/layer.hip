@@ -672,18 +672,45 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
     const int ns = (a.pos + 1 + kAttT - 1) / kAttT;
     const float *pb = a.part + ((size_t)kh * a.nsplit) * G * (hd + 2) + (size_t)gg * (hd + 2);
     const size_t stride = (size_t)G * (hd + 2);
-    float m = -INFINITY;
-    for (int s = tid; s < ns; s += kThreads) m = fmaxf(m, pb[s * stride + hd]);
+    // the gate row of the output first (read at the very end), then each chunk's (m, l):
+    // with ns <= kThreads one chunk per thread, kept in registers for the weights
+    constexpr int kGPer = kAttMaxHD / kThreads;
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.q + (size_t)h * 2 * hd + hd, (uint32_t)hd * 4u);
+    float gv[kGPer];
+#pragma unroll
+    for (int i = 0; i < kGPer; i++) {
+        const int d = tid + i * kThreads;
+        gv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, d < hd ? d * 4 : (int)kOOB, 0, 0));
+    }
+    const bool one = ns <= kThreads;
+    float m = -INFINITY, mv = -INFINITY, lv = 0.f;
+    if (one) {
+        if (tid < ns) {
+            mv = pb[tid * stride + hd];
+            lv = pb[tid * stride + hd + 1];
+        }
+        m = mv;
+    } else {
+        for (int s = tid; s < ns; s += kThreads) m = fmaxf(m, pb[s * stride + hd]);
+    }
     m = wave_max_f(m);
     if (lane == 0) s_red[wave] = m;
     __syncthreads();
     m = s_red[0];
     for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_red[w]);
     float l = 0.f;
-    for (int s = tid; s < ns; s += kThreads) {
-        const float w = expf(pb[s * stride + hd] - m);
-        s_w[s] = w;
-        l += pb[s * stride + hd + 1] * w;
+    if (one) {
+        if (tid < ns) {
+            const float w = expf(mv - m);
+            s_w[tid] = w;
+            l = lv * w;
+        }
+    } else {
+        for (int s = tid; s < ns; s += kThreads) {
+            const float w = expf(pb[s * stride + hd] - m);
+            s_w[s] = w;
+            l += pb[s * stride + hd + 1] * w;
+        }
     }
     l = wave_sum_f(l);
     __syncthreads();
@@ -695,12 +722,12 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
     for (int d0 = lane * 4; d0 < hd; d0 += 256) {   // hd % 64 == 0: whole float4s
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         int s = wave;
-        for (; s + 3 * kWaves < ns; s += 4 * kWaves) {   // 4 chunks' loads in flight
-            float4 v[4];
+        for (; s + 15 * kWaves < ns; s += 16 * kWaves) {   // 16 chunks' loads in flight
+            float4 v[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++) v[u] = *(const float4 *)(pb + (size_t)(s + u * kWaves) * stride + d0);
+            for (int u = 0; u < 16; u++) v[u] = *(const float4 *)(pb + (size_t)(s + u * kWaves) * stride + d0);
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 16; u++) {
                 const float w = s_w[s + u * kWaves];
                 acc.x = fmaf(v[u].x, w, acc.x);
                 acc.y = fmaf(v[u].y, w, acc.y);
@@ -719,10 +746,13 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
         *(float4 *)&s_acc[wave][d0] = acc;
     }
     __syncthreads();
-    const float *gate = a.q + (size_t)h * 2 * hd + hd;
-    for (int d = tid; d < hd; d += kThreads) {
-        const float acc = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
-        a.ctx[(size_t)h * hd + d] = acc * inv * (1.f / (1.f + expf(-gate[d])));
+#pragma unroll
+    for (int i = 0; i < kGPer; i++) {
+        const int d = tid + i * kThreads;
+        if (d < hd) {
+            const float acc = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
+            a.ctx[(size_t)h * hd + d] = acc * inv * (1.f / (1.f + expf(-gv[i])));
+        }
     }
 }
 
