@@ -626,7 +626,7 @@ static int launch_lanes_cu(const ColiVkTensor *t, const float *x, float *y, hipS
 // fmt 6 lanes-layout GEMV in one of the modes; returns the grid size (0 = not launched)
 template <int MODE>
 static int launch_lanes_mode(const ColiVkTensor *t, const float *x, float *y, hipStream_t st, const TopkArgs &ta) {
-    const int nb = t->gs >= 32 * kLaneChunks ? launch_lanes_cu<kLaneChunks, MODE>(t, x, y, st, ta)
+    const int nb = t->gs % (32 * kLaneChunks) == 0 ? launch_lanes_cu<kLaneChunks, MODE>(t, x, y, st, ta)
                                              : launch_lanes_cu<1, MODE>(t, x, y, st, ta);
     if (nb) {
         const hipError_t e = hipGetLastError();

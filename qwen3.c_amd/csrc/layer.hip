@@ -947,7 +947,7 @@ static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *
         if (VD % 8 || wph < 1 || wph > 64 || (wph & (wph - 1)) || a.I % VD) return refuse("gated norm head size");
     }
     const int l = lpr < 2 ? 2 : lpr;
-    const bool wide = t0->gs >= 32 * kLaneChunks;
+    const bool wide = t0->gs % (32 * kLaneChunks) == 0;   // a unit of kLaneChunks chunks lies in one group
     switch (xf) {
     case XF_PLAIN: return wide ? proj_lpr<kLaneChunks, XF_PLAIN>(a, l, st) : proj_lpr<1, XF_PLAIN>(a, l, st);
     case XF_NORM: return wide ? proj_lpr<kLaneChunks, XF_NORM>(a, l, st) : proj_lpr<1, XF_NORM>(a, l, st);

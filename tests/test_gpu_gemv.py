@@ -43,6 +43,7 @@ def test_cfg0_matmul(lib, orc, gen):
 @pytest.mark.parametrize("O,I,gs", [
     (1, 32, 32), (7, 256, 128), (64, 512, 128), (33, 2048, 64), (5, 4096, 128),
     (3, 6144, 128), (2, 8192, 256), (16, 250, 32), (9, 129, 32),          # fast path
+    (7, 1024, 256), (5, 960, 96), (3, 2048, 512), (4, 4096, 4096),        # fast path, group max by LDS atomics
     (9, 8200, 128), (17, 100, 8), (8, 264, 24), (4, 2048, 16), (6, 520, 40),  # generic path
 ])
 def test_fmt6_shapes(lib, orc, gen, O, I, gs):
