@@ -562,19 +562,24 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
             kv[st][e + 3] = __int_as_float(v4.w);
         }
     }
-    float vv[kAttT][kVPer];   // the cached row, or this token's v at pos (the other load reads 0)
+    // V: the cached rows, and this token's v for the position pos (selected below); dims
+    // slots past hd are skipped uniformly
+    float vv[kAttT][kVPer];
 #pragma unroll
-    for (int t = 0; t < kAttT; t++)
+    for (int i = 0; i < kVPer; i++) {
+        if (i > 0 && i * kThreads >= hd) continue;   // uniform; a guarded body keeps the unroll
+        const int d = tid + i * kThreads;
+        const float nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                       rn, owns_pos && d < hd ? d * 4 : (int)kOOB, 0, 0));
 #pragma unroll
-        for (int i = 0; i < kVPer; i++) {
-            const int d = tid + i * kThreads, tt = t0 + t;
-            const bool on = t < n && d < hd;
+        for (int t = 0; t < kAttT; t++) {
+            const int tt = t0 + t;
+            const bool on = t < n && d < hd && tt != a.pos;
             const float c = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                          rv, on && tt != a.pos ? (tt * hd + d) * 4 : (int)kOOB, 0, 0));
-            const float nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                           rn, on && tt == a.pos ? d * 4 : (int)kOOB, 0, 0));
-            vv[t][i] = c + nv;
+                                                          rv, on ? (tt * hd + d) * 4 : (int)kOOB, 0, 0));
+            vv[t][i] = tt == a.pos ? nv : c;
         }
+    }
     for (int gg = wave; gg < G; gg += kWaves)
         norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
     if (owns_pos && wave == kWaves - 1) {   // the new key row and value row (c/qwen.c:605-614)
