@@ -464,53 +464,62 @@ struct AttnArgs {
 // zero-centred RMSNorm over hd, then partial RoPE at pos (c/qwen.c:326-330, :570-579), of
 // the row src into the LDS row x and, if gdst != NULL, into gdst.  One wave; every output
 // element is written by the lane that computes it from src (no cross-lane LDS reads).
-__device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
-    constexpr int kPer = kAttMaxHD / 64, kPairs = (kAttMaxHR + 63) / 64;
+// The loads of one row (issued by row_load, consumed by row_finish): the row and its norm
+// weight at lane + 64 q, and the lane's rotation pairs (jj, jj + hr) with their weights and
+// cos/sin.  Splitting lets a wave issue several rows' loads before it waits for any.
+struct RowLd {
+    static constexpr int kPer = kAttMaxHD / 64, kPairs = (kAttMaxHR + 63) / 64;
+    float v[kPer], wv[kPer], lo[kPairs], hi[kPairs], wl[kPairs], wh[kPairs], cs[kPairs], sn[kPairs];
+};
+__device__ __forceinline__ void row_load(RowLd &R, const float *src, const float *w, const AttnArgs &a) {
     const int lane = threadIdx.x & 63, hd = a.hd, hr = a.rot / 2;
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, (uint32_t)hd * 4), rw = buf_rsrc(w, (uint32_t)hd * 4);
     auto ld = [](__amdgpu_buffer_rsrc_t r, bool on, int i) {   // unconditional: out of range reads 0
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? i * 4 : (int)kOOB, 0, 0));
     };
-    // every load first, one memory round trip: the row and its norm weight at lane + 64 q,
-    // and the lane's rotation pairs (jj, jj + hr) with their weights and cos/sin
-    float v[kPer], wv[kPer], lo[kPairs], hi[kPairs], wl[kPairs], wh[kPairs], cs[kPairs], sn[kPairs];
 #pragma unroll
-    for (int q = 0; q < kPer; q++) {
+    for (int q = 0; q < RowLd::kPer; q++) {
         const int d = lane + 64 * q;
-        v[q] = ld(rs, d < hd, d);
-        wv[q] = ld(rw, d < hd, d);
+        R.v[q] = ld(rs, d < hd, d);
+        R.wv[q] = ld(rw, d < hd, d);
     }
 #pragma unroll
-    for (int p = 0; p < kPairs; p++) {
+    for (int p = 0; p < RowLd::kPairs; p++) {
         const int jj = lane + 64 * p, jc = jj < kAttMaxHR ? jj : kAttMaxHR - 1;
         const bool on = jj < hr;
-        lo[p] = ld(rs, on, jj);
-        hi[p] = ld(rs, on, jj + hr);
-        wl[p] = ld(rw, on, jj);
-        wh[p] = ld(rw, on, jj + hr);
-        cs[p] = a.cs[jc];
-        sn[p] = a.sn[jc];
+        R.lo[p] = ld(rs, on, jj);
+        R.hi[p] = ld(rs, on, jj + hr);
+        R.wl[p] = ld(rw, on, jj);
+        R.wh[p] = ld(rw, on, jj + hr);
+        R.cs[p] = a.cs[jc];
+        R.sn[p] = a.sn[jc];
     }
+}
+// zero-centred RMSNorm over hd, then partial RoPE at pos, of a loaded row into the LDS row x
+// and, if gdst != NULL, into gdst.  One wave; every output element is written by the lane
+// that computes it (no cross-lane LDS reads).
+__device__ __forceinline__ void row_finish(float *x, float *gdst, const RowLd &R, const AttnArgs &a) {
+    const int lane = threadIdx.x & 63, hd = a.hd, hr = a.rot / 2;
     double ss = 0;
 #pragma unroll
-    for (int q = 0; q < kPer; q++) ss += (double)v[q] * v[q];   // zeros past hd add 0
+    for (int q = 0; q < RowLd::kPer; q++) ss += (double)R.v[q] * R.v[q];   // zeros past hd add 0
     ss = wave_sum_d(ss);
     const float r = 1.f / sqrtf((float)(ss / hd) + a.eps);
 #pragma unroll
-    for (int q = 0; q < kPer; q++) {
+    for (int q = 0; q < RowLd::kPer; q++) {
         const int d = lane + 64 * q;
         if (d >= a.rot && d < hd) {
-            const float o = v[q] * r * (1.f + wv[q]);
+            const float o = R.v[q] * r * (1.f + R.wv[q]);
             x[d] = o;
             if (gdst) gdst[d] = o;
         }
     }
 #pragma unroll
-    for (int p = 0; p < kPairs; p++) {
+    for (int p = 0; p < RowLd::kPairs; p++) {
         const int jj = lane + 64 * p;
         if (jj < hr) {
-            const float l = lo[p] * r * (1.f + wl[p]), h = hi[p] * r * (1.f + wh[p]);
-            const float o0 = l * cs[p] - h * sn[p], o1 = h * cs[p] + l * sn[p];
+            const float l = R.lo[p] * r * (1.f + R.wl[p]), h = R.hi[p] * r * (1.f + R.wh[p]);
+            const float o0 = l * R.cs[p] - h * R.sn[p], o1 = h * R.cs[p] + l * R.sn[p];
             x[jj] = o0;
             x[jj + hr] = o1;
             if (gdst) {
@@ -519,6 +528,11 @@ __device__ void norm_rope_row(float *x, float *gdst, const float *src, const flo
             }
         }
     }
+}
+__device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
+    RowLd R;
+    row_load(R, src, w, a);
+    row_finish(x, gdst, R, a);
 }
 
 // One block per (kv head, chunk of kAttT positions).  Every K and V element the block
@@ -580,12 +594,23 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
             vv[t][i] = tt == a.pos ? nv : c;
         }
     }
-    for (int gg = wave; gg < G; gg += kWaves)
-        norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
-    if (owns_pos && wave == kWaves - 1) {   // the new key row and value row (c/qwen.c:605-614)
-        const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
-        norm_rope_row(s_k, a.Kc + row, a.k + (size_t)kh * hd, a.kn, a);
-        for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
+    {   // the wave's first two q rows and, in the chunk holding pos, the new key row: all
+        // their loads first, then the norms (rows past two per wave follow one by one)
+        const int g0 = wave, g1 = wave + kWaves;
+        const bool own_k = owns_pos && wave == kWaves - 1;
+        RowLd r0, r1, rk;
+        if (g0 < G) row_load(r0, a.q + (size_t)(kh * G + g0) * 2 * hd, a.qn, a);
+        if (g1 < G) row_load(r1, a.q + (size_t)(kh * G + g1) * 2 * hd, a.qn, a);
+        if (own_k) row_load(rk, a.k + (size_t)kh * hd, a.kn, a);
+        if (g0 < G) row_finish(s_q[g0], nullptr, r0, a);
+        if (g1 < G) row_finish(s_q[g1], nullptr, r1, a);
+        for (int gg = wave + 2 * kWaves; gg < G; gg += kWaves)
+            norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
+        if (own_k) {   // the new key row and value row (c/qwen.c:605-614)
+            const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
+            row_finish(s_k, a.Kc + row, rk, a);
+            for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
+        }
     }
     __syncthreads();
     // scores: 16 lanes per position, 4 positions per wave step; each q fragment is read
