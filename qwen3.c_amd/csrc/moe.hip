@@ -36,7 +36,7 @@ namespace coli {
 constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
 constexpr int kGSteps = 2;                // gate/up row steps per tile
 constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
-constexpr int kRouteReps = 8;             // copies of the route block (readers spread over them)
+constexpr int kRouteReps = 4;             // copies of the route block (readers spread over them)
 constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1], K <= 8
 
 struct MoeArgs {
