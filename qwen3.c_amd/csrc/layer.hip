@@ -893,7 +893,7 @@ struct SegIn {
 static int proj_u(int ngroups) {
     const long per_step = (long)kWaves * n_cu();
     const long need = (ngroups + per_step - 1) / per_step;
-    return need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : need <= 5 ? 5 : need <= 6 ? 6 : 8;
+    return need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : need <= 5 ? 5 : need <= 6 ? 6 : need <= 7 ? 7 : 8;
 }
 
 template <int LPR, int CU, int U, int XF>
@@ -916,6 +916,7 @@ static bool launch_proj(ProjArgs &a, hipStream_t st) {
     case 4: return launch_proj_u<LPR, CU, 4, XF>(a, st);
     case 5: return launch_proj_u<LPR, CU, 5, XF>(a, st);
     case 6: return launch_proj_u<LPR, CU, 6, XF>(a, st);
+    case 7: return launch_proj_u<LPR, CU, 7, XF>(a, st);
     default: return launch_proj_u<LPR, CU, 8, XF>(a, st);
     }
 }
