@@ -12,7 +12,15 @@
  *   - tensors are created lazily through the in/out ColiVkTensor** handle and own a
  *     device copy of the caller's host weights (c/backend_vulkan.c:1055-1085);
  *   - one host thread; at most one expert group in flight (c/backend_vulkan.c:1648).
- * Entry points for the GLM (MLA absorb) paths, which c/qwen.c never calls, return 0.
+ * Entry points that always return 0 (the caller then computes that step on the CPU):
+ *   - the GLM MLA paths, which c/qwen.c never calls: coli_vk_attention_absorb,
+ *     coli_vk_attn_qprep, coli_vk_attention_absorb_project;
+ *   - the staged attention/GDN forms that take host-computed q or recurrence inputs:
+ *     coli_vk_gqa, coli_vk_gqa_project, coli_vk_gdn, coli_vk_gdn_project.  The engine
+ *     reaches them only when a fused block (coli_vk_gqa_full*, coli_vk_gdn_full*) is off,
+ *     and falls back per call (c/qwen.c:620-636, 732-745).  coli_vk_gqa_available and
+ *     coli_vk_gdn_available still report 1: they also gate the KV mirror, the GDN state
+ *     and the fused blocks, which are implemented.
  *
  * Part 2 (coli_hip_*) has no counterpart in the reference: device-pointer forms of the
  * hot path for callers whose inputs already live in HBM (the benchmark, the parity
@@ -76,10 +84,11 @@ int  coli_vk_expert_group_issue_id(ColiVkTensor *const *gates, ColiVkTensor *con
 /* c/backend_vulkan.h:105 */
 int  coli_vk_tensor_ensure(ColiVkTensor **tensor, const void *weights, const float *scales,
                            int fmt, int I, int O, int grp);
-/* c/backend_vulkan.h:114-122, 125-131, 138-141: GLM MLA paths (unused by c/qwen.c): return 0 */
+/* c/backend_vulkan.h:114-116: device KV mirror (rows kv_head * max_t + pos; also the GQA cache) */
 int  coli_vk_kv_ensure(int layer, int max_rows, int K, int Rd);
 int  coli_vk_kv_row(int layer, int pos, const float *L, const float *R);
 void coli_vk_kv_reset(void);
+/* c/backend_vulkan.h:117-119, 125-131, 138-141: GLM MLA paths (unused by c/qwen.c): return 0 */
 int  coli_vk_attention_absorb(ColiVkTensor **kvb, const void *w, const float *sc, int fmt, int grp,
                               float *ctx, const float *q, int layer, int S, int H,
                               int Q, int R, int V, int K, int st0, int T, float scale);
@@ -207,9 +216,14 @@ int   coli_hip_sync(void *stream);
 int   coli_hip_memcpy(void *dst, const void *src, size_t bytes);
 /* y[S,O] = x[S,I] @ dequant(W)^T on device pointers. */
 int   coli_hip_gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, void *stream);
-/* GEMV fused with the k best outputs (k <= 8; value desc, index asc); d_y may be NULL. */
+/* GEMV fused with the k best outputs (k <= 8; value desc, index asc); d_y may be NULL.
+ * If the in-launch merge's bounded wait gives up, that launch writes -1 to d_idx[0..k)
+ * and sets the error word that coli_hip_gemv_error reports. */
 int   coli_hip_gemv_topk(const ColiVkTensor *t, const float *d_x, float *d_y, int k,
                          int *d_idx, float *d_val, void *stream);
+/* Error word of the fused top-k launches since the last call (synchronises the device):
+ * 0 none, 1 a bounded wait gave up, -1 runtime error.  Reading clears it. */
+int   coli_hip_gemv_error(void);
 /* Create a tensor whose contents are generated on the device with the synthetic-data
  * spec (fmt 6: bytes = stream(seed,1), [scale,zero] = stream(seed,2) with scale sigma;
  * fmt 0: rows = sigma * normal(stream(seed,3))); equal to uploading the host-generated
@@ -226,9 +240,14 @@ int   coli_hip_synth_normal(float *d_dst, size_t n, uint64_t seed, double sigma,
  * them on one stream. */
 int   coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x,
                           float *d_out, int accumulate, int *d_idx, float *d_val, void *stream);
-/* Error flag of the MoE launches since the last call (synchronizes the device): 0 none,
- * 1 a bounded wait gave up, 2 an out-of-range expert id, -1 runtime error. */
+/* Error word of the MoE launches since the last call (synchronizes the device): 0 none, 1 a bounded wait gave up, 2 an out-of-range
+ * expert id, -1 runtime error.  Reading clears it. */
 int   coli_hip_moe_error(void);
+/* Test hook for the failure path: sets the MoE error word from the host (code 1 or 2), so
+ * the next MoE launches' bounded waits give up at their 16th poll (every kernel still
+ * exits normally) and the stream entry points report the failure (return 0, device
+ * disabled) as after a real give-up.  Returns 1 when the word was written. */
+int   coli_hip_moe_force_error(int code);
 /* The layer's MoE block over S token rows d_xs[S, D] (prefill / ragged batch,
  * c/qwen.c:1050-1183): per-token routing, rows grouped by expert, expert projections as
  * grouped GEMMs on MFMA (int8 digits of the activations x int4 weights, exact integer

@@ -53,6 +53,8 @@ _SIGS = {
     "coli_vk_eg_table_set_shared": (_I, [_I, _P, _P, _P, _P, _I]),
     "coli_hip_moe_decode": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "coli_hip_moe_error": (_I, []),
+    "coli_hip_moe_force_error": (_I, [_I]),
+    "coli_hip_gemv_error": (_I, []),
     "coli_hip_moe_prefill": (_I, [_I, _P, _I, _P, _I, _P, _P, _P, _P]),
     # attention / GatedDeltaNet layer blocks and the residual stream (c/backend_vulkan.h:110-279)
     "coli_vk_kv_ensure": (_I, [_I, _I, _I, _I]),
@@ -289,6 +291,12 @@ class Lib:
     def moe_error(self):
         return int(self.L.coli_hip_moe_error())
 
+    def moe_force_error(self, code=1):
+        self._ok(self.L.coli_hip_moe_force_error(code), "coli_hip_moe_force_error")
+
+    def gemv_error(self):
+        return int(self.L.coli_hip_gemv_error())
+
     # ---- attention / GatedDeltaNet state (c/backend_vulkan.h:110-116, 146-156, 258-279) ----
     def _ok(self, r, what):
         if not r:
@@ -431,3 +439,8 @@ class Lib:
         self._ok(self.L.coli_vk_stream_norm_argmax(t.ref, None, None, t.fmt, t.I, t.O, t.gs, eps, C.byref(idx),
                                                    C.byref(val)), "coli_vk_stream_norm_argmax")
         return idx.value, val.value
+
+    def stream_copy_resid(self, D):
+        x = np.empty(D, np.float32)
+        self._ok(self.L.coli_vk_stream_copy_resid(_ptr(x), D), "coli_vk_stream_copy_resid")
+        return x

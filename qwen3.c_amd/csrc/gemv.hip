@@ -31,6 +31,7 @@ struct TopkArgs {
     uint32_t epoch;              // tag of this launch (8 bits used)
     int *out_i;                  // fused top-k: the k best (value desc, index asc)
     float *out_v;
+    int *err;                    // fused top-k: set to 1 when a bounded poll gives up
 };
 
 // ---- argmax as a 64-bit key: [63:56] launch epoch, [55:24] order-preserving bits of the
@@ -232,6 +233,7 @@ __device__ void topk_final_block(const TopkArgs &tk, int nblk) {
         tk.out_i[tid] = bad ? -1 : row;
         tk.out_v[tid] = v;
     }
+    if (bad && tid == 0) __hip_atomic_store(tk.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The k best of nblk sorted partial lists (k entries each).  The global top k can only
@@ -575,15 +577,22 @@ constexpr int kU = COLI_GEMV_U;
 constexpr int kGemvBlocksPerCU = COLI_GEMV_BPC;
 constexpr int kMaxBlocksPerCU = 8;
 
-// Resident blocks per CU of one kernel instantiation (queried once).
+// Resident blocks per CU of one kernel instantiation, queried once per kernel (the cache is
+// keyed by the kernel's address: every gemv6_lanes instantiation has the same type).
 template <typename Kern>
 static int occupancy(Kern kern) {
-    static int v = 0;
-    if (!v) {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n < 1) n = 1;
-        v = n > kMaxBlocksPerCU ? kMaxBlocksPerCU : n;
-    }
+    static struct {
+        const void *k;
+        int v;
+    } cache[64];
+    static int n_cached = 0;
+    const void *key = (const void *)kern;
+    for (int i = 0; i < n_cached; i++)
+        if (cache[i].k == key) return cache[i].v;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess || n < 1) n = 1;
+    const int v = n > kMaxBlocksPerCU ? kMaxBlocksPerCU : n;
+    if (n_cached < 64) cache[n_cached++] = {key, v};
     return v;
 }
 
@@ -638,7 +647,7 @@ static int launch_lanes_mode(const ColiVkTensor *t, const float *x, float *y, hi
 static bool launch_one(const ColiVkTensor *t, const float *x, float *y, hipStream_t st) {
     int nb;
     if (t->layout == kLayoutLanes) {
-        const TopkArgs none = {0, nullptr, nullptr, nullptr, 0, nullptr, nullptr};
+        const TopkArgs none = {0, nullptr, nullptr, nullptr, 0, nullptr, nullptr, nullptr};
         nb = launch_lanes_mode<0>(t, x, y, st, none);
     } else {
         nb = grid_size((t->O + kWaves - 1) / kWaves, occupancy(gemv_generic));
@@ -664,7 +673,7 @@ bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t 
     long nbp = ((long)n + kThreads * 8 - 1) / (kThreads * 8);
     if (nbp > (long)n_cu() * 2) nbp = (long)n_cu() * 2;
     if (!scratch(&g_tk.buf, &g_tk.cap, (size_t)nbp * kTopK * 8)) return false;
-    TopkArgs ta = {k, (float *)g_tk.buf, (int *)((float *)g_tk.buf + (size_t)nbp * kTopK), nullptr, 0, nullptr, nullptr};
+    TopkArgs ta = {k, (float *)g_tk.buf, (int *)((float *)g_tk.buf + (size_t)nbp * kTopK), nullptr, 0, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(topk_partial, dim3((unsigned)nbp), dim3(kThreads), 0, st, d_v, n, ta);
     hipLaunchKernelGGL(topk_final, dim3(1), dim3(kFinalThreads), 0, st, ta.part_v, ta.part_i, (int)nbp, k, d_val,
                        d_idx);
@@ -688,7 +697,7 @@ bool gemv_argmax(const ColiVkTensor *t, const float *d_x, float *d_y, hipStream_
         hipLaunchKernelGGL(argmax_reset, dim3(1), dim3(64), 0, st, (unsigned long long *)g_slots);
         g_epoch = 1;
     }
-    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch, nullptr, nullptr};
+    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch, nullptr, nullptr, nullptr};
     if (!launch_lanes_mode<1>(t, d_x, d_y, st, ta)) return false;
     *epoch = g_epoch;
     *slots = (const unsigned long long *)g_slots;
@@ -696,7 +705,7 @@ bool gemv_argmax(const ColiVkTensor *t, const float *d_x, float *d_y, hipStream_
 }
 
 bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_t st, const TopkOut *tk) {
-    if (!t || S < 1) return false;
+    if (!tensor_live(t) || S < 1) return false;
     const bool want_k = tk && tk->k > 0;
     if (want_k && (S != 1 || tk->k > kTopK)) return false;
     if (!d_y) {
@@ -713,14 +722,16 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
         return true;
     }
     if (want_k && t->layout == kLayoutLanes && t->O < (1 << 24)) {   // fused: one launch
-        const int n = kFusedGrid * kTopK + 1;   // the last word holds the two counters
-        if (!scratch(&g_keys, &g_keys_cap, (size_t)n * 8)) return false;
+        // block lists, then one word with the two counters, then the error word (not reset)
+        const int n = kFusedGrid * kTopK + 1;
+        if (!scratch(&g_keys, &g_keys_cap, (size_t)(n + 1) * 8)) return false;
         g_tk_epoch = (g_tk_epoch + 1) & 0xFFu;
         if (g_tk_epoch == 0) {   // tags wrap: clear keys and counters, no old key carries the new tag
             hipLaunchKernelGGL(keys_reset, dim3((n + 255) / 256), dim3(256), 0, st, (unsigned long long *)g_keys, n);
             g_tk_epoch = 1;
         }
-        const TopkArgs ta = {tk->k, nullptr, nullptr, (unsigned long long *)g_keys, g_tk_epoch, tk->idx, tk->val};
+        const TopkArgs ta = {tk->k,   nullptr, nullptr, (unsigned long long *)g_keys, g_tk_epoch, tk->idx, tk->val,
+                             (int *)((unsigned long long *)g_keys + n)};
         return launch_lanes_mode<2>(t, d_x, d_y, st, ta) != 0;
     }
     for (int s = 0; s < S; s++)
@@ -832,6 +843,7 @@ COLI_API int coli_vk_matmul_argmax(ColiVkTensor **tensor, const void *weights, c
     if (!gemv(*tensor, (const float *)g_st.dx, nullptr, 1, stream(), &tk)) return 0;
     int res[16];
     if (!fetch(res, g_st.dk, 64, "matmul_argmax")) return 0;
+    if (res[0] < 0 || res[0] >= O) return 0;   // a selection that gave up: the caller's host scan
     *idx = res[0];
     if (val) memcpy(val, &res[8], 4);
     return 1;
@@ -854,5 +866,37 @@ COLI_API int coli_hip_gemv_topk(const ColiVkTensor *t, const float *d_x, float *
     return gemv(t, d_x, d_y, 1, stream_ ? (hipStream_t)stream_ : stream(), &tk) ? 1 : 0;
 }
 
+namespace coli {
+// Error word of the fused top-k launches since the last call (synchronises the device):
+// 0 none, 1 a bounded wait of the merge gave up (that launch wrote -1 to d_idx), -1 runtime error.
+int gemv_error_take() {
+    if (!g_keys) return 0;
+    int *w = (int *)((unsigned long long *)g_keys + kFusedGrid * kTopK + 1);
+    int e = 0;
+    if (hipStreamSynchronize(stream()) != hipSuccess || hipMemcpy(&e, w, 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (e) {
+        const int z = 0;
+        if (hipMemcpy(w, &z, 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return e;
+}
+
+void gemv_shutdown() {
+    scratch_free(&g_tk.buf, &g_tk.cap);
+    scratch_free(&g_logits, &g_logits_cap);
+    scratch_free(&g_slots, &g_slots_cap);
+    scratch_free(&g_keys, &g_keys_cap);
+    host_scratch_free(&g_st.hx, &g_st.hxc);
+    host_scratch_free(&g_st.hy, &g_st.hyc);
+    scratch_free(&g_st.dx, &g_st.dxc);
+    scratch_free(&g_st.dy, &g_st.dyc);
+    scratch_free(&g_st.dk, &g_st.dkc);
+    g_epoch = g_tk_epoch = 0;
+}
+}  // namespace coli
+
 // the library's stream (for callers that time or order work against it)
 COLI_API void *coli_hip_stream(void) { return (void *)stream(); }
+
+COLI_API int coli_hip_gemv_error(void) { return gemv_error_take(); }

@@ -32,7 +32,9 @@ struct ColiVkTensor {
     int row_bytes;     // device row stride
     uint8_t *w;        // device weights
     float *sz;         // device scales (+zeros)
-    size_t bytes;      // device bytes held
+    size_t bytes;      // device bytes held (weights + scales)
+    size_t wbytes;     // device weight bytes (row_bytes * O), what coli_vk_tensor_bytes reports
+    unsigned gen;      // runtime generation that allocated it (a shutdown invalidates the handle)
 };
 
 namespace coli {
@@ -53,6 +55,7 @@ bool host_scratch(void **p, size_t *cap, size_t need);  // grow-only pinned host
 bool sync_stream(const char *who);
 
 // tensors
+bool tensor_live(const ColiVkTensor *t);  // non-NULL and allocated since the last shutdown
 constexpr int kLaneMaxI = 4096;          // fmt 6 lanes layout / fast GEMV path: nl <= 64
 constexpr int kLaneChunks = 2;           // 16-byte chunks owned by one lane of a row
 ColiVkTensor *tensor_alloc(int fmt, int I, int O, int gs);   // not yet filled or counted
@@ -83,6 +86,21 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
                 int *d_idx, float *d_val, hipStream_t st, const float *d_xw = nullptr, float eps = 0.f);
 // expert table complete for the layer
 bool moe_ready(int layer);
+
+// MoE error word of the decode launches: 0 none, 1 a bounded wait gave up, 2 a route held
+// an out-of-range expert id.  moe_error_take reads and clears it (synchronises the device);
+// -1 on a runtime error.
+int moe_error_take();
+
+// Teardown of each source file's state at coli_vk_shutdown: scratch buffers are freed and
+// every device pointer into the weight arena is forgotten, so calls after a shutdown
+// refuse instead of running kernels on freed memory.
+void gemv_shutdown();
+void moe_shutdown();
+void prefill_shutdown();
+void layer_shutdown();
+void scratch_free(void **p, size_t *cap);
+void host_scratch_free(void **p, size_t *cap);
 
 // device residual stream (layer.hip): the residual row of a live stream of width D, and
 // the last non-fused route's normed row (the expert input); NULL when not available

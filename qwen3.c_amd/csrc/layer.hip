@@ -947,7 +947,7 @@ static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *
     const ColiVkTensor *t0 = segs[0].t;
     for (int i = 0; i < n; i++) {
         const ColiVkTensor *t = segs[i].t;
-        if (!t || !segs[i].y) return refuse("NULL projection tensor");
+        if (!tensor_live(t) || !segs[i].y) return refuse("NULL or stale projection tensor");
         if (t->fmt != 6 || t->layout != kLayoutLanes) return refuse("projection is not fmt 6 (gs % 32 == 0, I <= 4096)");
         if (t->I != t0->I || t->gs != t0->gs || t->nl != t0->nl || t->row_bytes != t0->row_bytes)
             return refuse("fused projections differ in input geometry");
@@ -1090,7 +1090,7 @@ static bool gdn_block(int gi, const float *src, const float *ln, const float *pa
         return refuse("GDN projection shapes");
     if (!params) {
         if (!G.alog || G.ba_VH != d.VH || G.ba_VD != d.VD) return refuse("GDN A_log/dt_bias/gnorm not set");
-        if (!ta || !tb || ta->O != d.VH || tb->O != d.VH || ta->I != tqkv->I || tb->I != tqkv->I ||
+        if (!tensor_live(ta) || !tensor_live(tb) || ta->O != d.VH || tb->O != d.VH || ta->I != tqkv->I || tb->I != tqkv->I ||
             (ta->fmt != 0 && ta->fmt != 1 && ta->fmt != 6) || (tb->fmt != 0 && tb->fmt != 1 && tb->fmt != 6))
             return refuse("GDN a/b projections");
     }
@@ -1188,6 +1188,23 @@ static bool route_tail(int ln_layer, const float *resid, ColiVkTensor *router, i
     (void)E, (void)topk;
     if (logits && !gemv(router, nrm, logits, 1, st)) return false;
     return true;
+}
+
+void layer_shutdown() {
+    for (int i = 0; i < kMaxLayers; i++) {   // arena slices: gone with the arena
+        g_kv[i] = KvState();
+        g_qk[i] = QkNorm();
+        g_gdn[i] = GdnState();
+        g_ln[i] = LnState();
+    }
+    for (int i = 0; i < W_COUNT; i++) scratch_free(&g_w[i].p, &g_w[i].cap);
+    scratch_free((void **)&g_str.d_resid, &g_str.resid_cap);
+    scratch_free((void **)&g_str.d_y, &g_str.dy_cap);
+    scratch_free((void **)&g_str.d_fnw, &g_str.fnw_cap);
+    scratch_free((void **)&g_str.d_xn, &g_str.xn_cap);
+    host_scratch_free((void **)&g_str.h_y, &g_str.hy_cap);
+    host_scratch_free((void **)&g_str.h_nrm, &g_str.hnrm_cap);
+    g_str = StreamState();
 }
 
 }  // namespace coli
@@ -1535,9 +1552,26 @@ COLI_API int coli_vk_stream_begin(const float *x, int D) {
     return 1;
 }
 
+// A fused MoE launch whose bounded wait gave up (or that met a bad expert id) leaves the
+// residual wrong: like a failed fence wait in the reference (c/backend_vulkan.c:1094-1124,
+// G.ready = 0), that disables the device and the call returns 0, so the engine takes its
+// host path.  The stream must be idle (every caller has synchronised).
+static bool stream_moe_ok(const char *who) {
+    const int e = moe_error_take();
+    if (e == 0) return true;
+    fprintf(stderr, "[HIP] %s: fused MoE reported %s\n", who,
+            e == 1 ? "a bounded wait that gave up" : e == 2 ? "an out-of-range expert id" : "a runtime error");
+    return fail(who, hipErrorLaunchFailure);
+}
+
 COLI_API int coli_vk_stream_end(float *x, int D) {
     if (!g_str.live || D != g_str.D) return 0;
     if (!sync_stream("stream end")) return 0;
+    if (!stream_moe_ok("stream end")) {
+        g_str.live = 0;
+        g_str.pending = 0;
+        return 0;
+    }
     if (x && hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) != hipSuccess) return 0;
     if (g_str.pending) {
         int *dh = hist_dev();
@@ -1568,8 +1602,8 @@ COLI_API int coli_vk_stream_add(const float *y, int D) {
 COLI_API const float *coli_vk_stream_nrm(void) { return g_str.live && !g_str.fused_last ? g_str.h_nrm : nullptr; }
 
 COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
-    if (!x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
-    if (!sync_stream("copy resid")) return 0;
+    if (!ok() || !x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
+    if (!sync_stream("copy resid") || !stream_moe_ok("copy resid")) return 0;
     return hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
 }
 
@@ -1597,6 +1631,8 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
     int res[16];
     if (!sync_stream("stream_norm_argmax") || hipMemcpy(res, d_iv, 64, hipMemcpyDeviceToHost) != hipSuccess)
         return 0;
+    if (!stream_moe_ok("stream_norm_argmax")) return 0;
+    if (res[0] < 0 || res[0] >= O) return 0;   // no valid winner: the engine's host scan decides
     *idx = res[0];
     if (val) memcpy(val, &res[8], 4);
     return 1;

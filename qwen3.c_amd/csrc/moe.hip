@@ -24,7 +24,7 @@
 // atomics (single-copy atomic, coherent across the XCDs' L2s): a consumer polls until the
 // tag equals the launch epoch.  There are no counters to order, so no device-scope fences
 // (an L2 write-back each on gfx950) are issued.  Polls are bounded: past the limit they set an
-// error flag and give up, so every wave always exits.
+// error word stamped with the launch's epoch and give up, so every wave always exits.
 #include "moe_common.h"
 
 #include <stdio.h>
@@ -57,7 +57,7 @@ struct MoeArgs {
     unsigned long long *tagv;             // logits [E + 1] | route [kRouteReps][kRouteStride] |
                                           // h [(K + 1) * I] | y [(K + 1) * D]
                                           // (logit E = the shared-expert gate dot)
-    int *err;
+    unsigned long long *err;              // error word: (epoch << 32) | code of a failing launch
     uint32_t epoch;
     int gRows, nG;                        // gate/up rows per tile, tiles per expert
     int nD, nC;                           // down tiles per slot (kDRows rows), combine tiles
@@ -72,12 +72,21 @@ __device__ __forceinline__ void tag_put(unsigned long long *p, uint32_t epoch, f
     __hip_atomic_store(p, ((unsigned long long)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
-// The error flag is read on every 16th poll only: each read is one more memory round trip
-// between a poll and the next.
-__device__ __forceinline__ bool poll_give_up(int *err, int polls) {
+// The error word holds (epoch << 32) | code of a launch that failed (code 1: a bounded wait
+// gave up, 2: a route held an out-of-range expert id).  A wait gives up past kPollLimit
+// polls, or at its 16th poll once its own launch has failed; the word is read on every 16th
+// poll only (each read is one more memory round trip between a poll and the next).  The
+// epoch stamp means no launch has to clear the word: an earlier launch's failure never
+// matches.
+__device__ __forceinline__ void err_set(unsigned long long *err, uint32_t epoch, int code) {
+    __hip_atomic_store(err, ((unsigned long long)epoch << 32) | (uint32_t)code, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool poll_give_up(unsigned long long *err, uint32_t epoch, int polls) {
     if (polls > kPollLimit ||
-        ((polls & 15) == 15 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ((polls & 15) == 15 &&
+         (uint32_t)(__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == epoch)) {
+        err_set(err, epoch, 1);
         return true;
     }
     if (polls < 8) __builtin_amdgcn_s_sleep(1);   // back off: the line may be in demand
@@ -95,11 +104,11 @@ __device__ __forceinline__ unsigned long long *h_of(const MoeArgs &a, int slot) 
 __device__ __forceinline__ unsigned long long *y_of(const MoeArgs &a, int slot) {
     return h_of(a, a.K + 1) + (size_t)slot * a.g.D;
 }
-__device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t epoch, int *err) {
+__device__ __forceinline__ float tag_get(const unsigned long long *p, uint32_t epoch, unsigned long long *err) {
     for (int polls = 0;; polls++) {
         const unsigned long long v = aload(p);
         if ((uint32_t)(v >> 32) == epoch) return __uint_as_float((uint32_t)v);
-        if (poll_give_up(err, polls)) return 0.f;
+        if (poll_give_up(err, epoch, polls)) return 0.f;
     }
 }
 
@@ -376,7 +385,7 @@ __device__ void tile_route(const MoeArgs &a, RouteLds &R) {
             v[q] = aload(&a.tagv[e <= E ? e : E]);
             all &= e > E || (uint32_t)(v[q] >> 32) == a.epoch;
         }
-        if (all || poll_give_up(a.err, polls)) break;
+        if (all || poll_give_up(a.err, a.epoch, polls)) break;
     }
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
@@ -427,7 +436,7 @@ __device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, 
         int e = a.E;
         if (slot < a.K) e = __float_as_int(tag_get(&route_of(a, blockIdx.x % kRouteReps)[slot], a.epoch, a.err));
         if (e < 0 || e > a.E) {
-            __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            err_set(a.err, a.epoch, 2);
             e = a.E;
         }
         *s_e = e;
@@ -454,7 +463,7 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
         int e = a.E;
         if (slot < K) e = __float_as_int(tag_get(&route[slot], a.epoch, a.err));
         if (e < 0 || e > a.E) {
-            __hip_atomic_store(a.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            err_set(a.err, a.epoch, 2);
             e = a.E;
         }
         s_rec[0] = a.rec[e];
@@ -464,12 +473,12 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
     unsigned long long *ys = y_of(a, slot);
     const int nw = a.g.I / 8;
     const uint32_t ep = a.epoch;
-    int *err = a.err;
+    unsigned long long *err = a.err;
     auto gather = [&](float (&hv)[kHWords][8]) {
         if (tid < a.nG) {   // one word per G tile: the tile's last row
             const int r = min((tid + 1) * a.gRows, a.g.I) - 1;
             for (int polls = 0;; polls++)
-                if ((uint32_t)(aload(hs + r) >> 32) == ep || poll_give_up(err, polls)) break;
+                if ((uint32_t)(aload(hs + r) >> 32) == ep || poll_give_up(err, ep, polls)) break;
         }
         lds_barrier();   // no wait for the weight loads in flight
         for (int polls = 0;; polls++) {
@@ -484,7 +493,7 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
                     hv[k][c] = __uint_as_float((uint32_t)v);
                 }
             }
-            if (all || poll_give_up(err, polls)) break;
+            if (all || poll_give_up(err, ep, polls)) break;
         }
     };
     down_slot<TPR>(a.g, s_rec[0], H, r0, gather, [&](int r, float y) { tag_put(&ys[r], ep, y); });
@@ -508,7 +517,7 @@ __device__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
             all &= s >= NS || (uint32_t)(v >> 32) == a.epoch;
             y[s] = __uint_as_float((uint32_t)v);
         }
-        if (all || poll_give_up(a.err, polls)) break;
+        if (all || poll_give_up(a.err, a.epoch, polls)) break;
     }
     float accum = 0.f;
 #pragma unroll
@@ -579,7 +588,7 @@ struct MoeScratch {
 static MoeScratch g_ms;
 
 static bool geom_of(const ColiVkTensor *gt, const ColiVkTensor *dt, MoeGeom &m) {
-    if (!gt || !dt || gt->fmt != 6 || dt->fmt != 6 || gt->layout != kLayoutLanes || dt->layout != kLayoutLanes)
+    if (!tensor_live(gt) || !tensor_live(dt) || gt->fmt != 6 || dt->fmt != 6 || gt->layout != kLayoutLanes || dt->layout != kLayoutLanes)
         return false;
     memset(&m, 0, sizeof(m));
     m.D = gt->I;
@@ -647,26 +656,44 @@ static bool reject(const char *why) {
     return false;
 }
 
-// The layer's MoE block on device pointers (stream-ordered, no sync).  Launches share one
-// scratch area: issue them on one stream.
-bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
-                int *d_idx, float *d_val, hipStream_t st, const float *d_xw, float eps) {
+// Tag words a launch uses: logits [E + 1] | route copies | h [(K + 1) I] | y [(K + 1) D]
+static size_t moe_tag_words(int E, int K, const MoeGeom &m) {
+    return (size_t)E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
+}
+
+// clear n 64-bit words (a fill kernel rather than a memset, so the launch can be captured)
+__global__ void clear_words(unsigned long long *w, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0ull;
+}
+
+// The next launch epoch of a tag buffer.  Tags are 32-bit epochs and a consumer accepts a
+// word whose tag equals its launch's, so when the counter wraps, the tag words and the error
+// word are cleared first: no word written 2^32 launches ago can pass for a new one.  (A
+// fresh buffer holds zeros, and epoch 0 is never used.)
+static uint32_t next_epoch(uint32_t *epoch, unsigned long long *tags, size_t nwords, unsigned long long *err,
+                           hipStream_t st) {
+    if (++*epoch == 0) {
+        hipLaunchKernelGGL(clear_words, dim3(64), dim3(256), 0, st, tags, nwords);
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(64), 0, st, err, (size_t)1);
+        *epoch = 1;
+    }
+    return *epoch;
+}
+
+// Validate a launch against the expert table and fill its arguments (everything but the
+// tag buffer, error word and epoch).
+static bool moe_args(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
+                     int *d_idx, float *d_val, const float *d_xw, float eps, MoeArgs &a) {
     EgTable &T = g_eg;
     if (!ok()) return false;
     if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return reject("no expert table for the layer");
-    if (!router || !d_x || !d_out) return reject("NULL argument");
+    if (!tensor_live(router) || !d_x || !d_out) return reject("NULL argument or stale router handle");
     if (K < 1 || K > kTopK || K > T.E || T.E > kMaxE) return reject("K outside 1..8 or E above 1024");
     if (router->I != T.D || router->O != T.E || (router->fmt != 0 && router->fmt != 1) ||
         router->layout != kLayoutRows)
         return reject("router is not [E, D] fmt 0 or 1");
     for (int e = 0; e <= T.E; e++)
         if (!T.valid[(size_t)layer * (T.E + 1) + e]) return reject("expert table slot not set");
-    const MoeGeom &m = T.geom;
-    const size_t ntag = (size_t)T.E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
-    const size_t misc = 256;
-    if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, misc)) return false;
-    if (++g_ms.epoch == 0) g_ms.epoch = 2;   // 0 is what fresh scratch holds; keep the parity alternating
-    MoeArgs a;
     memset(&a, 0, sizeof(a));
     a.x = d_x;
     a.xw = d_xw;
@@ -683,11 +710,22 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.accumulate = accumulate;
     a.idx_out = d_idx;
     a.val_out = d_val;
+    a.g = T.geom;
+    return true;
+}
+
+// The layer's MoE block on device pointers (stream-ordered, no sync).  Launches share one
+// scratch area: issue them on one stream.
+bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out, int accumulate,
+                int *d_idx, float *d_val, hipStream_t st, const float *d_xw, float eps) {
+    MoeArgs a;
+    if (!moe_args(layer, router, K, d_x, d_out, accumulate, d_idx, d_val, d_xw, eps, a)) return false;
+    const size_t ntag = moe_tag_words(a.E, K, a.g);
+    if (!scratch(&g_ms.tag, &g_ms.tag_cap, ntag * 8) || !scratch(&g_ms.misc, &g_ms.misc_cap, 256)) return false;
     a.tagv = (unsigned long long *)g_ms.tag;
-    a.err = (int *)((uint8_t *)g_ms.misc + 64);
-    a.epoch = g_ms.epoch;
-    a.g = m;
-    return dispatch_shape<LaunchMoe>(m, a, st) || (ok() && reject("expert shape not compiled"));
+    a.err = (unsigned long long *)((uint8_t *)g_ms.misc + 64);
+    a.epoch = next_epoch(&g_ms.epoch, a.tagv, g_ms.tag_cap / 8, a.err, st);
+    return dispatch_shape<LaunchMoe>(a.g, a, st) || (ok() && reject("expert shape not compiled"));
 }
 
 bool moe_ready(int layer) {
@@ -700,9 +738,7 @@ bool moe_ready(int layer) {
 
 bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGeom *geom, int *E) {
     EgTable &T = g_eg;
-    if (!T.d_rec || layer < 0 || layer >= T.n_layers || !T.geom_set) return false;
-    for (int e = 0; e <= T.E; e++)
-        if (!T.valid[(size_t)layer * (T.E + 1) + e]) return false;
+    if (!moe_ready(layer)) return false;
     *d_rec = T.d_rec + (size_t)layer * (T.E + 1);
     *d_shgate = T.d_shgate + (size_t)layer * T.D;
     *geom = T.geom;
@@ -710,17 +746,39 @@ bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGe
     return true;
 }
 
-// 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id
-int moe_error() {
-    if (!g_ms.misc) return 0;
-    int e = 0;
+// The failure code a word holds (its low 32 bits), or 0.
+static int err_code(unsigned long long w) { return (int)(uint32_t)w; }
+
+// 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id.
+int moe_error_take() {
+    unsigned long long *words[1] = {g_ms.misc ? (unsigned long long *)((uint8_t *)g_ms.misc + 64) : nullptr};
+    if (!words[0]) return 0;
     if (hipDeviceSynchronize() != hipSuccess) return -1;
-    if (hipMemcpy(&e, (uint8_t *)g_ms.misc + 64, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
-    if (e) {
-        const int z = 0;
-        if (hipMemcpy((uint8_t *)g_ms.misc + 64, &z, 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    int code = 0;
+    for (unsigned long long *w : words) {
+        if (!w) continue;
+        unsigned long long v = 0;
+        if (hipMemcpy(&v, w, 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+        if (err_code(v)) {
+            if (!code) code = err_code(v);
+            const unsigned long long z = 0;
+            if (hipMemcpy(w, &z, 8, hipMemcpyHostToDevice) != hipSuccess) return -1;
+        }
     }
-    return e;
+    return code;
+}
+
+// Host-forced failure for tests: the error word is stamped with the next scratch launch's
+// epoch, so that launch's bounded waits give up at their 16th poll (the kernels still exit
+// normally) and the word reports the failure.
+static bool moe_error_force(int code) {
+    if (!ok() || !scratch(&g_ms.misc, &g_ms.misc_cap, 256) || code < 1 || code > 2) return false;
+    uint32_t next = g_ms.epoch + 1;
+    if (next == 0) next = 1;
+    const unsigned long long v = ((unsigned long long)next << 32) | (uint32_t)code;
+    const hipError_t e = hipMemcpyAsync((uint8_t *)g_ms.misc + 64, &v, 8, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("moe error word", e);
+    return sync_stream("moe error word");
 }
 
 // ---------------------------------------------------------------- expert group kernels
@@ -877,6 +935,22 @@ __global__ void silu_mul_kernel(const float *g, const float *u, float *h, size_t
 
 static void *g_gu_d = nullptr, *g_gu_h = nullptr;
 static size_t g_gu_dc = 0, g_gu_hc = 0;
+
+void moe_shutdown() {
+    free(g_eg.h_rec);
+    free(g_eg.valid);
+    g_eg = EgTable();   // the device table lived in the arena
+    scratch_free(&g_ms.tag, &g_ms.tag_cap);
+    scratch_free(&g_ms.misc, &g_ms.misc_cap);
+    g_ms.epoch = 0;
+    scratch_free(&g_grp.d_buf, &g_grp.d_cap);
+    host_scratch_free(&g_grp.h_buf, &g_grp.h_cap);
+    scratch_free(&g_grp.d_xs, &g_grp.d_xs_cap);
+    if (g_grp.done) (void)hipEventDestroy(g_grp.done);
+    g_grp = EgGroup();
+    scratch_free(&g_gu_d, &g_gu_dc);
+    host_scratch_free(&g_gu_h, &g_gu_hc);
+}
 
 }  // namespace coli
 
@@ -1116,4 +1190,7 @@ COLI_API int coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, c
 
 // Error flag of the MoE launches since the last call (synchronizes the device):
 // 0 none, 1 a poll gave up, 2 a route held an out-of-range expert id, -1 runtime error.
-COLI_API int coli_hip_moe_error(void) { return moe_error(); }
+COLI_API int coli_hip_moe_error(void) { return moe_error_take(); }
+
+// Test hook: set the error word from the host (see moe_error_force).
+COLI_API int coli_hip_moe_force_error(int code) { return moe_error_force(code) ? 1 : 0; }

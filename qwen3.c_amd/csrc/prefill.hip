@@ -783,7 +783,7 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     const float *shg;
     MoeGeom m;
     int E;
-    if (!ok() || !router || !d_xs || !d_out || S < 1) return false;
+    if (!ok() || !tensor_live(router) || !d_xs || !d_out || S < 1) return false;
     if (!moe_layer(layer, &rec, &shg, &m, &E)) return false;
     if (K < 1 || K > kTopK || K > E || E > kMaxE) return false;
     if (router->I != m.D || router->O != E || (router->fmt != 0 && router->fmt != 1) || router->layout != kLayoutRows)
@@ -856,6 +856,8 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     if (err != hipSuccess) return fail("moe prefill launch", err);
     return true;
 }
+
+void prefill_shutdown() { scratch_free(&g_pf.buf, &g_pf.cap); }
 
 }  // namespace coli
 

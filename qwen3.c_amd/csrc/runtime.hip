@@ -24,6 +24,7 @@ struct Runtime {
     int nblocks = 0;
     size_t used_bytes = 0, tensor_count = 0;
     long fail_after = -1;   // COLI_HIP_FAIL_AFTER=n: the (n+1)-th checked call reports a device loss
+    unsigned gen = 1;       // bumped by every shutdown: handles of an earlier generation are dead
 };
 Runtime G;
 
@@ -97,6 +98,18 @@ bool scratch(void **p, size_t *cap, size_t need) {
     return true;
 }
 
+void scratch_free(void **p, size_t *cap) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+}
+
+void host_scratch_free(void **p, size_t *cap) {
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+}
+
 bool host_scratch(void **p, size_t *cap, size_t need) {
     if (need <= *cap && *p) return true;
     size_t want = need < 4096 ? 4096 : need;
@@ -148,8 +161,12 @@ ColiVkTensor *tensor_alloc(int fmt, int I, int O, int gs) {
     t->w = base;
     t->sz = sfl ? (float *)(base + wbytes) : nullptr;
     t->bytes = wbytes + sbytes;
+    t->wbytes = wbytes;
+    t->gen = G.gen;
     return t;
 }
+
+bool tensor_live(const ColiVkTensor *t) { return t && t->gen == G.gen && t->w; }
 
 size_t tensor_host_row_bytes(const ColiVkTensor *t) {
     return t->fmt == 6 ? (size_t)(t->I + 1) / 2 : t->fmt == 1 ? (size_t)t->I : (size_t)t->I * 4;
@@ -213,7 +230,7 @@ void tensor_register(ColiVkTensor *t) {
 // (the caller keeps its quantized copy as CPU fallback).  Added here: fmt 0 (f32 rows),
 // which the f32 MoE router of the benchmark configurations uses.
 static bool upload(ColiVkTensor **out, const void *w, const float *s, int fmt, int I, int O, int gs) {
-    if (*out) return (*out)->fmt == fmt && (*out)->I == I && (*out)->O == O;
+    if (*out) return tensor_live(*out) && (*out)->fmt == fmt && (*out)->I == I && (*out)->O == O;
     if (!w || ((fmt == 6 || fmt == 1) && !s)) return false;
     ColiVkTensor *t = tensor_alloc(fmt, I, O, gs);
     if (!t) return false;
@@ -279,13 +296,24 @@ COLI_API int coli_vk_init(const char *spv_path) {
     return 1;
 }
 
-// c/backend_vulkan.h:38, c/backend_vulkan.c:4137
+// c/backend_vulkan.h:38, c/backend_vulkan.c:4139-4160.  Every file's state is dropped with
+// the arena: tensors, the expert table, KV/GDN/norm state and scratch buffers.  Handles of
+// the old generation are refused afterwards (coli_vk_tensor_free still releases them),
+// and coli_vk_init can bring the device up again.
 COLI_API void coli_vk_shutdown(void) {
     if (!G.st) return;
     (void)hipStreamSynchronize(G.st);
+    gemv_shutdown();
+    moe_shutdown();
+    prefill_shutdown();
+    layer_shutdown();
+    scratch_free(&g_stage, &g_stage_cap);
     for (int i = 0; i < G.nblocks; i++) (void)hipFree(G.blocks[i].base);
     G.nblocks = 0;
     G.used_bytes = G.tensor_count = 0;
+    (void)hipStreamDestroy(G.st);
+    G.st = nullptr;
+    G.gen++;
     G.ready = 0;
 }
 
@@ -318,21 +346,25 @@ COLI_API int coli_vk_tensor_ensure(ColiVkTensor **tensor, const void *weights, c
     return upload(tensor, weights, scales, fmt, I, O, grp) ? 1 : 0;
 }
 
-// c/backend_vulkan.h:137, c/backend_vulkan.c:4119-4135: the arena slice is not reclaimed.
+// c/backend_vulkan.h:137, c/backend_vulkan.c:4119-4135: the arena slice is not reclaimed;
+// the counters drop weights + scales, as the upload added them (a handle of an earlier
+// generation was already uncounted by the shutdown).
 COLI_API void coli_vk_tensor_free(ColiVkTensor *t) {
     if (!t) return;
-    G.used_bytes -= t->bytes;
-    G.tensor_count--;
+    if (t->gen == G.gen) {
+        G.used_bytes -= t->bytes;
+        G.tensor_count--;
+    }
     free(t);
 }
 
-// c/backend_vulkan.h:138
-COLI_API size_t coli_vk_tensor_bytes(const ColiVkTensor *t) { return t ? t->bytes : 0; }
+// c/backend_vulkan.h:138, c/backend_vulkan.c:4137: the weight bytes (scales not counted)
+COLI_API size_t coli_vk_tensor_bytes(const ColiVkTensor *t) { return t ? t->wbytes : 0; }
 
 // Device view of a tensor for callers that drive kernels on device pointers.
 COLI_API int coli_hip_tensor_info(const ColiVkTensor *t, int *fmt, int *I, int *O, int *gs,
                                   int *row_bytes, void **d_w, void **d_sz) {
-    if (!t) return 0;
+    if (!tensor_live(t)) return 0;
     if (fmt) *fmt = t->fmt;
     if (I) *I = t->I;
     if (O) *O = t->O;

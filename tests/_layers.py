@@ -11,6 +11,7 @@ import ctypes as C
 
 import numpy as np
 
+import _util
 from _util import P
 
 _P = C.c_void_p
@@ -56,24 +57,33 @@ def bind(orc, ref=None):
 
 
 class Mat:
-    """A projection y = W x, W [O, I]: fmt 6 (q, sz) or fmt 0 (f32 rows)."""
+    """A projection y = W x, W [O, I]: fmt 6 (q, sz), fmt 0 (f32 rows) or fmt 1 (int8 rows
+    with per-row power-of-two scales, as vk_dense_init uploads the router and GDN a/b,
+    c/qwen.c:1876-1878).  The oracle sees a fmt-1 matrix as its exact f32 equivalent
+    q * s (_util.int8_rows: bit-identical products for power-of-two scales)."""
 
     def __init__(self, gen, seed, O, I, gs, fmt=6, sigma=0.02):
         self.O, self.I, self.gs, self.fmt = O, I, gs, fmt
         if fmt == 6:
             self.q, self.sz = gen.fmt6(O, I, gs, seed)
             self.w = self.q
+        elif fmt == 1:
+            q8, self.s8, self.w = _util.int8_rows(gen, seed, O, I, sigma)
+            self.q8 = q8.view(np.uint8).reshape(-1)
+            self.q, self.sz = None, None
         else:
             self.w = gen.f32rows(O, I, seed, sigma)
             self.q, self.sz = None, None
 
     def orc(self):
-        return OrcMat(self.fmt, P(self.w), P(self.sz), self.I, self.O, self.gs)
+        return OrcMat(0 if self.fmt == 1 else self.fmt, P(self.w), P(self.sz), self.I, self.O, self.gs)
 
     def ref6(self):
         return RefQ6(P(self.q), P(self.sz))
 
     def upload(self, lib):
+        if self.fmt == 1:
+            return lib.tensor(self.q8, self.s8, 1, self.I, self.O)
         return lib.tensor(self.w, self.sz, self.fmt, self.I, self.O, self.gs)
 
 

@@ -19,13 +19,19 @@ def rms(orc, x, w, eps):
 
 
 class Stack:
-    def __init__(self, lib, gen, base, n_layers, D, gqa, gdn, moe_layer, max_t, ab_fmt=6, first_layer=0):
+    def __init__(self, lib, gen, base, n_layers, D, gqa, gdn, moe_layer, max_t, ab_fmt=6, first_layer=0,
+                 router_f=None, kv_rows=0, state_base=0):
         """gqa: dict(H, KH, hd, rot, gs); gdn: dict(KH, KD, VH, VD, K, gs); moe_layer: a tests/_moe.py
-        Layer whose experts every layer shares (each layer keeps its own norms)."""
-        self.D, self.max_t, self.moe = D, max_t, moe_layer
+        Layer whose experts every layer shares (each layer keeps its own norms).  router_f:
+        the f32 rows the oracle routes with (the exact equivalent of an int8 router; default
+        the layer's f32 router).  kv_rows > 0: every attention cache is seeded with that many
+        random rows (device and oracle alike), so decoding starts deep in the window.
+        state_base: first KV-mirror / GDN-state index of the stack (the library keys that
+        state by index and refuses other dimensions for an index already in use)."""
+        self.D, self.max_t, self.moe, self.router_f = D, max_t, moe_layer, router_f
         self.eps = np.float32(1e-6)
         self.layers = []
-        kvi = gi = 0
+        kvi = gi = state_base
         for i in range(n_layers):
             seed = gen.stream(base, 100 + i)
             if (i + 1) % 4 == 0:
@@ -33,7 +39,16 @@ class Stack:
                 t = [m.upload(lib) for m in (W.q, W.k, W.v, W.o)]
                 lib.kv_ensure(kvi, W.KH * max_t, W.hd, W.hd)
                 lib.gqa_norm_weight(kvi, W.qn, W.kn)
-                self.layers.append(dict(kind="gqa", W=W, t=t, idx=kvi, cache=W.new_cache(max_t)))
+                cache = W.new_cache(max_t)
+                if kv_rows:
+                    for h in range(W.KH):   # rows [h * max_t, h * max_t + kv_rows)
+                        kr = gen.normal(kv_rows * W.hd, gen.stream(seed, 50 + h), 1.0)
+                        vr = gen.normal(kv_rows * W.hd, gen.stream(seed, 60 + h), 1.0)
+                        r0 = h * max_t * W.hd
+                        cache[0][r0:r0 + kv_rows * W.hd] = kr
+                        cache[1][r0:r0 + kv_rows * W.hd] = vr
+                        lib.kv_load(kvi, h * max_t, kr.reshape(kv_rows, W.hd), vr.reshape(kv_rows, W.hd))
+                self.layers.append(dict(kind="gqa", W=W, t=t, idx=kvi, cache=cache))
                 kvi += 1
             else:
                 W = _layers.GdnWeights(gen, seed, D, gdn["KH"], gdn["KD"], gdn["VH"], gdn["VD"], gdn["K"], gdn["gs"],
@@ -54,7 +69,7 @@ class Stack:
         out = W.oracle(orc, L["cache"], self.max_t, pos, x) if L["kind"] == "gqa" else W.oracle(orc, L["state"], x)
         resid = (resid + out).astype(np.float32)
         nrm = rms(orc, resid, W.post_ln, self.eps)
-        moe, idx, val, _ = self.moe.oracle(orc, nrm, K)
+        moe, idx, val, _ = self.moe.oracle(orc, nrm, K, router=self.router_f)
         return (resid + moe).astype(np.float32), nrm, idx, val
 
     # ---- device (stream route_pipe) ---------------------------------------------------

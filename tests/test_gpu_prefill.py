@@ -66,16 +66,20 @@ def cfg4(lib, gen):
     return Table(lib, [Layer(lib, gen, 0xC0F4, 2048, 512, 256, 128)])
 
 
-def test_prefill_cfg4(lib, orc_omp, gen, torch_dev, cfg4):
-    """configs[4] shape at S = 128 tokens (the oracle's cost grows with S; the full
-    S = 512 run is the benchmark's)."""
+@pytest.mark.parametrize("S", [128, 512])
+def test_prefill_cfg4(lib, orc_omp, gen, torch_dev, cfg4, S):
+    """configs[4] at its full M = 512 tokens (and at 128): experts get up to ~30 rows, so the
+    two-x-tile gate/up body runs at D = 2048."""
     import torch
-    L, K, S = cfg4.activate()[0], 8, 128
+    L, K = cfg4.activate()[0], 8
     xs = gen.normal(S * L.D, 0xC0F5)
     got = run_prefill(lib, torch, torch_dev, L, K, xs, S)
     check(orc_omp, L, K, xs, S, got)
     counts = np.bincount(got[1], minlength=L.E)
+    print(f"  rows per expert: max {counts.max()}, empty experts {(counts == 0).sum()}", flush=True)
     assert counts.max() > 8 and (counts == 0).sum() < L.E   # ragged groups
+    if S == 512:
+        assert counts.max() > 16   # an expert with more than one 16-row x tile
 
 
 def test_prefill_cfg4_router_int8(lib, orc_omp, gen, torch_dev, cfg4):
