@@ -240,7 +240,18 @@ int   coli_hip_synth_normal(float *d_dst, size_t n, uint64_t seed, double sigma,
  * them on one stream. */
 int   coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x,
                           float *d_out, int accumulate, int *d_idx, float *d_val, void *stream);
-/* Error word of the MoE launches since the last call (synchronizes the device): 0 none, 1 a bounded wait gave up, 2 an out-of-range
+/* coli_hip_moe_decode without any allocation: same arguments, same kernel and results.  No
+ * counterpart in the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops).  The cross-block words live in a static device
+ * array of 256 KiB per device (error line + 32736 tag words), held until the process
+ * ends: a call needing more tag words ((E + 1) + 128 + (K + 1)(I + D)) is refused with a
+ * message and returns 0.  Nothing needs clearing between calls (words carry the call's
+ * epoch); calls that overlap on one device race on the array.  Errors are reported by
+ * coli_hip_moe_error. */
+int   coli_hip_moe_decode_noalloc(int layer, const ColiVkTensor *router, int K, const float *d_x,
+                                  float *d_out, int accumulate, int *d_idx, float *d_val, void *stream);
+/* Error word of the MoE launches since the last call, coli_hip_moe_decode_noalloc's
+ * included (synchronizes the device): 0 none, 1 a bounded wait gave up, 2 an out-of-range
  * expert id, -1 runtime error.  Reading clears it. */
 int   coli_hip_moe_error(void);
 /* Test hook for the failure path: sets the MoE error word from the host (code 1 or 2), so

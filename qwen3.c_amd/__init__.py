@@ -54,6 +54,7 @@ _SIGS = {
     "coli_hip_moe_decode": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "coli_hip_moe_error": (_I, []),
     "coli_hip_moe_force_error": (_I, [_I]),
+    "coli_hip_moe_decode_noalloc": (_I, [_I, _P, _I, _P, _P, _I, _P, _P, _P]),
     "coli_hip_gemv_error": (_I, []),
     "coli_hip_moe_prefill": (_I, [_I, _P, _I, _P, _I, _P, _P, _P, _P]),
     # attention / GatedDeltaNet layer blocks and the residual stream (c/backend_vulkan.h:110-279)
@@ -287,6 +288,12 @@ class Lib:
     def moe_prefill_dev(self, layer, router, K, d_xs, S, d_out, d_idx=None, d_val=None, stream=None):
         if not self.L.coli_hip_moe_prefill(layer, router.handle, K, d_xs, S, d_out, d_idx, d_val, stream):
             raise RuntimeError("coli_hip_moe_prefill failed")
+
+    def moe_decode_noalloc_dev(self, layer, router, K, d_x, d_out, accumulate=False, d_idx=None, d_val=None,
+                               stream=None):
+        """coli_hip_moe_decode_noalloc; returns its 0/1 result (0: refused)."""
+        return int(self.L.coli_hip_moe_decode_noalloc(layer, router.handle, K, d_x, d_out, int(accumulate), d_idx,
+                                                      d_val, stream))
 
     def moe_error(self):
         return int(self.L.coli_hip_moe_error())

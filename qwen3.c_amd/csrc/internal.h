@@ -91,6 +91,9 @@ bool moe_ready(int layer);
 // an out-of-range expert id.  moe_error_take reads and clears it (synchronises the device);
 // -1 on a runtime error.
 int moe_error_take();
+// Device address of the no-alloc MoE scratch array, looked up once per device with that
+// device current (coli_vk_init).  false: the no-alloc entry point refuses on that device.
+bool moe_noalloc_init(int dev);
 
 // Teardown of each source file's state at coli_vk_shutdown: scratch buffers are freed and
 // every device pointer into the weight arena is forgotten, so calls after a shutdown

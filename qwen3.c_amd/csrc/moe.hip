@@ -746,13 +746,70 @@ bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGe
     return true;
 }
 
+// ---------------------------------------------------------------- allocation-free variant
+// coli_hip_moe_decode_noalloc runs the same launch with its cross-block words in a static
+// device array instead of library scratch, for callers that cannot allocate (HIP graph
+// capture, serving loops).  The array's first 256-byte line holds the error word, the rest
+// the tag words; every device holds its own copy at its own address, looked up once per
+// device at init (hipGetSymbolAddress), and each device keeps its own launch epoch.  Calls
+// on one device share the array: calls that overlap on one device race.
+namespace noalloc {
+constexpr size_t kScratchBytes = (size_t)256 << 10;   // 32736 tag words after the error line
+static __device__ __align__(256) unsigned long long scratch[kScratchBytes / 8];
+}  // namespace noalloc
+
+constexpr int kMaxDevices = 16;
+struct NoAllocDev {
+    unsigned long long *ptr = nullptr;   // device address of noalloc::scratch (never the host symbol)
+    uint32_t epoch = 0;                  // kept across shutdown: the array outlives it
+};
+static NoAllocDev g_na[kMaxDevices];
+
+bool moe_noalloc_init(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return false;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc::scratch));
+    if (e != hipSuccess || !p) {
+        fprintf(stderr, "[HIP] no-alloc MoE scratch: hipGetSymbolAddress failed: %s\n", hipGetErrorString(e));
+        g_na[dev].ptr = nullptr;
+        return false;
+    }
+    g_na[dev].ptr = (unsigned long long *)p;
+    return true;
+}
+
+static bool moe_decode_noalloc(int layer, const ColiVkTensor *router, int K, const float *d_x, float *d_out,
+                               int accumulate, int *d_idx, float *d_val, hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || !g_na[dev].ptr)
+        return reject("no-alloc scratch not set up on this device");
+    MoeArgs a;
+    if (!moe_args(layer, router, K, d_x, d_out, accumulate, d_idx, d_val, nullptr, 0.f, a)) return false;
+    constexpr size_t kErrWords = 256 / 8, kTagWords = noalloc::kScratchBytes / 8 - kErrWords;
+    const size_t ntag = moe_tag_words(a.E, K, a.g);
+    if (ntag > kTagWords) {
+        fprintf(stderr, "[HIP] moe block (no-alloc) refused: needs %zu bytes of tag words, the static scratch holds %zu\n",
+                ntag * 8, kTagWords * 8);
+        return false;
+    }
+    NoAllocDev &n = g_na[dev];
+    a.err = n.ptr;
+    a.tagv = n.ptr + kErrWords;
+    a.epoch = next_epoch(&n.epoch, a.tagv, kTagWords, a.err, st);
+    return dispatch_shape<LaunchMoe>(a.g, a, st) || (ok() && reject("expert shape not compiled"));
+}
+
 // The failure code a word holds (its low 32 bits), or 0.
 static int err_code(unsigned long long w) { return (int)(uint32_t)w; }
 
 // 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id.
+// Covers the scratch launches and the no-alloc launches of the current device.
 int moe_error_take() {
-    unsigned long long *words[1] = {g_ms.misc ? (unsigned long long *)((uint8_t *)g_ms.misc + 64) : nullptr};
-    if (!words[0]) return 0;
+    unsigned long long *words[2] = {g_ms.misc ? (unsigned long long *)((uint8_t *)g_ms.misc + 64) : nullptr,
+                                    nullptr};
+    int dev = -1;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) words[1] = g_na[dev].ptr;
+    if (!words[0] && !words[1]) return 0;
     if (hipDeviceSynchronize() != hipSuccess) return -1;
     int code = 0;
     for (unsigned long long *w : words) {
@@ -1191,6 +1248,15 @@ COLI_API int coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, c
 // Error flag of the MoE launches since the last call (synchronizes the device):
 // 0 none, 1 a poll gave up, 2 a route held an out-of-range expert id, -1 runtime error.
 COLI_API int coli_hip_moe_error(void) { return moe_error_take(); }
+
+// The same block with no allocation: cross-block words in a static device array.
+COLI_API int coli_hip_moe_decode_noalloc(int layer, const ColiVkTensor *router, int K, const float *d_x,
+                                         float *d_out, int accumulate, int *d_idx, float *d_val, void *stream_) {
+    return moe_decode_noalloc(layer, router, K, d_x, d_out, accumulate, d_idx, d_val,
+                              stream_ ? (hipStream_t)stream_ : stream())
+               ? 1
+               : 0;
+}
 
 // Test hook: set the error word from the host (see moe_error_force).
 COLI_API int coli_hip_moe_force_error(int code) { return moe_error_force(code) ? 1 : 0; }

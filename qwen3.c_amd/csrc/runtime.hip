@@ -288,6 +288,7 @@ COLI_API int coli_vk_init(const char *spv_path) {
     if (hipStreamCreateWithFlags(&G.st, hipStreamNonBlocking) != hipSuccess) return 0;
     G.dev = 0;
     G.ncu = p.multiProcessorCount;
+    (void)moe_noalloc_init(G.dev);   // a failure only disables coli_hip_moe_decode_noalloc
     const char *fa = getenv("COLI_HIP_FAIL_AFTER");
     G.fail_after = fa ? atol(fa) : -1;
     G.ready = 1;
