@@ -244,7 +244,7 @@ int   coli_hip_moe_decode(int layer, const ColiVkTensor *router, int K, const fl
  * counterpart in the reference; it is for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops).  The cross-block words live in a static device
  * array of 256 KiB per device (error line + 32736 tag words), held until the process
- * ends: a call needing more tag words ((E + 1) + 128 + (K + 1)(I + D)) is refused with a
+ * ends: a call needing more tag words (3 (E + 1) + 128 + (K + 1)(I + D)) is refused with a
  * message and returns 0.  Nothing needs clearing between calls (words carry the call's
  * epoch); calls that overlap on one device race on the array.  Errors are reported by
  * coli_hip_moe_error. */

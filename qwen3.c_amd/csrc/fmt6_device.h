@@ -182,7 +182,7 @@ __device__ __forceinline__ void rank_select(const float2 *cand, int n, int k, fl
 // Block-wide best-k (k <= K) over per-thread sorted lists; result to out_v/out_i
 // (written by thread 0).  All kThreads threads call.
 template <int K>
-__device__ void block_topk_merge(float (&tv)[K], int (&ti)[K], int k, float *out_v, int *out_i) {
+__device__ __forceinline__ void block_topk_merge(float (&tv)[K], int (&ti)[K], int k, float *out_v, int *out_i) {
     __shared__ float s_v[kWaves][K];
     __shared__ int s_i[kWaves][K];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -334,7 +334,7 @@ __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr,
 }
 
 template <int NT = kThreads>
-__device__ inline void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P) {
+__device__ __forceinline__ void prep_x(const XRegsT<NT> &xr, int gs, int ncols, XPrep &P) {
     const int tid = threadIdx.x;
     const int nwords = ncols / 8, ngrp = (ncols + gs - 1) / gs, wpg = gs / 8;
     // Word w sits in lane w % 64, so a group of wpg <= 16 words (a power of two) is an

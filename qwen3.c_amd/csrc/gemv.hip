@@ -56,7 +56,7 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 }
 
 // merge this block's per-thread lists and publish its k best as partials
-__device__ void topk_publish(float (&tv)[kTopK], int (&ti)[kTopK], const TopkArgs &tk) {
+__device__ __forceinline__ void topk_publish(float (&tv)[kTopK], int (&ti)[kTopK], const TopkArgs &tk) {
     block_topk_merge<kTopK>(tv, ti, tk.k, tk.part_v + blockIdx.x * kTopK, tk.part_i + blockIdx.x * kTopK);
 }
 
@@ -209,7 +209,7 @@ __device__ __forceinline__ unsigned long long wave_rounds(unsigned long long (&L
 // kTopK rounds of a wave maximum over its lanes' list heads (the lane whose head wins
 // moves to its next key), and the 4 wave lists are ranked in LDS.  Keys of another launch
 // carry another tag and are polled until overwritten.
-__device__ void topk_final_block(const TopkArgs &tk, int nblk) {
+__device__ __forceinline__ void topk_final_block(const TopkArgs &tk, int nblk) {
     __shared__ __attribute__((aligned(16))) unsigned long long s_wl[kWaves * kTopK];
     __shared__ unsigned long long s_top[kTopK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

@@ -529,7 +529,7 @@ __device__ __forceinline__ void row_finish(float *x, float *gdst, const RowLd &R
         }
     }
 }
-__device__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
+__device__ __forceinline__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
     RowLd R;
     row_load(R, src, w, a);
     row_finish(x, gdst, R, a);
@@ -797,12 +797,63 @@ __global__ void rms_rows(const float *__restrict__ x, const float *__restrict__ 
     for (int i = threadIdx.x; i < D; i += kThreads) y[i] = x[i] * r * (1.f + w[i]);
 }
 
-// softmax + K greedy picks + renorm of one router row (device top-k of the route tail)
-__global__ __launch_bounds__(kThreads) void route_row(const float *__restrict__ logits, int E, int K, int *idx,
-                                                      float *val) {
+// Router logits of the route tail, one row per wave: lg[e] = the exact dot x . router row e
+// rounded to fp32 (times the int8 row scale), bd[e] = its bound against the reference's
+// sequential fp32 sum (router_row, c/qwen.c:178-189 / 230-238).  fmt 0 or 1 rows.
+__global__ __launch_bounds__(kThreads) void router_lb(const float *__restrict__ x, const uint8_t *__restrict__ rw,
+                                                      const float *__restrict__ rs, int rfmt, int rrb, int E, int D,
+                                                      float *__restrict__ lg, float *__restrict__ bd) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (r >= E) return;   // wave uniform
+    const bool int8 = rfmt == 1;
+    const __amdgpu_buffer_rsrc_t rr = buf_rsrc(rw + (size_t)r * rrb, int8 ? (uint32_t)D : (uint32_t)D * 4u);
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (uint32_t)D * 4u);
+    float4 w[kRouterRC];
+    auto load_row = [&](int c0, float4 (&wv)[kRouterRC]) {
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++) {
+            const int col = c0 + (lane + c * 64) * 4;
+            if (!int8) {
+                const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rr, col * 4, 0, kStream);
+                wv[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+            } else {
+                const uint32_t q = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, col, 0, kStream);
+                wv[c] = make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16),
+                                    (float)(int8_t)(q >> 24));
+            }
+        }
+    };
+    auto load_x = [&](int c0, float4 (&xq)[kRouterRC]) {
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++) {
+            const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, (c0 + (lane + c * 64) * 4) * 4, 0, kCached);
+            xq[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+        }
+    };
+    const float scale = int8 ? rs[r] : 1.f;
+    const float B = router_row(D, scale, int8, w, false, load_row, load_x, [&](float L, float) {
+        if (lane == 0) lg[r] = L;
+    });
+    if (lane == 0) bd[r] = B;
+}
+
+// softmax + K greedy picks + renorm of one router row (device top-k of the route tail),
+// certified against the reference's sequential logits (route_certify); x = the router input.
+__global__ __launch_bounds__(64) void route_row(const float *__restrict__ lb, const float *__restrict__ x,
+                                                const uint8_t *__restrict__ rw, const float *__restrict__ rs,
+                                                int rfmt, int rrb, int D, int E, int K, int *idx, float *val) {
     __shared__ RouteLds R;
-    for (int e = threadIdx.x; e < E; e += kThreads) R.p[e] = logits[e];
-    route_select(R, E, K);
+    __shared__ CertLds C;
+    for (int e = threadIdx.x; e < E; e += 64) {
+        R.p[e] = lb[e];
+        C.l[e] = lb[e];
+        C.b[e] = lb[E + e];
+    }
+    wave_lds_order();
+    route_wave(R, E, K, C.l, C.b);
+    route_certify_wave(
+        R, C, K, D, rfmt == 1, rs, [&](float *xn) { stage_input_wave(x, nullptr, D, 0.f, xn); },
+        [&](int e) { return rw + (size_t)e * rrb; });
     if (threadIdx.x < K) {
         idx[threadIdx.x] = R.idx[threadIdx.x];
         val[threadIdx.x] = R.val[threadIdx.x] / R.vsum;
@@ -869,7 +920,7 @@ static bool put_vec(float **d, int *have, const float *h, int n, const char *who
 // ---------------------------------------------------------------- work buffers
 enum {
     W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_AB, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
-    W_HIST, W_COUNT
+    W_HIST, W_BND, W_COUNT
 };
 struct WorkBuf {
     void *p = nullptr;
@@ -1180,13 +1231,20 @@ const float *stream_nrm_dev(int D) {
 // fused: the layer's MoE block runs on the device (expert table) and accumulates into
 // resid; otherwise idx/val (route_pipe) or nothing is produced here.
 static bool route_tail(int ln_layer, const float *resid, ColiVkTensor *router, int E, int topk, float eps,
-                       float *nrm, float *logits, hipStream_t st) {
+                       float *nrm, float *logits, hipStream_t st, float *bounds = nullptr) {
     const LnState &ln = g_ln[ln_layer];
     hipLaunchKernelGGL(rms_rows, dim3(1), dim3(kThreads), 0, st, resid, ln.post_ln, nrm, ln.D, eps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("post norm launch", e);
-    (void)E, (void)topk;
-    if (logits && !gemv(router, nrm, logits, 1, st)) return false;
+    (void)topk;
+    if (logits) {   // logits [E] (and their bounds [E] at `bounds`, or in work memory)
+        if (router->fmt != 0 && router->fmt != 1) return gemv(router, nrm, logits, 1, st);
+        if (!bounds && !(bounds = wbuf(W_BND, E))) return false;
+        hipLaunchKernelGGL(router_lb, dim3((E + kWaves - 1) / kWaves), dim3(kThreads), 0, st, nrm, router->w,
+                           router->sz, router->fmt, router->row_bytes, E, ln.D, logits, bounds);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail("router launch", e);
+    }
     return true;
 }
 
@@ -1644,7 +1702,7 @@ COLI_API void coli_vk_decode_prof(double decode_ms, int tokens) { (void)decode_m
 // After the block: post_ln, then the fused MoE (device expert table) or the device top-k
 // read back into idx_out / val_out (and nrm into the host cache for stream_nrm).
 static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float eps, int *idx_out, float *val_out) {
-    float *dn = wbuf(W_NRM, g_str.D), *dl = wbuf(W_LOGIT, (size_t)E + 2 * kMaxK);
+    float *dn = wbuf(W_NRM, g_str.D), *dl = wbuf(W_LOGIT, (size_t)2 * E + 2 * kMaxK);
     int *dh = hist_dev();
     if (!dn || !dl || !dh || topk < 1 || topk > kTopK || E > kMaxE) return 0;   // device top-k: K <= 8
     // fused: the MoE block norms the residual itself (post_ln) and adds into it
@@ -1656,12 +1714,13 @@ static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float 
         return 1;
     }
     if (!ok()) return 0;
-    if (!route_tail(ln_layer, g_str.d_resid, router, E, topk, eps, dn, nullptr, stream())) return 0;
+    if (router->fmt != 0 && router->fmt != 1) return 0;   // routers are f32 or int8 rows
+    if (!route_tail(ln_layer, g_str.d_resid, router, E, topk, eps, dn, dl, stream(), dl + E)) return 0;
     g_str.fused_last = 0;
-    if (!gemv(router, dn, dl, 1, stream())) return 0;
-    int *di = (int *)(dl + E);
-    float *dv = dl + E + kMaxK;
-    hipLaunchKernelGGL(route_row, dim3(1), dim3(kThreads), 0, stream(), dl, E, topk, di, dv);
+    int *di = (int *)(dl + 2 * E);
+    float *dv = dl + 2 * E + kMaxK;
+    hipLaunchKernelGGL(route_row, dim3(1), dim3(64), 0, stream(), dl, dn, router->w, router->sz, router->fmt,
+                       router->row_bytes, g_str.D, E, topk, di, dv);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("route launch", e) ? 1 : 0;
     if (!host_scratch((void **)&g_str.h_nrm, &g_str.hnrm_cap, (size_t)(g_str.D + 2 * kMaxK) * 4)) return 0;

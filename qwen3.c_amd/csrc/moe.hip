@@ -54,7 +54,8 @@ struct MoeArgs {
     int accumulate;                       // out += (residual stream) instead of out =
     int *idx_out;                         // optional [K]
     float *val_out;                       // optional [K + 1] (renormed weights, then shgt)
-    unsigned long long *tagv;             // logits [E + 1] | route [kRouteReps][kRouteStride] |
+    unsigned long long *tagv;             // logits [E + 1] | crude / tight bounds [E + 1] each |
+                                          // route [kRouteReps][kRouteStride] |
                                           // h [(K + 1) * I] | y [(K + 1) * D]
                                           // (logit E = the shared-expert gate dot)
     unsigned long long *err;              // error word: (epoch << 32) | code of a failing launch
@@ -96,10 +97,10 @@ __device__ __forceinline__ bool poll_give_up(unsigned long long *err, uint32_t e
 
 // tag-buffer regions
 __device__ __forceinline__ unsigned long long *route_of(const MoeArgs &a, int rep) {
-    return a.tagv + a.E + 1 + (size_t)rep * kRouteStride;
+    return a.tagv + 3 * (a.E + 1) + (size_t)rep * kRouteStride;
 }
 __device__ __forceinline__ unsigned long long *h_of(const MoeArgs &a, int slot) {
-    return a.tagv + a.E + 1 + kRouteReps * kRouteStride + (size_t)slot * a.g.I;
+    return a.tagv + 3 * (a.E + 1) + kRouteReps * kRouteStride + (size_t)slot * a.g.I;
 }
 __device__ __forceinline__ unsigned long long *y_of(const MoeArgs &a, int slot) {
     return h_of(a, a.K + 1) + (size_t)slot * a.g.D;
@@ -132,7 +133,7 @@ constexpr int kHWords = (kMoeMaxI / 8 + kThreads - 1) / kThreads;
 
 // v: the thread's words q = tid + k * kThreads (8 columns each) of the I values (zeros
 // past I).  Group maxima and chunk q sums as in prep_x.  Ends with __syncthreads().
-__device__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
+__device__ __forceinline__ void prep_h(const float (&v)[kHWords][8], int I, int gs, HPrep &H) {
     const int tid = threadIdx.x, nw = I / 8, wpg = gs / 8;
     const bool runs = wpg <= 16 && (wpg & (wpg - 1)) == 0;
     if (!runs) {
@@ -292,11 +293,43 @@ __device__ __forceinline__ float4 int8x4(uint32_t q) {
     return make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16), (float)(int8_t)(q >> 24));
 }
 
-// xn, wn: LDS rows of D floats.  The tile's router rows are loaded first (in flight while
-// the block stages the input row x, normed when a.xw != NULL (c/qwen.c:326-330, x r (1 + w)
-// in the reference's order), into xn); then every wave reads x from LDS.
-__device__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn, float *wn) {
-    constexpr int kRC = 8;   // float4 per lane and pass: 2048 columns
+// The router's input row into LDS (all threads; ends with a barrier): x itself, or with a
+// norm weight the zero-centred RMSNorm of x (c/qwen.c:326-330: double sum of squares,
+// x r (1 + w) in the reference's order).  Router and route tiles run this same code, so
+// they see the same row bit for bit.
+__device__ __forceinline__ void stage_input(const float *x, const float *xw, int D, float eps, float *xn, double *s_red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (!xw) {
+        for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = x[i];
+        __syncthreads();
+        return;
+    }
+    double ss = 0;
+    for (int i = threadIdx.x; i < D; i += kThreads) {
+        const float v = x[i];
+        xn[i] = v;
+        ss += (double)v * v;
+    }
+    ss = wave_sum_dpp(ss);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+    double t = 0;
+    for (int k = 0; k < kWaves; k++) t += s_red[k];
+    const float rs = 1.f / sqrtf((float)(t / D) + eps);
+    for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = xn[i] * rs * (1.f + xw[i]);
+    __syncthreads();
+}
+
+// Bounds of the logits: crude (published with the logits) and tight (published later), the
+// words after the logits (E + 1 each; the shared gate's are not used).
+__device__ __forceinline__ unsigned long long *bounds_of(const MoeArgs &a) { return a.tagv + a.E + 1; }
+__device__ __forceinline__ unsigned long long *tight_of(const MoeArgs &a) { return a.tagv + 2 * (a.E + 1); }
+
+// xn: an LDS row of D floats.  The tile's router rows are loaded first (in flight while the
+// block stages the input row, normed when a.xw != NULL, into xn); then every wave reads x
+// from LDS or global.  Each router row publishes its logit, then its bound (router_row).
+__device__ __forceinline__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), D = a.g.D;
     const int r = r0 + wave;
     const bool live = r <= a.E, gate = r == a.E;   // wave-uniform
@@ -304,47 +337,27 @@ __device__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn, 
     const bool f32 = gate || a.rfmt == 0;
     // buffer loads: columns past D (and rows past E) read 0, no per-lane conditions
     const __amdgpu_buffer_rsrc_t rr = buf_rsrc(row, !live ? 0u : f32 ? (uint32_t)D * 4u : (uint32_t)D);
-    float4 w[kRC];
-    auto load_row = [&](int c0) {
+    float4 w[kRouterRC];
+    auto load_row = [&](int c0, float4 (&wv)[kRouterRC]) {
         if (f32) {
 #pragma unroll
-            for (int c = 0; c < kRC; c++) {
+            for (int c = 0; c < kRouterRC; c++) {
                 const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rr, (c0 + (lane + c * 64) * 4) * 4, 0, kStream);
-                w[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+                wv[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
             }
         } else {
 #pragma unroll
-            for (int c = 0; c < kRC; c++)
-                w[c] = int8x4((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, c0 + (lane + c * 64) * 4, 0, kStream));
+            for (int c = 0; c < kRouterRC; c++)
+                wv[c] = int8x4((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, c0 + (lane + c * 64) * 4, 0, kStream));
         }
     };
-    load_row(0);
-    if (a.xw) {   // the normed input row into LDS (one block reduction)
-        double ss = 0;
-        for (int i = threadIdx.x; i < D; i += kThreads) {
-            const float v = a.x[i];
-            xn[i] = v;
-            wn[i] = a.xw[i];
-            ss += (double)v * v;
-        }
-        ss = wave_sum_dpp(ss);
-        __syncthreads();
-        if (lane == 0) s_red[wave] = ss;
-        __syncthreads();
-        double t = 0;
-        for (int k = 0; k < kWaves; k++) t += s_red[k];
-        const float rs = 1.f / sqrtf((float)(t / D) + a.eps);
-        for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = xn[i] * rs * (1.f + wn[i]);
-        __syncthreads();
-    }
+    load_row(0, w);
+    if (a.xw) stage_input(a.x, a.xw, D, a.eps, xn, s_red);
     if (!live) return;
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)D * 4u);
-    double acc = 0.0;
-    for (int c0 = 0; c0 < D; c0 += kRC * 256) {
-        if (c0) load_row(c0);
-        float4 xq[kRC];
+    auto load_x = [&](int c0, float4 (&xq)[kRouterRC]) {
 #pragma unroll
-        for (int c = 0; c < kRC; c++) {
+        for (int c = 0; c < kRouterRC; c++) {
             const int col = c0 + (lane + c * 64) * 4;
             if (a.xw) {
                 xq[c] = col < D ? *(const float4 *)(xn + col) : make_float4(0.f, 0.f, 0.f, 0.f);   // LDS
@@ -353,80 +366,120 @@ __device__ void tile_router(const MoeArgs &a, int r0, double *s_red, float *xn, 
                 xq[c] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
             }
         }
-#pragma unroll
-        for (int c = 0; c < kRC; c++) {
-            acc = fma((double)xq[c].x, (double)w[c].x, acc);
-            acc = fma((double)xq[c].y, (double)w[c].y, acc);
-            acc = fma((double)xq[c].z, (double)w[c].z, acc);
-            acc = fma((double)xq[c].w, (double)w[c].w, acc);
+    };
+    const bool int8 = !gate && a.rfmt == 1;
+    const float scale = int8 ? a.rs[r] : 1.f;
+    const uint32_t ep = a.epoch;
+    const float B = router_row(D, scale, int8, w, true, load_row, load_x, [&](float L, float Bc) {
+        if (lane == 0) {
+            tag_put(&a.tagv[r], ep, L);
+            if (!gate) tag_put(&bounds_of(a)[r], ep, Bc);
         }
-    }
-    acc = wave_sum_dpp(acc);
-    if (lane == 0) {
-        float l = (float)acc;
-        if (!gate && a.rfmt == 1) l *= a.rs[r];   // c/qwen.c:237: acc * scale[o]
-        tag_put(&a.tagv[r], a.epoch, l);
-    }
+    });
+    if (lane == 0 && !gate) tag_put(&tight_of(a)[r], ep, B);
 }
 
 // ---------------------------------------------------------------- T: route
-// c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate.
-__device__ void tile_route(const MoeArgs &a, RouteLds &R) {
-    const int tid = threadIdx.x, E = a.E, K = a.K;
-    // the thread's logits e = tid + q kThreads <= E (logit E is the shared-expert gate dot),
-    // all polled together: one round trip per poll however many a thread holds
-    constexpr int kPer = (kMaxE + 1 + kThreads - 1) / kThreads;
-    unsigned long long v[kPer];
+// c/qwen.c:332-336 softmax_row, :807-817 top-k and renorm, :833-834 shared gate, on one wave
+// of the tile (route_wave, no block barriers); the picks certified against the reference's
+// sequential fp32 logits (route_certify_wave).
+template <int kPer>   // words per lane: E + 1 <= 64 kPer
+__device__ __forceinline__ void tile_route_n(const MoeArgs &a, RouteLds &R, CertLds &C) {
+    const int lane = threadIdx.x, E = a.E, K = a.K;
+    // the lane's logits e = lane + 64 q <= E (logit E is the shared-expert gate dot) and their
+    // bounds, all polled together: one round trip per poll however many a lane holds
+    unsigned long long v[kPer], vb[kPer];
     for (int polls = 0;; polls++) {
         bool all = true;
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
-            const int e = tid + q * kThreads;
+            const int e = lane + 64 * q;
             v[q] = aload(&a.tagv[e <= E ? e : E]);
+            vb[q] = aload(&bounds_of(a)[e < E ? e : E - 1]);
             all &= e > E || (uint32_t)(v[q] >> 32) == a.epoch;
+            all &= e >= E || (uint32_t)(vb[q] >> 32) == a.epoch;
         }
-        if (all || poll_give_up(a.err, a.epoch, polls)) break;
+        if (__ballot(!all) == 0ull || poll_give_up(a.err, a.epoch, polls)) break;
     }
+    float gate = 0.f;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
+        const int e = lane + 64 * q;
         const float l = __uint_as_float((uint32_t)v[q]);
-        if (e < E) R.p[e] = l;
-        else if (e == E) R.gate = l;
+        if (e < E) {
+            R.p[e] = l;
+            C.l[e] = l;
+            C.b[e] = __uint_as_float((uint32_t)vb[q]);
+        } else if (e == E) {
+            gate = l;
+        }
     }
-    route_select(R, E, K);
-    // thread (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
+    gate = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gate), E & 63));
+    wave_lds_order();
+    route_wave(R, E, K, C.l, C.b);   // with the crude bounds
+    if (R.amb) {   // the tight bounds of the candidates (published by now), and the check again
+        const int nc = R.ncand;
+        for (int r = lane; r < nc; r += 64) {
+            const int e = R.cid[r];
+            const float b = tag_get(&tight_of(a)[e], a.epoch, a.err);
+            R.clo[r] = C.l[e] - b;
+            R.chi[r] = C.l[e] + b;
+        }
+        wave_lds_order();
+        float thr;
+        const int amb = cert_check(R, K, nc, &thr);
+        if (lane == 0) {
+            R.amb = amb;
+            R.thr = thr;
+        }
+        wave_lds_order();
+    }
+    route_certify_wave(
+        R, C, K, a.g.D, a.rfmt == 1, a.rs, [&](float *xn) { stage_input_wave(a.x, a.xw, a.g.D, a.eps, xn); },
+        [&](int e) { return a.rw + (size_t)e * a.rrb; });
+    // lane (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
     // renormed weights, 2K the shared gate
     const float sm = R.vsum;
-    for (int q = tid; q < kRouteReps * kRouteStride; q += kThreads) {
+    for (int q = lane; q < kRouteReps * kRouteStride; q += 64) {
         const int c = q / kRouteStride, k = q % kRouteStride;
         if (k > 2 * K) continue;
-        float v;
-        if (k < K) v = __int_as_float(R.idx[k]);
-        else if (k < 2 * K) v = R.val[k - K] / sm;
-        else v = 1.f / (1.f + expf(-R.gate));
-        tag_put(&route_of(a, c)[k], a.epoch, v);
+        float w;
+        if (k < K) w = __int_as_float(R.idx[k]);
+        else if (k < 2 * K) w = R.val[k - K] / sm;
+        else w = 1.f / (1.f + expf(-gate));
+        tag_put(&route_of(a, c)[k], a.epoch, w);
         if (c == 0) {
             if (k < K && a.idx_out) a.idx_out[k] = R.idx[k];
-            if (k >= K && a.val_out) a.val_out[k - K] = v;
+            if (k >= K && a.val_out) a.val_out[k - K] = w;
         }
     }
 }
 
+__device__ __forceinline__ void tile_route(const MoeArgs &a, RouteLds &R, CertLds &C) {
+    if (threadIdx.x >= 64) return;
+    if (a.E + 1 <= 320) tile_route_n<5>(a, R, C);
+    else if (a.E + 1 <= 576) tile_route_n<9>(a, R, C);
+    else tile_route_n<17>(a, R, C);
+}
+
 // ---------------------------------------------------------------- LDS of the kernel
 struct RouterLds {
-    float xn[kLaneMaxI], wn[kLaneMaxI];   // the normed input row, the norm weight
+    float xn[kLaneMaxI];   // the (normed) input row
+};
+struct RouteTileLds {
+    RouteLds r;
+    CertLds c;
 };
 union MoeLds {
-    RouterLds n;   // R tiles
-    XPrep x;       // G tiles
-    HPrep h;       // D tiles
-    RouteLds r;    // T tile
+    RouterLds n;      // R tiles
+    XPrep x;          // G tiles
+    HPrep h;          // D tiles
+    RouteTileLds t;   // T tile
 };
 
 // ---------------------------------------------------------------- G tile
 template <int LPR, int CU>
-__device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, int *s_e) {
+__device__ __forceinline__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, int *s_e) {
     const MoeGeom &g = a.g;
     const int j = (threadIdx.x & 63) % LPR;
     LaneX<CU> L;   // x digits of the lane first: they do not depend on the route
@@ -456,7 +509,7 @@ __device__ void tile_gateup(const MoeArgs &a, const XPrep &P, int slot, int r0, 
 // out[r] = ((0 + w_0 y_0) + w_1 y_1 ...) + shgt y_sh, the reference's order
 // (c/qwen.c:870-877, :917), polling its rows' tagged y of every slot directly.
 template <int TPR>
-__device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertRec *s_rec) {
+__device__ __forceinline__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertRec *s_rec) {
     const int tid = threadIdx.x, K = a.K;
     const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
     if (tid == 0) {
@@ -500,7 +553,7 @@ __device__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot, int r0, ExpertR
 }
 
 constexpr int kCRows = 64;   // combine tile rows (one thread each)
-__device__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
+__device__ __forceinline__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
     const int tid = threadIdx.x, K = a.K, NS = K + 1, D = a.g.D;
     const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
     const unsigned long long *ys = y_of(a, 0);
@@ -556,10 +609,10 @@ __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
         }
         prep_x(xr, g.gs, ncols, S.x);
     }
-    if (t < tGs) tile_router(a, t * kRRows, s_red, S.n.xn, S.n.wn);
+    if (t < tGs) tile_router(a, t * kRRows, s_red, S.n.xn);
     else if (t < tDsh) tile_gateup<LPRG, kLaneChunks>(a, S.x, K, (t - tGs) * a.gRows, s_e);
     else if (t < tT) tile_dslot<TPRD>(a, S.h, K, (t - tDsh) * kDRows, s_rec);
-    else if (t == tT) tile_route(a, S.r);
+    else if (t == tT) tile_route(a, S.t.r, S.t.c);
     else if (t < tDk) tile_gateup<LPRG, kLaneChunks>(a, S.x, (t - tGk) / a.nG, ((t - tGk) % a.nG) * a.gRows, s_e);
     else if (t < tC) tile_dslot<TPRD>(a, S.h, (t - tDk) / a.nD, ((t - tDk) % a.nD) * kDRows, s_rec);
     else tile_combine(a, (t - tC) * kCRows, s_w);
@@ -656,9 +709,10 @@ static bool reject(const char *why) {
     return false;
 }
 
-// Tag words a launch uses: logits [E + 1] | route copies | h [(K + 1) I] | y [(K + 1) D]
+// Tag words a launch uses: logits [E + 1] | crude bounds [E + 1] | tight bounds [E + 1] |
+// route copies | h [(K + 1) I] | y [(K + 1) D]
 static size_t moe_tag_words(int E, int K, const MoeGeom &m) {
-    return (size_t)E + 1 + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
+    return 3 * ((size_t)E + 1) + kRouteReps * kRouteStride + (size_t)(K + 1) * (m.I + m.D);
 }
 
 // clear n 64-bit words (a fill kernel rather than a memset, so the launch can be captured)

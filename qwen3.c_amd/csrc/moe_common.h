@@ -48,12 +48,18 @@ struct RouteLds {
     float p[kMaxE + 64];               // logits in; exp(l - max), zero padded to a multiple of 64
     unsigned long long cand[kMaxE + 8];   // candidates: expert index, then keys (p bits << 24 | 0xFFFFFF - e)
     unsigned hmax[2 * kWaves];         // half-wave maxima of the exp bits
-    float red[kWaves];
+    float red[kWaves], bred[kWaves];
     float sum, gate, vsum;
     int ncand, tie;
     unsigned long long top[kTopK];     // the first K candidates in rank order
     int idx[kTopK];
     float val[kTopK];
+    // certification (route_wave with bounds): the candidates by rank, their expert ids and
+    // logit intervals [lo, hi]; the lowest pick's lower end; 1 if a decision is ambiguous
+    int cid[kMaxE + 8];
+    float clo[kMaxE + 8], chi[kMaxE + 8];
+    float thr;
+    int amb;
 };
 
 // u32 maximum over each half wave (32 lanes): valid in lanes 31 and 63
@@ -71,169 +77,425 @@ __device__ __forceinline__ float wave_sum_dppf(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Routing of one token on the block (kThreads threads): R.p[0, E) holds the router
-// logits.  c/qwen.c:332-336 softmax_row (max from -1e30, e = expf(l - max), s = sequential
-// sum of e in index order, p = e / s), :807-817 the K greedy picks (strict '>' from the
-// lowest index: the order (p desc, index asc)) and the renorm in rank order.  Leaves the
-// picks in R.idx / R.val (rank order, val = p) and the renorm sum in R.vsum.
+// ---------------------------------------------------------------- certified routing
+// The reference computes a router logit as a sequential fp32 sum of rounded products
+// (c/qwen.c:178-189; int8 rows :230-238, acc * scale after the sum).  The device's logit L
+// is the exact dot rounded once (fp64 accumulation of exact products), and B bounds
+// |L - l_ref| rigorously (running-error analysis of recursive summation, Higham 2002,
+// "Accuracy and Stability of Numerical Algorithms", sec. 4.2): with u = 2^-24, exact
+// products p_i, exact prefix sums S_k and A = sum |p_i|,
+//   |l_ref - sum p_i| <= s (u sum_k |S_k| + u A (1 + u + n gamma_n))      (s: int8 row scale, else 1)
+// and |L - sum p_i s| <= 3.2 u |L| (two roundings).  sum_k |S_k| is bounded from above per
+// block of 4 columns: |S_k| <= |S_b| + (sum of the block's |p|), S_b the prefix before the
+// block, computed in fp32 (its rounding, < 32 n u A over all blocks, is added).  A routing
+// decision between experts whose intervals [L - B, L + B] do not overlap is the
+// reference's; route_certify_wave recomputes l_ref exactly (seq_logit) for every candidate whose
+// interval meets the decision boundary.
+__device__ __forceinline__ float router_bound(float L, float sum_abs_prefix, float A, int n, float scale) {
+    const float u = 0x1p-24f, nu = (float)n * u;
+    const float gam = nu / (1.f - nu);
+    const float sum = sum_abs_prefix + A * (2.f + u + (float)n * gam + 32.f * nu);
+    return (scale * u * sum + 3.2f * u * fabsf(L)) * (1.f + 0x1p-12f) + 0x1p-126f;
+}
+// The same bound with sum_k |S_k| <= sum_k sum_{i<=k} |p_i| = sum_i (n - i) |p_i| (no prefix
+// sums: the router has it when L is ready; about 20x looser).  wsum = sum_i (n - i) |p_i|
+// bounded from above per block of 4 columns by (n - first column) * (the block's sum |p|).
+
+// Inclusive prefix sum over the wave (lane order), fp32, by DPP: row_shr 1/2/4/8 within
+// rows of 16, then row_bcast15 / row_bcast31 across rows.
+__device__ __forceinline__ float wave_scan_incl(float v) {
+#define COLI_SCAN_STEP(ctrl, rmask) \
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), (ctrl), (rmask), 0xF, false))
+    COLI_SCAN_STEP(0x111, 0xF);   // row_shr:1
+    COLI_SCAN_STEP(0x112, 0xF);   // row_shr:2
+    COLI_SCAN_STEP(0x114, 0xF);   // row_shr:4
+    COLI_SCAN_STEP(0x118, 0xF);   // row_shr:8
+    COLI_SCAN_STEP(0x142, 0xA);   // row_bcast15 -> rows 1, 3
+    COLI_SCAN_STEP(0x143, 0xC);   // row_bcast31 -> rows 2, 3
+#undef COLI_SCAN_STEP
+    return v;
+}
+
+// One router row on one wave: L (exact dot rounded to fp32, times the int8 row scale) and
+// its bound B.  The row and x are read in passes of 2048 columns, lane l holding columns
+// c0 + 4 (l + 64 c) .. + 3 for c < 8.  rload(c0, w) fills the lane's 8 float4 weights of a
+// pass (int8 rows converted), xload(c0, xq) its 8 float4 x values; the first pass's weights
+// may be loaded by the caller before (prefetch), pass `w0_loaded`.  publish(L, Bc) is called
+// (on every lane) with the crude bound Bc before the prefix sums of the tight bound (the
+// return value) are computed, so a consumer waiting for L is not delayed by them.
+constexpr int kRouterRC = 8;
+template <typename RLoad, typename XLoad, typename Publish>
+__device__ __forceinline__ float router_row(int D, float scale, bool int8, float4 (&w)[kRouterRC], bool w0_loaded,
+                                            RLoad rload, XLoad xload, Publish publish) {
+    constexpr int kPass = kRouterRC * 256, kMaxPass = (kLaneMaxI + kPass - 1) / kPass;
+    const int lane = threadIdx.x & 63;
+    double acc = 0.0;
+    float T[kMaxPass][kRouterRC];   // per chunk: the lane's 4-column sum of products (fp32)
+    float A = 0.f;                  // the lane's sum of |p|
+    float Wt = 0.f;                 // the lane's sum of (n - i) |p_i| (blocks of 4 from above)
+    float4 xq[kRouterRC];
+    // fp32 estimates for the bound (their rounding is covered by its slack terms)
+    auto terms = [&](int ps) {
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++)
+            T[ps][c] = fmaf(xq[c].w, w[c].w, fmaf(xq[c].z, w[c].z, fmaf(xq[c].y, w[c].y, xq[c].x * w[c].x)));
+    };
+    const int np = (D + kPass - 1) / kPass;
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ps++) {
+        if (ps >= np) break;
+        const int c0 = ps * kPass;
+        if (c0 || !w0_loaded) rload(c0, w);
+        xload(c0, xq);
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++) {
+            acc = fma((double)xq[c].x, (double)w[c].x, acc);
+            acc = fma((double)xq[c].y, (double)w[c].y, acc);
+            acc = fma((double)xq[c].z, (double)w[c].z, acc);
+            acc = fma((double)xq[c].w, (double)w[c].w, acc);
+            const float a = fmaf(fabsf(xq[c].w), fabsf(w[c].w),
+                                 fmaf(fabsf(xq[c].z), fabsf(w[c].z),
+                                      fmaf(fabsf(xq[c].y), fabsf(w[c].y), fabsf(xq[c].x) * fabsf(w[c].x))));
+            A += a;
+            Wt = fmaf((float)(D - (c0 + 4 * (lane + 64 * c))), a, Wt);
+        }
+        if (ps + 1 < np) terms(ps);   // the last pass's terms after the logit is out
+    }
+    acc = wave_sum_dpp(acc);
+    float L = (float)acc;
+    if (int8) L *= scale;   // c/qwen.c:237: acc * scale[o]
+    A = wave_sum_dppf(A);
+    publish(L, router_bound(L, wave_sum_dppf(Wt), A, D, int8 ? scale : 1.f));
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ps++)
+        if (ps == np - 1) terms(ps);
+    // prefix before each lane block: the chunk scans are independent, then the chunk bases
+    float inc[kMaxPass][kRouterRC];
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ps++)
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++) inc[ps][c] = ps < np ? wave_scan_incl(T[ps][c]) : 0.f;
+    float base = 0.f, pre = 0.f;   // prefix before the chunk; sum over blocks of |S_b|
+#pragma unroll
+    for (int ps = 0; ps < kMaxPass; ps++)
+#pragma unroll
+        for (int c = 0; c < kRouterRC; c++) {
+            if (ps >= np) continue;
+            pre += fabsf(base + (inc[ps][c] - T[ps][c]));
+            base += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inc[ps][c]), 63));
+        }
+    pre = 4.f * wave_sum_dppf(pre);
+    return router_bound(L, pre + 4.f * A, A, D, int8 ? scale : 1.f);
+}
+
+// The reference's logit of one router row (c/qwen.c:178-189: acc += x[i] * w[i] in index
+// order, fp32, no contraction; int8 rows :230-238, then acc * scale).  x in LDS; rows are
+// 16-byte aligned (device rows are padded to 16 bytes).
+__device__ __forceinline__ float seq_logit(const float *x, const uint8_t *row, bool int8, int D, float scale) {
+    float acc = 0.f;
+    int i0 = 0;
+    for (; i0 + 64 <= D; i0 += 64) {
+        float w[64];
+        if (!int8) {
+            const float4 *r4 = (const float4 *)(row + (size_t)i0 * 4);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float4 v = r4[j];
+                w[4 * j] = v.x, w[4 * j + 1] = v.y, w[4 * j + 2] = v.z, w[4 * j + 3] = v.w;
+            }
+        } else {
+            const int4 *r4 = (const int4 *)(row + i0);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int4 v = r4[j];
+                const int q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int b = 0; b < 16; b++) w[16 * j + b] = (float)(int8_t)(q[b / 4] >> (8 * (b % 4)));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 64; j++) acc = __fadd_rn(acc, __fmul_rn(x[i0 + j], w[j]));
+    }
+    for (; i0 < D; i0++) {
+        const float w = int8 ? (float)(int8_t)row[i0] : ((const float *)row)[i0];
+        acc = __fadd_rn(acc, __fmul_rn(x[i0], w));
+    }
+    return int8 ? __fmul_rn(acc, scale) : acc;
+}
+
+struct CertLds {
+    float l[kMaxE], b[kMaxE];                      // device logits and their bounds
+    __attribute__((aligned(16))) float x[kLaneMaxI];   // the router's input row (exact path only)
+};
+
+// ---------------------------------------------------------------- routing on one wave
+// Orders this wave's LDS accesses for the compiler: a wave's LDS operations complete in
+// issue order, so what a lane writes is visible to the wave's later reads.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ float wave_min_dpp(float v) { return -wave_max_dpp(-v); }
+
+// Maximum over each aligned run of 8 lanes, in every lane of the run (all lanes active).
+__device__ __forceinline__ uint32_t run8_umax(uint32_t v) {
+    v = COLI_DPP_UMAX(v, 0xB1, 0xF);    // quad_perm [1,0,3,2]
+    v = COLI_DPP_UMAX(v, 0x4E, 0xF);    // quad_perm [2,3,0,1]
+    v = COLI_DPP_UMAX(v, 0x141, 0xF);   // row_half_mirror
+    return v;
+}
+
+// The certainty check over the candidates by rank (R.clo / R.chi, nc of them, the first K
+// the picks): 1 when two consecutive picks' intervals meet or a later candidate's interval
+// reaches the lowest pick's lower end (*thr).  One wave.
+__device__ __forceinline__ int cert_check(const RouteLds &R, int K, int nc, float *thr) {
+    const int lane = threadIdx.x & 63;
+    float t = INFINITY;
+    for (int r = lane; r < K; r += 64) t = fminf(t, R.clo[r]);
+    *thr = wave_min_dpp(t);
+    bool a = false;
+    for (int r = lane; r < nc; r += 64) {
+        if (r >= 1 && r < K) a |= !(R.clo[r - 1] > R.chi[r]);
+        if (r >= K) a |= R.chi[r] >= *thr;
+    }
+    return __ballot(a) != 0ull;
+}
+
+__device__ __forceinline__ int key_expert(unsigned long long k) { return (int)(0xFFFFFFu - (uint32_t)(k & 0xFFFFFFu)); }
+__device__ __forceinline__ float key_value(unsigned long long k) { return __uint_as_float((uint32_t)(k >> 24)); }
+
+// Rank of key `me` among keys[0, n8) (n8 a multiple of 8, zero padded; keys unique), and
+// the largest key below it (0 when none).
+__device__ __forceinline__ int key_rank(const unsigned long long *keys, int n8, unsigned long long me,
+                                        unsigned long long *succ) {
+    int rank = 0;
+    unsigned long long sc = 0ull;
+    for (int o0 = 0; o0 < n8; o0 += 8) {   // 8 broadcast reads in flight, no conditions
+        unsigned long long o8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) o8[u] = keys[o0 + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            rank += o8[u] > me ? 1 : 0;
+            sc = o8[u] < me && o8[u] > sc ? o8[u] : sc;
+        }
+    }
+    *succ = sc;
+    return rank;
+}
+
+// Routing of one token by ONE wave (no block barriers; the block's other waves may do
+// other work or exit).  R.p[0, E) holds the router logits.  c/qwen.c:332-336 softmax_row
+// (max from -1e30, e = expf(l - max), s = sequential sum of e in index order, p = e / s),
+// :807-817 the K greedy picks (strict '>' from the lowest index: the order (p desc, index
+// asc)) and the renorm in rank order.  Leaves the picks in R.idx / R.val (rank order,
+// val = p), the renorm sum in R.vsum, e in R.p and s in R.sum.
 //
-// p = fl(e / s) is monotone in e, so the order (e desc, index asc) is the reference's
-// order (p desc, index asc) unless two distinct e round to the same p; that needs them
-// within 2^-21 relative.  Candidates: the 8 half-wave maxima of e are 8 distinct experts,
-// so with theta the least of them every expert that can reach the K-th p has
-// e >= theta (1 - 2^-21).  They are ranked by (e desc, index asc).  A group of equal p is
-// a run of that order; if it holds distinct e, two neighbours in the run are distinct and
-// within 2^-21, so when any candidate and its successor are, the exact path runs: the
-// sequential sum s of the reference and a re-rank by (p desc, index asc).  Otherwise the
-// e order is the reference's and p = e / s with s from a parallel sum (it only scales the
-// weights: relative error ~1e-7 against the reference's).  Starts and ends with
-// __syncthreads().
-__device__ inline void route_select(RouteLds &R, int E, int K) {
-    constexpr int kPer = kMaxE / kThreads;   // experts per thread
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int Epad = (E + 63) & ~63;
-    __syncthreads();
-    float lv[kPer];
+// p = fl(e / s) is monotone in e, so the order (e desc, index asc) is the reference's order
+// (p desc, index asc) unless two distinct e round to the same p; that needs them within
+// 2^-21 relative.  Candidates: each aligned run of 8 lanes holds 8 kMaxE / 64 experts; the
+// 8 runs' maxima of e are 8 distinct experts, so with theta the least of them every expert
+// that can reach the K-th p has e >= theta (1 - 2^-21).  They are ranked by (e desc, index
+// asc).  A group of equal p is a run of that order; if it holds distinct e, two neighbours
+// in the run are distinct and within 2^-21, so when any candidate and its successor are,
+// the exact path runs: the reference's sequential sum s and a re-rank by (p desc, index
+// asc).  Otherwise the e order is the reference's and p = e / s with s from a parallel sum
+// (it only scales the weights: relative error ~1e-7 against the reference's).
+//
+// With bounds (lg, bd: LDS arrays of the device logits and of bounds on their distance to
+// the reference's logits, router_row) the candidate set widens to every expert whose
+// interval [l - b, l + b] can reach a pick's (e >= theta (1 - 2 Bmax - 2^-19), Bmax the
+// largest bound: exp(-2 Bmax) >= 1 - 2 Bmax), and R.amb = 1 when two consecutive picks'
+// intervals meet or another candidate's interval reaches the lowest pick's lower end
+// (R.thr): then route_certify_wave decides with the reference's logits.  The candidates
+// by rank go to R.cid / R.clo / R.chi.
+template <int kPer>   // experts per lane: E <= 64 kPer
+__device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const float *lg, const float *bd) {
+    const int lane = threadIdx.x & 63;
+    float ev[kPer];
     float m = -1e30f;   // the reference's initial max
+    float bm = 0.f;     // largest bound
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
-        lv[q] = e < E ? R.p[e] : -INFINITY;
-        m = fmaxf(m, lv[q]);
+        const int e = lane + 64 * q;
+        ev[q] = e < E ? R.p[e] : -INFINITY;
+        m = fmaxf(m, ev[q]);
+        if (bd && e < E) bm = fmaxf(bm, bd[e]);
     }
     m = wave_max_dpp(m);
-    if (lane == 0) R.red[wave] = m;
-    if (tid == 0) {
-        R.ncand = 0;
-        R.tie = 0;
-    }
-    __syncthreads();
-    m = R.red[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; w++) m = fmaxf(m, R.red[w]);
-    uint32_t mx = 0u;
-    float ps = 0.f;   // parallel partial sum
+    if (bd) bm = wave_max_dpp(bm);
+    float ps = 0.f;     // parallel partial sum
+    uint32_t gm = 0u;   // the lane's largest e (bits order like the values: e >= 0)
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
-        if (e < Epad) {
-            const float ev = e < E ? expf(lv[q] - m) : 0.f;
-            R.p[e] = ev;
-            ps += ev;
-            mx = max(mx, __float_as_uint(ev));   // ev >= 0: the bits order like the values
-        }
+        const int e = lane + 64 * q;
+        ev[q] = e < E ? expf(ev[q] - m) : 0.f;
+        if (e < E) R.p[e] = ev[q];
+        ps += ev[q];
+        gm = max(gm, __float_as_uint(ev[q]));
     }
-    ps = wave_sum_dppf(ps);
-    mx = half_wave_umax(mx);
-    if (lane == 31 || lane == 63) R.hmax[2 * wave + (lane >> 5)] = mx;
-    __syncthreads();   // R.red is free again: reuse it for the partial sums
-    if (lane == 0) R.red[wave] = ps;
-    uint32_t theta = R.hmax[0];
+    const float s = wave_sum_dppf(ps);
+    gm = run8_umax(gm);   // the maximum of the lane's run of 8
+    uint32_t theta = 0xFFFFFFFFu;
 #pragma unroll
-    for (int i = 1; i < 2 * kWaves; i++) theta = min(theta, R.hmax[i]);
-    const float lo = __uint_as_float(theta) * (1.f - 0x1p-21f);
+    for (int g = 0; g < 8; g++) theta = min(theta, (uint32_t)__builtin_amdgcn_readlane((int)gm, 8 * g));
+    const float lo = __uint_as_float(theta) * (bd ? fmaxf(0.f, 1.f - 2.f * bm - 0x1p-19f) : 1.f - 0x1p-21f);
+    // candidates: compacted into R.cand as keys (e bits << 24 | 0xFFFFFF - index)
+    int nc = 0;
 #pragma unroll
     for (int q = 0; q < kPer; q++) {
-        const int e = tid + q * kThreads;
-        if (e < E && R.p[e] >= lo) R.cand[atomicAdd(&R.ncand, 1)] = (unsigned long long)e;
-    }
-    __syncthreads();
-    const int nc = R.ncand, nc8 = (nc + 7) & ~7;
-    for (int c = tid; c < nc8; c += kThreads) {   // keys by e; zeros pad to a multiple of 8
-        unsigned long long k = 0ull;
-        if (c < nc) {
-            const int e = (int)R.cand[c];
-            k = ((unsigned long long)__float_as_uint(R.p[e]) << 24) | (0xFFFFFFu - (uint32_t)e);
+        const int e = lane + 64 * q;
+        const bool f = e < E && ev[q] >= lo;
+        const unsigned long long mk = __ballot(f);
+        if (f) {
+            const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+            R.cand[pos] = ((unsigned long long)__float_as_uint(ev[q]) << 24) | (0xFFFFFFu - (uint32_t)e);
         }
-        R.cand[c] = k;
+        nc += __popcll(mk);
     }
-    if (tid == 0) {
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) s += R.red[w];
-        R.sum = s;
-    }
-    __syncthreads();
-    // rank by counting (keys are unique); the first K go to R.top.  Each candidate also
-    // finds its successor in that order (the largest key below its own): distinct but close
-    // e there may round to one p, and then the exact path decides.
-    for (int c = tid; c < nc; c += kThreads) {
+    const int nc8 = (nc + 7) & ~7;
+    if (nc + lane < nc8) R.cand[nc + lane] = 0ull;   // pad to a multiple of 8 (zero is below every key)
+    wave_lds_order();
+    // rank by counting; the first K go to R.top.  A candidate whose successor is distinct
+    // but within 2^-21 may share its p: then the exact path decides.
+    bool tie = false;
+    for (int c = lane; c < nc; c += 64) {
         const unsigned long long me = R.cand[c];
-        int rank = 0;
-        unsigned long long succ = 0ull;
-        for (int o0 = 0; o0 < nc8; o0 += 8) {   // 8 broadcast reads in flight, no conditions
-            unsigned long long o8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) o8[u] = R.cand[o0 + u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                rank += o8[u] > me ? 1 : 0;
-                succ = o8[u] < me && o8[u] > succ ? o8[u] : succ;
-            }
-        }
+        unsigned long long succ;
+        const int rank = key_rank(R.cand, nc8, me, &succ);
         if (rank < K) R.top[rank] = me;
-        const float a = __uint_as_float((uint32_t)(me >> 24)), b = __uint_as_float((uint32_t)(succ >> 24));
-        if (succ && b < a && b >= a * (1.f - 0x1p-21f)) R.tie = 1;
+        const float a = key_value(me), b = key_value(succ);
+        tie |= succ && b < a && b >= a * (1.f - 0x1p-21f);
+        if (bd) {
+            const int e = key_expert(me);
+            R.cid[rank] = e;
+            R.clo[rank] = lg[e] - bd[e];
+            R.chi[rank] = lg[e] + bd[e];
+        }
     }
-    __syncthreads();
-    if (R.tie) {   // exact: the reference's sequential sum, then (p desc, index asc)
-        if (tid == 0) {
-            float s = 0.f;
-            for (int e0 = 0; e0 < Epad; e0 += 64) {
-                float4 v[16];
-#pragma unroll
-                for (int c = 0; c < 16; c++) v[c] = *(const float4 *)&R.p[e0 + 4 * c];
-#pragma unroll
-                for (int c = 0; c < 16; c++) {
-                    s += v[c].x;
-                    s += v[c].y;
-                    s += v[c].z;
-                    s += v[c].w;
-                }
-            }
-            R.sum = s;
+    wave_lds_order();
+    int amb = 0;
+    float thr = -INFINITY;
+    if (bd) amb = cert_check(R, K, nc, &thr);
+    float sum = s;
+    if (__ballot(tie)) {   // exact: the reference's sequential sum, then (p desc, index asc)
+        float ss = 0.f;
+        if (lane == 0)
+            for (int e = 0; e < E; e++) ss += R.p[e];
+        sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ss), 0));
+        for (int c = lane; c < nc; c += 64) {
+            const int e = key_expert(R.cand[c]);
+            R.cand[c] = ((unsigned long long)__float_as_uint(R.p[e] / sum) << 24) | (0xFFFFFFu - (uint32_t)e);
         }
-        __syncthreads();
-        const float s = R.sum;
-        for (int c = tid; c < nc; c += kThreads) {
-            const int e = (int)(0xFFFFFFu - (uint32_t)(R.cand[c] & 0xFFFFFFu));
-            R.cand[c] = ((unsigned long long)__float_as_uint(R.p[e] / s) << 24) | (0xFFFFFFu - (uint32_t)e);
-        }
-        __syncthreads();
-        for (int c = tid; c < nc; c += kThreads) {
+        wave_lds_order();
+        for (int c = lane; c < nc; c += 64) {
             const unsigned long long me = R.cand[c];
-            int rank = 0;
-            for (int o0 = 0; o0 < nc8; o0 += 8) {
-                unsigned long long o8[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) o8[u] = R.cand[o0 + u];
-#pragma unroll
-                for (int u = 0; u < 8; u++) rank += o8[u] > me ? 1 : 0;
-            }
+            unsigned long long succ;
+            const int rank = key_rank(R.cand, nc8, me, &succ);
             if (rank < K) R.top[rank] = me;
         }
-        __syncthreads();
-        if (tid < K) {
-            const unsigned long long me = R.top[tid];
-            R.idx[tid] = (int)(0xFFFFFFu - (uint32_t)(me & 0xFFFFFFu));
-            R.val[tid] = __uint_as_float((uint32_t)(me >> 24));
+        wave_lds_order();
+        if (lane < K) {
+            const unsigned long long me = R.top[lane];
+            R.idx[lane] = key_expert(me);
+            R.val[lane] = key_value(me);
         }
-    } else if (tid < K) {
-        const unsigned long long me = R.top[tid];
-        const int e = (int)(0xFFFFFFu - (uint32_t)(me & 0xFFFFFFu));
-        R.idx[tid] = e;
-        R.val[tid] = R.p[e] / R.sum;
+    } else if (lane < K) {
+        const unsigned long long me = R.top[lane];
+        R.idx[lane] = key_expert(me);
+        R.val[lane] = key_value(me) / sum;
     }
-    __syncthreads();
-    if (tid == 0) {   // the renorm sum in rank order (c/qwen.c:816; trailing +0 leaves it unchanged)
-        float v8[kTopK], sm = 0.f;
+    wave_lds_order();
+    if (lane == 0) {   // the renorm sum in rank order (c/qwen.c:816)
+        float sm = 0.f;
+        for (int j = 0; j < K; j++) sm += R.val[j];
+        R.vsum = sm;
+        R.sum = sum;
+        R.ncand = nc;
+        R.amb = amb;
+        R.thr = thr;
+    }
+    wave_lds_order();
+}
+
+// route_wave_n for the number of experts per lane that E needs (E <= kMaxE)
+__device__ __forceinline__ void route_wave(RouteLds &R, int E, int K, const float *lg = nullptr, const float *bd = nullptr) {
+    if (E <= 256) route_wave_n<4>(R, E, K, lg, bd);
+    else if (E <= 512) route_wave_n<8>(R, E, K, lg, bd);
+    else route_wave_n<16>(R, E, K, lg, bd);
+}
+
+// The router's input row into LDS by one wave, bit for bit what the block form stage_input
+// (moe.hip) stages: x itself, or the zero-centred RMSNorm of x with weight xw
+// (c/qwen.c:326-330).  The block form sums squares per thread t over i = t + 256 k, per wave
+// by wave_sum_dpp, then the 4 wave sums in order; lane l here plays threads l + 64 w of the
+// 4 waves w, so every addition happens in the same order.
+__device__ __forceinline__ void stage_input_wave(const float *x, const float *xw, int D, float eps, float *xn) {
+    const int lane = threadIdx.x & 63;
+    if (!xw) {
+        for (int i = lane; i < D; i += 64) xn[i] = x[i];
+        wave_lds_order();
+        return;
+    }
+    double ws[kWaves];
 #pragma unroll
-        for (int j = 0; j < kTopK; j++) v8[j] = j < K ? R.val[j] : 0.f;
+    for (int w = 0; w < kWaves; w++) {
+        double ss = 0;
+        for (int i = lane + 64 * w; i < D; i += kThreads) {
+            const float v = x[i];
+            ss += (double)v * v;
+        }
+        ws[w] = wave_sum_dpp(ss);
+    }
+    double t = 0;
 #pragma unroll
-        for (int j = 0; j < kTopK; j++) sm += v8[j];
+    for (int w = 0; w < kWaves; w++) t += ws[w];
+    const float rs = 1.f / sqrtf((float)(t / D) + eps);
+    for (int i = lane; i < D; i += 64) xn[i] = x[i] * rs * (1.f + xw[i]);
+    wave_lds_order();
+}
+
+// After route_wave with bounds, on the same wave: when a decision was ambiguous (R.amb),
+// every candidate whose interval reaches the lowest pick's lower end (the picks among them)
+// gets its reference logit (seq_logit, one lane each), and the K best of those by (l_ref
+// desc, index asc) are the picks: an expert outside that set is below all K current picks
+// in exact arithmetic too.  Equal reference logits give equal p, so the reference's tie
+// rule (lower index) holds; distinct logits whose p round equal are the documented
+// exact-tie class.  The weights stay p / sum p from the device logits.  stage_x(C.x) fills
+// the input row (this wave only); row(e) is router row e.  Returns at once when nothing was
+// ambiguous.
+template <typename StageX, typename Row>
+__device__ __forceinline__ void route_certify_wave(RouteLds &R, CertLds &C, int K, int D, bool int8, const float *scales,
+                                   StageX stage_x, Row row) {
+    if (!R.amb) return;
+    const int lane = threadIdx.x & 63, nc = R.ncand;
+    const float thr = R.thr;
+    stage_x(C.x);
+    wave_lds_order();
+    for (int r = lane; r < nc; r += 64)   // reference logits over the lower ends
+        if (R.chi[r] >= thr) {
+            const int e = R.cid[r];
+            R.clo[r] = seq_logit(C.x, row(e), int8, D, int8 ? scales[e] : 1.f);
+        }
+    wave_lds_order();
+    for (int r = lane; r < nc; r += 64) {
+        if (!(R.chi[r] >= thr)) continue;
+        const float v = R.clo[r];
+        const int e = R.cid[r];
+        int rank = 0;
+        for (int j = 0; j < nc; j++) {
+            const float o = R.clo[j];
+            rank += (R.chi[j] >= thr && (o > v || (o == v && R.cid[j] < e))) ? 1 : 0;
+        }
+        if (rank < K) R.idx[rank] = e;
+    }
+    wave_lds_order();
+    if (lane < K) R.val[lane] = R.p[R.idx[lane]] / R.sum;
+    wave_lds_order();
+    if (lane == 0) {   // the renorm sum in rank order (c/qwen.c:816)
+        float sm = 0.f;
+        for (int j = 0; j < K; j++) sm += R.val[j];
         R.vsum = sm;
     }
-    __syncthreads();
+    wave_lds_order();
 }
 
 // the expert table of a layer (moe.hip): false if it is not complete

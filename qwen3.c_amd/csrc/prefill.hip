@@ -21,7 +21,7 @@
 // fall out of a 32-bit word after masking even and odd nibbles.  The x digit planes are
 // stored in that order (perm16).
 //
-// Launches: pf_logits (router, fp64 split-K partials) -> pf_route (per token: logits,
+// Launches: pf_logits (router logits, the reference's bits) -> pf_route (per token: logits,
 // routing, shared gate, x digit planes) -> pf_group (positions per expert) -> pf_gateup
 // (gate/up + SwiGLU) -> pf_digits (h as digit planes) -> pf_down -> pf_combine.
 #include "moe_common.h"
@@ -102,107 +102,82 @@ __device__ __forceinline__ void digit8(const float (&v)[8], bool valid, int col,
 }
 
 // ---------------------------------------------------------------- router logits
-// part[z][t][e] = sum over the z-th Dk-column slice of x[t][k] w[e][k]: fp32 values,
-// exact fp64 products, fp64 accumulation (the reference sums in fp32; pf_route adds the
-// slices in order and rounds once).  64 tokens x 64 experts per block of 256 threads,
-// 4 x 4 per thread; the slice is staged in LDS 32 columns at a time, transposed, double
-// buffered.  Router rows f32 (rfmt 0) or int8 (rfmt 1, scale applied by pf_route).
-constexpr int kLT = 64, kLE = 64, kLC = 32;
+// lg[t][e] = the reference's router logit of token t, bit for bit: acc += x[t][k] w[e][k]
+// for k in index order, fp32 products and sums, no contraction (c/qwen.c:178-189); int8
+// rows (rfmt 1) convert each weight and multiply acc by the row scale after the sum
+// (c/qwen.c:230-238).  One output per thread, 16 tokens x 16 experts per block of 256
+// threads; x and w tiles of kLC columns staged in LDS (double buffered), read as float4
+// (4 k per read, each lane's k order unchanged).
+constexpr int kLT = 16, kLE = 16, kLC = 64;
 __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, int S, int D,
-                                                 const uint8_t *__restrict__ rw, int rfmt, int rrb, int E, int Dk,
-                                                 double *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) float s_x[2][kLC][kLT + 4];   // +4: fewer conflicts on the transposed stores
-    __shared__ __attribute__((aligned(16))) float s_w[2][kLC][kLE + 4];
+                                                 const uint8_t *__restrict__ rw, const float *__restrict__ rs,
+                                                 int rfmt, int rrb, int E, float *__restrict__ lg) {
+    __shared__ __attribute__((aligned(16))) float s_x[2][kLT][kLC + 4];
+    __shared__ __attribute__((aligned(16))) float s_w[2][kLE][kLC + 4];
     const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-    const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE, kz = blockIdx.z * Dk;
-    float4 rx[2], rv[2];
-    // staging: row r = idx / 8 of the tile, columns 4 (idx % 8) .. + 3, idx = tid + 256 s
-    // (8 lanes read 128 contiguous bytes of a row)
+    const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE;
+    // staging: thread tid stages float4 (tid & 15) of row tid >> 4 for x and for w
+    const int sr = tid >> 4, sc = 4 * (tid & 15);
+    float4 rx, rv;
     auto load = [&](int kc) {
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int idx = tid + 256 * s, r = idx >> 3, k = kz + kc + 4 * (idx & 7);
-            const int t = t0 + r, e = e0 + r;
-            rx[s] = t < S ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (e >= E) {
-                rv[s] = make_float4(0.f, 0.f, 0.f, 0.f);
-            } else if (rfmt == 0) {
-                rv[s] = *(const float4 *)(rw + (size_t)e * rrb + 4 * (size_t)k);
-            } else {
-                const char4 c = *(const char4 *)(rw + (size_t)e * rrb + k);
-                rv[s] = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
-            }
+        const int t = t0 + sr, e = e0 + sr, k = kc + sc;
+        rx = (t < S && k < D) ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e >= E || k >= D) {
+            rv = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else if (rfmt == 0) {
+            rv = *(const float4 *)(rw + (size_t)e * rrb + 4 * (size_t)k);
+        } else {
+            const char4 c = *(const char4 *)(rw + (size_t)e * rrb + k);
+            rv = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
         }
     };
     auto store = [&](int buf) {
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int idx = tid + 256 * s, r = idx >> 3, c = 4 * (idx & 7);
-            s_x[buf][c][r] = rx[s].x;
-            s_x[buf][c + 1][r] = rx[s].y;
-            s_x[buf][c + 2][r] = rx[s].z;
-            s_x[buf][c + 3][r] = rx[s].w;
-            s_w[buf][c][r] = rv[s].x;
-            s_w[buf][c + 1][r] = rv[s].y;
-            s_w[buf][c + 2][r] = rv[s].z;
-            s_w[buf][c + 3][r] = rv[s].w;
-        }
+        *(float4 *)&s_x[buf][sr][sc] = rx;
+        *(float4 *)&s_w[buf][sr][sc] = rv;
     };
-    double acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
+    float acc = 0.f;
     load(0);
     store(0);
     __syncthreads();
-    for (int kc = 0, buf = 0; kc < Dk; kc += kLC, buf ^= 1) {
-        const bool more = kc + kLC < Dk;
+    for (int kc = 0, buf = 0; kc < D; kc += kLC, buf ^= 1) {
+        const bool more = kc + kLC < D;
         if (more) load(kc + kLC);
+        const int n = D - kc < kLC ? D - kc : kLC;   // D % 4 == 0
 #pragma unroll 4
-        for (int k = 0; k < kLC; k++) {
-            const float4 a = *(const float4 *)&s_x[buf][k][4 * ty];
-            const float4 b = *(const float4 *)&s_w[buf][k][4 * tx];
-            const double ad[4] = {a.x, a.y, a.z, a.w}, bd[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = fma(ad[i], bd[j], acc[i][j]);
+        for (int k = 0; k < n; k += 4) {
+            const float4 a = *(const float4 *)&s_x[buf][ty][k];
+            const float4 w = *(const float4 *)&s_w[buf][tx][k];
+            acc = __fadd_rn(acc, __fmul_rn(a.x, w.x));
+            acc = __fadd_rn(acc, __fmul_rn(a.y, w.y));
+            acc = __fadd_rn(acc, __fmul_rn(a.z, w.z));
+            acc = __fadd_rn(acc, __fmul_rn(a.w, w.w));
         }
         if (more) store(buf ^ 1);
         __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = t0 + 4 * ty + i;
-        if (t >= S) continue;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = e0 + 4 * tx + j;
-            if (e < E) part[((size_t)blockIdx.z * S + t) * E + e] = acc[i][j];
-        }
-    }
+    const int t = t0 + ty, e = e0 + tx;
+    if (t < S && e < E) lg[(size_t)t * E + e] = rfmt == 1 ? __fmul_rn(acc, rs[e]) : acc;
 }
 
 // ---------------------------------------------------------------- route per token
-// One block per token: the router logits (slices of part added in order, rounded once,
-// times the int8 scale; c/qwen.c:237), the routing (route_select), the shared expert's
-// gate sigmoid(x . sh_gate) (fp64 dot; c/qwen.c:1159), and x's digit planes for the
-// projections ([3][S][D] planes, [S][D/128] exponents and sums).
-__global__ __launch_bounds__(kThreads) void pf_route(const double *__restrict__ part, int KS, const float *__restrict__ xs,
-                                                    int S, int D, const float *__restrict__ rs, int rfmt,
-                                                    const float *__restrict__ sh_gate, int E, int K, int *tidx,
-                                                    float *tval, float *tshg, int8_t *__restrict__ xd,
+// One block per token: the routing (route_wave) of the token's reference logits, the
+// shared expert's gate sigmoid(x . sh_gate) (fp64 dot; c/qwen.c:1159), and x's digit
+// planes for the projections ([3][S][D] planes, [S][D/128] exponents and sums).
+__global__ __launch_bounds__(kThreads) void pf_route(const float *__restrict__ lg, const float *__restrict__ xs,
+                                                    int S, int D, const float *__restrict__ sh_gate, int E, int K,
+                                                    int *tidx, float *tval, float *tshg, int8_t *__restrict__ xd,
                                                     int *__restrict__ xe, float *__restrict__ xsum) {
     __shared__ RouteLds R;
     __shared__ double s_red[kWaves];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += kThreads) {
-        double l = 0.0;
-        for (int z = 0; z < KS; z++) l += part[((size_t)z * S + t) * E + e];
-        float lf = (float)l;
-        if (rfmt == 1) lf *= rs[e];
-        R.p[e] = lf;
+    if (wave == 0) {   // one wave routes while the others start on the digit planes
+        for (int e = lane; e < E; e += 64) R.p[e] = lg[(size_t)t * E + e];
+        wave_lds_order();
+        route_wave(R, E, K);
+        if (lane < K) {
+            tidx[t * K + lane] = R.idx[lane];
+            tval[t * K + lane] = R.val[lane] / R.vsum;
+        }
     }
     const float *x = xs + (size_t)t * D;
     const int ngD = D / kGS;
@@ -227,11 +202,6 @@ __global__ __launch_bounds__(kThreads) void pf_route(const double *__restrict__ 
 #pragma unroll
         for (int w = 0; w < kWaves; w++) s += s_red[w];
         R.gate = (float)s;
-    }
-    route_select(R, E, K);
-    if (tid < K) {
-        tidx[t * K + tid] = R.idx[tid];
-        tval[t * K + tid] = R.val[tid] / R.vsum;
     }
     if (tid == 0) tshg[t] = 1.f / (1.f + expf(-R.gate));
 }
@@ -792,10 +762,6 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     if (m.gs != kGS || m.D % kGS || m.I % kGS || m.D > 4096 || m.I > 4096) return false;
     const int D = m.D, I = m.I, np = S * K, P = np + S, ngD = D / kGS, ngI = I / kGS;
     if ((size_t)3 * S * D >= (1u << 31) || (size_t)3 * P * I >= (1u << 31) || (size_t)P * D >= (1u << 31)) return false;
-    // router split-K: slices of Dk columns (a multiple of 32) until about 1024 blocks
-    const int tiles = ((S + kLT - 1) / kLT) * ((E + kLE - 1) / kLE);
-    int KS = 1;
-    while (KS < 16 && D % (2 * KS * kLC) == 0 && tiles * KS < 1024) KS *= 2;
     // scratch layout
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -803,7 +769,7 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
         o += al256(bytes);
         return at;
     };
-    const size_t o_pt = take((size_t)KS * S * E * 8), o_ti = take((size_t)np * 4), o_tv = take((size_t)np * 4),
+    const size_t o_pt = take((size_t)S * E * 4), o_ti = take((size_t)np * 4), o_tv = take((size_t)np * 4),
                  o_sh = take((size_t)S * 4), o_off = take((size_t)(E + 1) * 4), o_pl = take((size_t)np * 4),
                  o_pp = take((size_t)np * 4), o_rk = take((size_t)np * 4), o_xd = take((size_t)3 * S * D),
                  o_xe = take((size_t)S * ngD * 4), o_xs = take((size_t)S * ngD * 4), o_h = take((size_t)P * I * 4),
@@ -811,13 +777,13 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
                  o_he = take((size_t)P * ngI * 4), o_hs = take((size_t)P * ngI * 4), o_y = take((size_t)P * D * 4);
     if (!scratch(&g_pf.buf, &g_pf.cap, o)) return false;
     uint8_t *b = (uint8_t *)g_pf.buf;
-    double *part = (double *)(b + o_pt);
+    float *lg = (float *)(b + o_pt);
     float *tv = d_val ? d_val : (float *)(b + o_tv), *tsh = (float *)(b + o_sh);
     int *ti = d_idx ? d_idx : (int *)(b + o_ti), *off = (int *)(b + o_off);
     int *pl = (int *)(b + o_pl), *pp = (int *)(b + o_pp), *rk = (int *)(b + o_rk);
 
-    hipLaunchKernelGGL(pf_logits, dim3((S + kLT - 1) / kLT, (E + kLE - 1) / kLE, KS), dim3(256), 0, st, d_xs, S, D,
-                       router->w, router->fmt, router->row_bytes, E, D / KS, part);
+    hipLaunchKernelGGL(pf_logits, dim3((S + kLT - 1) / kLT, (E + kLE - 1) / kLE), dim3(256), 0, st, d_xs, S, D,
+                       router->w, router->sz, router->fmt, router->row_bytes, E, lg);
     PfArgs a;
     memset(&a, 0, sizeof(a));
     a.rec = rec;
@@ -841,8 +807,8 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     a.he = (const int *)(b + o_he);
     a.hsum = (const float *)(b + o_hs);
     a.y = (float *)(b + o_y);
-    hipLaunchKernelGGL(pf_route, dim3(S), dim3(kThreads), 0, st, part, KS, d_xs, S, D, router->sz, router->fmt, shg, E,
-                       K, ti, tv, tsh, (int8_t *)(b + o_xd), (int *)(b + o_xe), (float *)(b + o_xs));
+    hipLaunchKernelGGL(pf_route, dim3(S), dim3(kThreads), 0, st, lg, d_xs, S, D, shg, E, K, ti, tv, tsh,
+                       (int8_t *)(b + o_xd), (int *)(b + o_xe), (float *)(b + o_xs));
     hipLaunchKernelGGL(pf_group, dim3(1), dim3(1024), 0, st, ti, np, E, off, pl, pp, rk);
     const int E8 = (E + 7) & ~7;
     auto blocks = [&](int nu) { return ((nu * a.nsp + 7) & ~7) + nu * E8; };

@@ -244,3 +244,19 @@ def test_moe_decode_composition(orc, gen):
     yk = np.empty(D, np.float32)
     orc.orc_expert_mlp_fmt6(eptr(ex, int(idx[0])), P(x), D, I, gs, P(yk))
     assert normrel(yk, y0) < 1e-5
+
+
+def test_neartie_construction_flips_exact_ranking(orc, gen):
+    """The near-tie routers of the GPU routing tests really separate the two orders: the
+    reference's picks (sequential fp32 logits, c/qwen.c:178-189, 807-817) differ from the
+    picks of exact arithmetic both in order (ranks 1-2) and in the set (rank K), so a device
+    that ranked by exact logits would fail those tests."""
+    import _neartie
+    D, E, K = 2048, 256, 8
+    for seed in (0x7E1, 0x7E2, 0x7E3):
+        x = gen.normal(D, seed)
+        W = _neartie.near_tie_router(orc, gen, x, E, D, K, seed)
+        ref, _ = _neartie.route_ref(orc, _neartie.seq_logits(orc, x, W, E, D), K)
+        ex = _neartie.exact_rank(x, W, D, K)
+        assert ref[0] == ex[1] and ref[1] == ex[0], (ref, ex)          # order flipped
+        assert ref[K - 1] != ex[K - 1] and set(ref[:K - 1]) == set(ex[:K - 1])   # the K-th pick differs

@@ -57,7 +57,7 @@ def test_noalloc_matches_alloc(lib, orc, gen, torch_dev):
 
 
 def test_noalloc_refuses_beyond_static_scratch(lib, orc, gen, torch_dev):
-    """D = 4096, K = 8: 9 + 128 + 9 * (512 + 4096) = 41609 tag words > the 32736 the static
+    """D = 4096, K = 8: 27 + 128 + 9 * (512 + 4096) = 41627 tag words > the 32736 the static
     array holds: refused (0); the allocating entry point still runs the block."""
     import torch
     L = Layer(lib, gen, 0xAB00, 4096, 512, 8, 128)
@@ -73,7 +73,7 @@ def test_noalloc_refuses_beyond_static_scratch(lib, orc, gen, torch_dev):
     lib.sync()
     ro, _, _, _ = L.oracle(orc, x, 8)
     assert _util.maxrel_scaled(out.cpu().numpy(), ro) <= 1e-3
-    # a smaller K fits again: 9 + 128 + 3 * 4608 = 13961 words
+    # a smaller K fits again: 27 + 128 + 3 * 4608 = 13979 words
     on = torch.zeros(L.D, device=torch_dev)
     assert lib.moe_decode_noalloc_dev(0, L.router, 2, dx.data_ptr(), on.data_ptr()) == 1
     lib.moe_decode_dev(0, L.router, 2, dx.data_ptr(), out.data_ptr())
