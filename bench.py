@@ -12,9 +12,11 @@ in GB/s from algorithmic bytes (nibbles + f32 [scale, zero] pairs + x + logits) 
 average launch duration, measured with one pair of HIP events around the K launches on
 the library's stream.  `roofline` prices that launch against the 8 TB/s HBM3E peak, with
 `traffic` = HBM bytes per launch from rocprofv3 counters (profiles/gemv6_lmhead_traffic.json).
-`moe_cfg2` times configs[2] (one decode MoE block, one launch) the same way.
-`cpu_baseline` times the reference's own CPU kernel (c/qwen.c:211-229, compiled from the
-reference checkout into oracle/_ref) on this host over a bounded row sample.
+`gemv_cfg0` times configs[0] per launch and sustained over 64 rotated weight copies,
+`moe_cfg2` configs[2] (one decode MoE block, one launch) the same way, `moe_prefill_cfg4`
+and `decode_cfg3` the prefill block and the 40-layer step.  `cpu_baseline` (configs[1] on
+all allowed threads) and `cpu_baselines` (configs[0..2], single thread and OpenMP) time the
+reference's own CPU kernels (compiled from the checkout into oracle/_ref) on this host.
 """
 import argparse
 import ctypes as C
@@ -54,6 +56,15 @@ def profile_traffic(name):
         return None
 
 
+def profile_mfma(kernel):
+    """MFMA utilisation of a prefill kernel from the committed rocprofv3 counter summary."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "pf_mfma_cfg4.json")) as f:
+            return json.load(f)["kernels"][kernel]["mfma_util"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def time_launches(lib, ext, step, steps, warmup):
     """Average duration of `step` (launches on the library stream): one event pair around
     `steps` back-to-back launches; also the host wall time per step."""
@@ -72,6 +83,49 @@ def time_launches(lib, ext, step, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return a.elapsed_time(b) / steps, wall * 1e3 / steps
+
+
+def time_isolated(lib, ext, step, n=40):
+    """Per-launch duration including launch overhead: each launch alone between two
+    synchronisations, an event pair around it; median over n launches."""
+    import torch
+    ts = []
+    for i in range(n):
+        lib.sync()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(ext)
+        step(i)
+        b.record(ext)
+        lib.sync()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def gemv_cfg0(lib, torch, dev, steps, warmup):
+    """one fmt6 GEMV 4096 x 2048 (gs 128).  Per launch (alone, with launch
+    overhead) and sustained (back-to-back launches over 64 weight copies, 303 MB, more than
+    the 256 MB Infinity Cache, so the weights stream from HBM)."""
+    O, K = 4096, 2048
+    ncopy = 64
+    ws = [lib.tensor_synth(6, K, O, GS, 0xC0 * 1000 + c, 0.02) for c in range(ncopy)]
+    x = torch.empty(K, dtype=torch.float32, device=dev)
+    y = torch.empty(O, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(x.data_ptr(), K, 0xC0, 1.0)
+    lib.sync()
+    nbytes = O * K // 2 + O * (K // GS) * 8 + K * 4 + O * 4
+
+    def step(i):
+        lib.gemv_dev(ws[i % ncopy], x.data_ptr(), y.data_ptr())
+
+    ext = torch.cuda.ExternalStream(lib.stream())
+    ms, _ = time_launches(lib, ext, step, max(steps, 4 * ncopy), warmup)
+    iso = time_isolated(lib, ext, step)
+    return {"workload": "cfg0: fmt6 GEMV 4096x2048 gs128 (y only)", "alg_bytes_per_launch": nbytes,
+            "sustained_us_per_op": round(ms * 1e3, 2), "sustained_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "sustained_frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "weight_copies": ncopy,
+            "per_launch_us": round(iso * 1e3, 2), "per_launch_GBs": round(nbytes / (iso * 1e-3) / 1e9, 1)}
 
 
 def moe_cfg2(lib, torch, dev, steps, warmup):
@@ -105,6 +159,7 @@ def moe_cfg2(lib, torch, dev, steps, warmup):
 
     ext = torch.cuda.ExternalStream(lib.stream())
     ms, wall_ms = time_launches(lib, ext, step, steps, warmup)
+    iso = time_isolated(lib, ext, step)
     if lib.moe_error():
         raise RuntimeError("MoE block reported a device-side error")
     # per expert: gate + up (I rows of D) and down (D rows of I): nibbles + [scale, zero]
@@ -115,48 +170,111 @@ def moe_cfg2(lib, torch, dev, steps, warmup):
     return layer, {"workload": "cfg2: MoE block decode, router f32 256x2048 + top-8 of 256 experts + shared, "
                         "gate/up 512x2048 down 2048x512 fmt6 gs128, one launch",
             "us_per_op": round(ms * 1e3, 2), "wall_us_per_step": round(wall_ms * 1e3, 2),
+            "per_launch_us": round(iso * 1e3, 2),
             "alg_bytes_per_launch": nbytes, "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+            "equiv_tok_s_40_layers": round(1.0 / (40 * ms * 1e-3), 1),
             "traffic": profile_traffic("moe_cfg2_traffic.json")}
 
 
-def cpu_baseline(budget_s=12.0):
-    """Reference CPU kernel on a bounded sample of the same workload (rows of W)."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, budget_s, min_n=10, max_n=50):
+    fn()   # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_n or (time.perf_counter() < t_end and len(times) < max_n):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baselines(budget_s=3.0):
+    """The reference's own CPU kernels (c/qwen.c, compiled from the checkout into
+    oracle/_ref; the C restatement oracle/liboracle*.so where that is absent) on this host:
+    configs[0] (matmul_q4g_asym 4096 x 2048), configs[1] (matmul_q4g_asym on a 16384-row
+    sample of the lm_head), configs[2] (moe_token: f32 router, softmax / top-8, 8 + 1
+    experts), each single-threaded (the reference's stock build) and with OpenMP on the
+    threads OMP_NUM_THREADS allows.  Median of >= 10 timed calls after a warm-up."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _util
 
-    ref_path = _util.REF_SO
-    kind = "reference" if os.path.exists(ref_path) else "port"
-    omp = os.environ.get("BENCH_CPU_OMP", "0") == "1"
-    if kind == "reference":
-        so = ref_path.replace("libqwenref.so", "libqwenref_omp.so") if omp else ref_path
-        L = C.CDLL(so)
-        fn = L.ref_matmul_q4g_asym
-    else:
-        L = C.CDLL(_util.ORACLE_OMP_SO if omp else _util.ORACLE_SO)
-        fn = L.orc_matmul_q4g_asym
-    fn.restype = None
-    fn.argtypes = [C.c_void_p] * 4 + [C.c_int] * 3
+    kind = "reference" if os.path.exists(_util.REF_SO) else "port"
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     gen = _util.Gen(_util.load_oracle())
-    rows = 16384
-    q, sz = gen.fmt6(rows, K_HID, GS, 0xC1)
-    x = gen.normal(K_HID, 7)
-    y = np.empty(rows, np.float32)
     P = _util.P
-    fn(P(y), P(x), P(q), P(sz), K_HID, rows, GS)   # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 50:
-        t0 = time.perf_counter()
-        fn(P(y), P(x), P(q), P(sz), K_HID, rows, GS)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    sample_bytes = rows * K_HID // 2 + rows * (K_HID // GS) * 8 + K_HID * 4 + rows * 4
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if omp else 1
-    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"matmul_q4g_asym on {rows} of the 248320 lm_head rows (K=2048, gs=128), "
-                      f"median of {len(times)} runs; full-op time {med * O_VOCAB / rows * 1e3:.1f} ms"}
+    libs = {}
+    for variant in ("single", "omp"):
+        if kind == "reference":
+            so = _util.REF_SO if variant == "single" else _util.REF_SO.replace("libqwenref.so", "libqwenref_omp.so")
+            L = C.CDLL(so)
+            gemv, moe = L.ref_matmul_q4g_asym, L.ref_moe_token
+        else:
+            L = C.CDLL(_util.ORACLE_SO if variant == "single" else _util.ORACLE_OMP_SO)
+            gemv, moe = L.orc_matmul_q4g_asym, None
+        gemv.restype = None
+        gemv.argtypes = [C.c_void_p] * 4 + [C.c_int] * 3
+        if moe is not None:
+            moe.restype = None
+            moe.argtypes = [C.c_void_p] * 5 + [C.c_int] * 5 + [C.c_void_p] * 2
+        libs[variant] = (gemv, moe)
+    out = {"kind": kind, "cpu_model": _cpu_model(), "host_cpus": os.cpu_count(), "omp_threads": threads}
+    # configs[0] and the configs[1] sample
+    for name, rows in (("cfg0", 4096), ("cfg1_sample", 16384)):
+        q, sz = gen.fmt6(rows, K_HID, GS, 0xC1 if rows == 16384 else 0xC0)
+        x = gen.normal(K_HID, 7)
+        y = np.empty(rows, np.float32)
+        nb = rows * K_HID // 2 + rows * (K_HID // GS) * 8 + K_HID * 4 + rows * 4
+        res = {}
+        for variant, (gemv, _) in libs.items():
+            t, n = _median_time(lambda: gemv(P(y), P(x), P(q), P(sz), K_HID, rows, GS), budget_s)
+            res[variant] = {"us_per_op": round(t * 1e6, 1), "GBs": round(nb / t / 1e9, 3), "runs": n}
+            if name == "cfg1_sample":
+                res[variant]["full_lm_head_ms"] = round(t * O_VOCAB / rows * 1e3, 1)
+                res[variant]["lm_head_tok_s"] = round(1.0 / (t * O_VOCAB / rows), 2)
+        out[name] = res
+    # configs[2]: one MoE block (moe_token) over all-resident host experts
+    if libs["single"][1] is not None:
+        D, I, E, K = K_HID, 512, 256, 8
+        mw = _util.MoeWeights(gen, 0xC2, D, I, E, GS)
+        ex = mw.orc_experts()
+        outv = np.empty(D, np.float32)
+        xs = [gen.normal(D, 0xC2 + 100 + i) for i in range(16)]
+        it = [0]
+        per_expert = 2 * (I * D // 2 + I * (D // GS) * 8) + (D * I // 2 + D * (I // GS) * 8)
+        nb = (K + 1) * per_expert + E * D * 4 + 3 * D * 4
+        res = {}
+        for variant, (_, moe) in libs.items():
+            def call():
+                x = xs[it[0] % len(xs)]
+                it[0] += 1
+                moe(P(x), P(mw.router), _util.eptr(ex), _util.eptr(ex, E), P(mw.sh_gate), D, I, E, K, GS, P(outv), None)
+            t, n = _median_time(call, budget_s)
+            res[variant] = {"us_per_op": round(t * 1e6, 1), "GBs": round(nb / t / 1e9, 3), "runs": n,
+                            "equiv_tok_s_40_layers": round(1.0 / (40 * t), 2)}
+        out["cfg2"] = res
+    return out
+
+
+def cpu_baseline(cb):
+    """The contract's cpu_baseline object: configs[1] (the metric's workload) on all
+    allowed threads, from the matrix cpu_baselines measured."""
+    r = cb["cfg1_sample"]["omp"]
+    return {"value": r["GBs"], "unit": "GB/s", "cores": cb["omp_threads"], "kind": cb["kind"],
+            "sample": f"matmul_q4g_asym (c/qwen.c:211-229) on 16384 of the 248320 lm_head rows (K=2048, gs=128), "
+                      f"OpenMP {cb['omp_threads']} threads on {cb['cpu_model']}, median of {r['runs']} runs; "
+                      f"full lm_head {r['full_lm_head_ms']} ms; single-thread {cb['cfg1_sample']['single']['GBs']} GB/s"}
 
 
 def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
@@ -187,7 +305,8 @@ def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
             "alg_bytes": nbytes, "achieved_GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
             "useful_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
-            "frac_bf16_dense_peak": round(flops / (ms * 1e-3) / 2.5e15, 4)}
+            "frac_bf16_dense_peak": round(flops / (ms * 1e-3) / 2.5e15, 4),
+            "mfma_util_counters": {"pf_gateup": profile_mfma("pf_gateup"), "pf_down": profile_mfma("pf_down")}}
 
 
 class DecodeStack:
@@ -400,13 +519,16 @@ def main():
                      "kernel": "gemv6_lanes<32,2,4,2> (fmt6 GEMV + fused top-8)",
                      "alg_bytes_per_launch": bytes_per},
     }
+    out["gemv_cfg0"] = gemv_cfg0(lib, torch, dev, args.steps, args.warmup)
     if not args.no_moe:
         layer, out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
         out["moe_prefill_cfg4"] = moe_prefill_cfg4(lib, torch, dev, layer, max(args.steps // 10, 5), 2)
     if not args.no_decode:
         out["decode_cfg3"] = decode_cfg3(lib, torch, dev, max(args.steps // 10, 5), 3)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline()
+        cb = cpu_baselines()
+        out["cpu_baseline"] = cpu_baseline(cb)
+        out["cpu_baselines"] = cb
     print(json.dumps(out), flush=True)
 
 
