@@ -309,6 +309,60 @@ def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
             "mfma_util_counters": {"pf_gateup": profile_mfma("pf_gateup"), "pf_down": profile_mfma("pf_down")}}
 
 
+def gemm_prefill(lib, torch, dev, steps, warmup):
+    """Dense fmt6 GEMM over S = 512 rows of x on MFMA (the prefill projections that
+    coli_vk_matmul runs for S >= 4, c/backend_vulkan.c:282-299): O = 8192, I = 2048 (the
+    configs[3] GatedDeltaNet qkv rows), two weight copies alternating.  One step = the x
+    digit decomposition + the GEMM launch."""
+    S, O, I = 512, 8192, K_HID
+    ws = [lib.tensor_synth(6, I, O, GS, 0xF40 + c, 0.02) for c in range(2)]
+    x = torch.empty(S * I, dtype=torch.float32, device=dev)
+    y = torch.empty(S * O, dtype=torch.float32, device=dev)
+    lib.synth_normal_dev(x.data_ptr(), S * I, 0xF4, 1.0)
+    lib.sync()
+
+    def step(i):
+        lib.gemv_dev(ws[i & 1], x.data_ptr(), y.data_ptr(), S=S)
+
+    ext = torch.cuda.ExternalStream(lib.stream())
+    ms, _ = time_launches(lib, ext, step, steps, warmup)
+    nbytes = O * I // 2 + O * (I // GS) * 8 + S * I * 4 + S * O * 4
+    flops = 2.0 * S * O * I
+    issued = 3 * 2.0 * (((S + 31) // 32) * 32) * (((O + 127) // 128) * 128) * I   # 3 digit planes, padded tiles
+    sec = ms * 1e-3
+    return {"workload": "dense fmt6 GEMM S=512 x (8192 x 2048) gs128 on MFMA (x digits + GEMM)",
+            "us_per_op": round(ms * 1e3, 2), "tokens_per_s": round(S / sec, 1),
+            "alg_bytes": nbytes, "achieved_GBs": round(nbytes / sec / 1e9, 1),
+            "useful_TFLOPs": round(flops / sec / 1e12, 2),
+            "i8_issued_frac_of_5POPs": round(issued / sec / 5.0e15, 4)}
+
+
+def gdn_prefill_cfg3(lib, calls=5):
+    """One GatedDeltaNet layer at configs[3] geometry over S = 512 tokens through the ABI
+    call the engine makes for prefill (coli_vk_gdn_full_seq, host buffers in and out,
+    c/qwen.c:1370): qkv + z in one GEMM, the chunk's recurrence in one launch, gated norm +
+    out-projection in one GEMM.  Wall clock per call, PCIe included."""
+    import numpy as np
+    D, KH, KD, VH, VD, K, S, layer = K_HID, 16, 128, 32, 128, 4, 512, 150
+    CD = 2 * KH * KD + VH * VD
+    tq = lib.tensor_synth(6, D, CD, GS, 0xF50, 0.02)
+    tz = lib.tensor_synth(6, D, VH * VD, GS, 0xF51, 0.02)
+    to = lib.tensor_synth(6, VH * VD, D, GS, 0xF52, 0.02)
+    rng = np.random.default_rng(0xF53)
+    lib.gdn_setup(layer, VH, KD, VD, K, CD, rng.normal(0, 0.3, CD * K).astype(np.float32))
+    x = rng.normal(0, 1, S * D).astype(np.float32)
+    prm = np.concatenate([rng.uniform(0.5, 1.0, (S, VH)), rng.uniform(0.0, 1.0, (S, VH)),
+                          1.0 + rng.normal(0, 0.1, (S, VD))], axis=1).astype(np.float32)
+    lib.gdn_full_seq(layer, x, prm, tq, tz, to, S, KH, KD, VH, VD, CD, K, 1e-6)   # warm-up
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        lib.gdn_full_seq(layer, x, prm, tq, tz, to, S, KH, KD, VH, VD, CD, K, 1e-6)
+    sec = (time.perf_counter() - t0) / calls
+    return {"workload": "cfg3 GatedDeltaNet layer prefill, 512 tokens (KH 16 KD 128 VH 32 VD 128 conv 4), "
+                        "coli_vk_gdn_full_seq host buffers", "ms_per_call": round(sec * 1e3, 3),
+            "tokens_per_s": round(S / sec, 1), "calls": calls}
+
+
 class DecodeStack:
     """the 40-layer hybrid decode model with random-init weights generated on the
     device.  Layer i is gated GQA when (i + 1) % 4 == 0 (c/qwen.c:398), GatedDeltaNet
@@ -523,6 +577,8 @@ def main():
     if not args.no_moe:
         layer, out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
         out["moe_prefill_cfg4"] = moe_prefill_cfg4(lib, torch, dev, layer, max(args.steps // 10, 5), 2)
+    out["gemm_prefill"] = gemm_prefill(lib, torch, dev, max(args.steps // 10, 5), 2)
+    out["gdn_prefill_cfg3"] = gdn_prefill_cfg3(lib)
     if not args.no_decode:
         out["decode_cfg3"] = decode_cfg3(lib, torch, dev, max(args.steps // 10, 5), 3)
     if not args.no_cpu:

@@ -734,6 +734,7 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
                              (int *)((unsigned long long *)g_keys + n)};
         return launch_lanes_mode<2>(t, d_x, d_y, st, ta) != 0;
     }
+    if (S >= kGemmMinS && gemm6_ok(t)) return gemm6(&t, &d_y, 1, d_x, S, st);   // c/backend_vulkan.c:282-299
     for (int s = 0; s < S; s++)
         if (!launch_one(t, d_x + (size_t)s * t->I, d_y + (size_t)s * t->O, st)) return false;
     return want_k ? topk(d_y, t->O, tk->k, tk->idx, tk->val, st) : true;
@@ -811,9 +812,14 @@ COLI_API int coli_vk_matmul_pair(ColiVkTensor **t1p, float *y1, const void *w1, 
     const size_t xb = (size_t)S * I * 4, y1b = (size_t)S * O1 * 4, yb = y1b + (size_t)S * O2 * 4;
     if (!stage_x(x, xb) || !scratch(&g_st.dy, &g_st.dyc, yb)) return 0;
     float *dy = (float *)g_st.dy;
-    if (!gemv(*t1p, (const float *)g_st.dx, dy, S, stream()) ||
-        !gemv(*t2p, (const float *)g_st.dx, dy + (size_t)S * O1, S, stream()))
+    const ColiVkTensor *tp[2] = {*t1p, *t2p};
+    float *const yp[2] = {dy, dy + (size_t)S * O1};
+    if (S >= kGemmMinS && gemm6_ok(tp[0]) && gemm6_ok(tp[1])) {   // one digit decomposition of x for both
+        if (!gemm6(tp, yp, 2, (const float *)g_st.dx, S, stream())) return 0;
+    } else if (!gemv(tp[0], (const float *)g_st.dx, yp[0], S, stream()) ||
+               !gemv(tp[1], (const float *)g_st.dx, yp[1], S, stream())) {
         return 0;
+    }
     if (!host_scratch(&g_st.hy, &g_st.hyc, yb)) return 0;
     hipError_t e = hipMemcpyAsync(g_st.hy, dy, yb, hipMemcpyDeviceToHost, stream());
     if (e == hipSuccess) e = hipStreamSynchronize(stream());

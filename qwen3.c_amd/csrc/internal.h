@@ -79,6 +79,21 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
 bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t st);
 bool rmsnorm_zc(const float *d_x, const float *d_w, float *d_y, int D, float eps, hipStream_t st);
 
+// Dense GEMM on MFMA over S rows of x (prefill.hip): d_y[i] [S][O_i] = x . t[i]^T for nt
+// fmt6 tensors of group size 128 sharing I (one digit decomposition of x serves all).  gx:
+// x is the GatedDeltaNet recurrence output and goes through its gated output norm first.
+constexpr int kGemmMaxI = kLaneMaxI;
+constexpr int kGemmMinS = 4;            // fewer rows of x: one GEMV launch per row
+struct GatedX {
+    const float *z;        // [S][I] z projection rows
+    const float *gnorm;    // norm weight [VD] of row s at gnorm + s * gstride
+    int gstride, VD;
+    float eps;
+};
+bool gemm6_ok(const ColiVkTensor *t);
+bool gemm6(const ColiVkTensor *const *t, float *const *d_y, int nt, const float *d_x, int S, hipStream_t st,
+           const GatedX *gx = nullptr);
+
 // the layer's MoE block in one launch (moe.hip): out (+)= sum_k val_k y_k + shgt y_sh.
 // d_xw != NULL: d_x is the residual and the block applies the post-attention RMSNorm
 // (weight d_xw, eps) itself.

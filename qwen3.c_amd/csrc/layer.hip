@@ -443,6 +443,198 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
     }
 }
 
+// ---------------------------------------------------------------- GDN over a chunk of tokens
+// The recurrence of n consecutive tokens in one launch (prefill, c/backend_vulkan.c:2018-
+// 2157): the block keeps its (head, 16-column) slice of the state in registers across the
+// tokens and walks them in order.  The conv inputs of all n tokens were projected at once
+// (qkv [n][CD]); each thread keeps its channels' last K - 1 inputs in registers (from the
+// ring for the chunk's first tokens) and prefetches the next token's input while the
+// current one computes.  Per token the arithmetic is gdn_core's with host params: the
+// same conv order, SiLU, l2 norms and delta rule.  The ring is not written here (other
+// blocks still read it for their first tokens): gdn_ring_push stores the chunk's last
+// inputs afterwards.
+struct GdnSeqArgs {
+    const float *qkv;      // [n][CD]
+    const float *ring;     // [K][CD], previous inputs at head + 1 .. head + K - 1 (oldest first)
+    int head, n;
+    const float *convw;    // [CD][K]
+    float *S;              // [VH][VD][KD]
+    float *y;              // [n][VH * VD]
+    const float *params;   // [n][prs]: decay(VH) | beta(VH) | gnorm
+    int prs;
+    float eps;
+    int KH, KD, VH, VD, K, CD;
+};
+
+constexpr int kGdnAhead = 8;   // tokens per load group (inputs in flight one group ahead)
+
+// kSeqCPW state columns per wave, kSeqCols per block.  Measured at configs[3] shapes over 512
+// tokens: one column per wave (four blocks per CU, the conv and norms of q and k recomputed
+// by four times as many blocks) made the whole coli_vk_gdn_full_seq call 1.47 ms against
+// 1.30 ms with four.
+constexpr int kSeqCPW = 4;
+constexpr int kSeqCols = kWaves * kSeqCPW;
+template <int KPL>
+__global__ __launch_bounds__(kThreads) void gdn_seq(GdnSeqArgs g) {
+    // conv outputs of a token, double buffered by token parity: a wave that starts token
+    // t + 1 writes the other buffer, and none can start t + 2 before every wave has passed
+    // t + 1's barrier, i.e. finished reading t's values: one barrier per token
+    __shared__ float s_q[2][kGdnMaxKD], s_k[2][kGdnMaxKD], s_v[2][kSeqCols];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nsl = g.VD / kSeqCols;
+    const int h = blockIdx.x / nsl, c0 = (blockIdx.x % nsl) * kSeqCols;
+    const int src = h / (g.VH / g.KH), KD = g.KD, key_dim = g.KH * KD, K = g.K;
+    float sv[kSeqCPW][KPL];
+#pragma unroll
+    for (int q = 0; q < kSeqCPW; q++) {
+        const float *col = g.S + ((size_t)h * g.VD + c0 + wave * kSeqCPW + q) * KD + lane * KPL;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) sv[q][e] = col[e];
+    }
+    constexpr int kCh = (2 * kGdnMaxKD + kSeqCols + kThreads - 1) / kThreads;
+    const int nch = 2 * KD + kSeqCols;
+    int chn[kCh];
+    float cw[kCh][kGdnMaxK - 1], wl[kCh], win[kCh][kGdnMaxK - 1];
+#pragma unroll
+    for (int i = 0; i < kCh; i++) {
+        const int t = tid + i * kThreads;
+        const bool on = t < nch;
+        chn[i] = !on ? 0
+                 : t < KD ? src * KD + t
+                 : t < 2 * KD ? key_dim + src * KD + (t - KD)
+                              : 2 * key_dim + h * g.VD + c0 + (t - 2 * KD);
+#pragma unroll
+        for (int q = 0; q + 1 < kGdnMaxK; q++) cw[i][q] = on && q + 1 < K ? g.convw[(size_t)chn[i] * K + q] : 0.f;
+        wl[i] = on ? g.convw[(size_t)chn[i] * K + K - 1] : 0.f;
+#pragma unroll
+        for (int q = 0; q + 1 < kGdnMaxK; q++) {
+            int slot = g.head + 1 + q;
+            if (slot >= K) slot -= K;
+            win[i][q] = on && q + 1 < K ? g.ring[(size_t)slot * g.CD + chn[i]] : 0.f;
+        }
+    }
+    // inputs and params by groups of kGdnAhead tokens: the next group's loads go out when a
+    // group starts, so the one wait per group (at its start) finds them long arrived
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qkv, (uint32_t)g.n * (uint32_t)g.CD * 4u);
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(g.params, (uint32_t)g.n * (uint32_t)g.prs * 4u);
+    auto ldf = [](__amdgpu_buffer_rsrc_t r, bool on, uint32_t i) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? (int)(i * 4u) : (int)kOOB, 0, 0));
+    };
+    float xn[kCh][kGdnAhead], dn[kGdnAhead], bn[kGdnAhead];
+    auto group_load = [&](int t0) {
+#pragma unroll
+        for (int j = 0; j < kGdnAhead; j++) {
+            const bool on = t0 + j < g.n;
+            const uint32_t tk = (uint32_t)(t0 + j);
+#pragma unroll
+            for (int i = 0; i < kCh; i++) xn[i][j] = ldf(rq, on && tid + i * kThreads < nch, tk * g.CD + chn[i]);
+            dn[j] = ldf(rp, on, tk * g.prs + h);
+            bn[j] = ldf(rp, on, tk * g.prs + g.VH + h);
+        }
+    };
+    group_load(0);
+    for (int tok0 = 0; tok0 < g.n; tok0 += kGdnAhead) {
+        float xg[kCh][kGdnAhead], dg[kGdnAhead], bg[kGdnAhead];
+#pragma unroll
+        for (int j = 0; j < kGdnAhead; j++) {
+#pragma unroll
+            for (int i = 0; i < kCh; i++) xg[i][j] = xn[i][j];
+            dg[j] = dn[j];
+            bg[j] = bn[j];
+        }
+        if (tok0 + kGdnAhead < g.n) group_load(tok0 + kGdnAhead);
+#pragma unroll
+        for (int j = 0; j < kGdnAhead; j++) {
+            const int tok = tok0 + j;
+            if (tok < g.n) {   // uniform
+                const int pb = j & 1;   // kGdnAhead is even: parity of tok
+                float xin[kCh];
+                const float decay = dg[j], beta = bg[j];
+#pragma unroll
+                for (int i = 0; i < kCh; i++) xin[i] = xg[i][j];
+                // conv1d + SiLU (c/qwen.c:697-707), older inputs first, this token last
+#pragma unroll
+                for (int i = 0; i < kCh; i++) {
+                    const int t = tid + i * kThreads;
+                    float acc = 0.f;
+#pragma unroll
+                    for (int q = 0; q + 1 < kGdnMaxK; q++)
+                        if (q + 1 < K) acc += cw[i][q] * win[i][q];
+                    acc += wl[i] * xin[i];
+                    // the window moves on: the K - 1 newest inputs, oldest first
+#pragma unroll
+                    for (int q = 0; q + 1 < kGdnMaxK; q++) {
+                        if (q + 2 < K) win[i][q] = win[i][q + 1];
+                        else if (q + 2 == K) win[i][q] = xin[i];
+                    }
+                    if (t < nch) {
+                        const float v = silu_f(acc);
+                        if (t < KD) s_q[pb][t] = v;
+                        else if (t < 2 * KD) s_k[pb][t - KD] = v;
+                        else s_v[pb][t - 2 * KD] = v;
+                    }
+                }
+                __syncthreads();
+                // l2norm of q and k (c/qwen.c:713-721), each wave for itself
+                float sq = 0.f, sk = 0.f;
+                for (int d = lane; d < KD; d += 64) {
+                    sq += s_q[pb][d] * s_q[pb][d];
+                    sk += s_k[pb][d] * s_k[pb][d];
+                }
+                sq = wave_sum_f(sq);
+                sk = wave_sum_f(sk);
+                const float rqn = 1.f / sqrtf(sq + g.eps) / sqrtf((float)KD);
+                const float rkn = 1.f / sqrtf(sk + g.eps);
+                float kq[KPL], qq[KPL];
+#pragma unroll
+                for (int e = 0; e < KPL; e++) {
+                    kq[e] = s_k[pb][lane * KPL + e] * rkn;
+                    qq[e] = s_q[pb][lane * KPL + e] * rqn;
+                }
+                // delta rule per column (c/qwen.c:749-767)
+#pragma unroll
+                for (int q = 0; q < kSeqCPW; q++) {
+                    const int vd = c0 + wave * kSeqCPW + q;
+                    float kv = 0.f;
+#pragma unroll
+                    for (int e = 0; e < KPL; e++) {
+                        sv[q][e] *= decay;
+                        kv = fmaf(sv[q][e], kq[e], kv);
+                    }
+                    kv = wave_sum_f(kv);
+                    const float delta = (s_v[pb][vd - c0] - kv) * beta;
+                    float yv = 0.f;
+#pragma unroll
+                    for (int e = 0; e < KPL; e++) {
+                        sv[q][e] = fmaf(kq[e], delta, sv[q][e]);
+                        yv = fmaf(sv[q][e], qq[e], yv);
+                    }
+                    yv = wave_sum_f(yv);
+                    if (lane == 0) g.y[(size_t)tok * g.VH * g.VD + (size_t)h * g.VD + vd] = yv;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kSeqCPW; q++) {
+        float *col = g.S + ((size_t)h * g.VD + c0 + wave * kSeqCPW + q) * KD + lane * KPL;
+#pragma unroll
+        for (int e = 0; e < KPL; e++) col[e] = sv[q][e];
+    }
+}
+
+// The chunk's inputs into the conv ring as if its tokens had been pushed one at a time:
+// token t's input at slot (head + t) % K; only the last K tokens survive.
+__global__ void gdn_ring_push(const float *__restrict__ qkv, int n, float *__restrict__ ring, int head, int K,
+                              int CD) {
+    const int t0 = n > K ? n - K : 0, cnt = n - t0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)cnt * CD;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int t = t0 + (int)(i / CD), c = (int)(i % CD);
+        ring[(size_t)((head + t) % K) * CD + c] = qkv[(size_t)t * CD + c];
+    }
+}
+
 // ---------------------------------------------------------------- GQA attention
 constexpr int kAttT = 32;       // positions per chunk (block)
 constexpr int kAttMaxG = 16;    // query heads per kv head
@@ -920,7 +1112,7 @@ static bool put_vec(float **d, int *have, const float *h, int n, const char *who
 // ---------------------------------------------------------------- work buffers
 enum {
     W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_AB, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
-    W_HIST, W_BND, W_COUNT
+    W_HIST, W_BND, W_SQKV, W_SZ, W_SY, W_COUNT
 };
 struct WorkBuf {
     void *p = nullptr;
@@ -1456,6 +1648,76 @@ COLI_API int coli_vk_gdn_ba_weight(int layer, const float *alog, const float *dt
     return 1;
 }
 
+// GDN prefill over S >= kGemmMinS tokens with host params (c/backend_vulkan.c:2018-2157),
+// per chunk of up to kGdnSeqChunk tokens: qkv and z of all the chunk's rows in one dense
+// GEMM (one digit decomposition of x), the recurrence of the chunk in one gdn_seq launch,
+// the ring push, then the gated norm and out-projection of all rows in one more GEMM.
+// False with nothing launched when the shapes are not the GEMM's or the conv is longer than
+// gdn_seq's register window (the caller then runs the tokens one at a time).
+constexpr int kGdnSeqChunk = 1024;
+static bool gdn_chunks(int gi, const float *dx, const float *dp, int S, const ColiVkTensor *tqkv,
+                       const ColiVkTensor *tz, const ColiVkTensor *tout, float *dout, const GdnDims &d,
+                       hipStream_t st, bool *ran) {
+    *ran = false;
+    if (gi < 0 || gi >= kMaxLayers || S < kGemmMinS) return true;
+    GdnState &G = g_gdn[gi];
+    const int VV = d.VH * d.VD, prs = 2 * d.VH + d.VD;
+    if (!G.S || G.VH != d.VH || G.KD != d.KD || G.VD != d.VD || !G.ring || !G.convw_set || G.K != d.K ||
+        G.CD != d.CD)
+        return true;   // gdn_block refuses these with a message
+    if (d.KH < 1 || d.VH % d.KH || d.CD != 2 * d.KH * d.KD + VV || d.KD % 64 || d.KD > kGdnMaxKD ||
+        d.VD % kSeqCols || d.K < 1 || d.K > kGdnMaxK || d.VD > 512 || (d.VD & (d.VD - 1)))
+        return true;
+    if (!gemm6_ok(tqkv) || !gemm6_ok(tz) || !gemm6_ok(tout) || tqkv->O != d.CD || tz->O != VV || tz->I != tqkv->I ||
+        tout->I != VV)
+        return true;
+    *ran = true;
+    const int D = tqkv->I, Dout = tout->O;
+    for (int s0 = 0; s0 < S; s0 += kGdnSeqChunk) {
+        const int n = min(kGdnSeqChunk, S - s0);
+        float *qkv = wbuf(W_SQKV, (size_t)n * d.CD), *z = wbuf(W_SZ, (size_t)n * VV), *y = wbuf(W_SY, (size_t)n * VV);
+        if (!qkv || !z || !y) return false;
+        const ColiVkTensor *tin[2] = {tqkv, tz};
+        float *const yin[2] = {qkv, z};
+        if (!gemm6(tin, yin, 2, dx + (size_t)s0 * D, n, st)) return false;
+        GdnSeqArgs a;
+        a.qkv = qkv;
+        a.ring = G.ring;
+        a.head = G.head;
+        a.n = n;
+        a.convw = G.convw;
+        a.S = G.S;
+        a.y = y;
+        a.params = dp + (size_t)s0 * prs;
+        a.prs = prs;
+        a.eps = d.eps;
+        a.KH = d.KH;
+        a.KD = d.KD;
+        a.VH = d.VH;
+        a.VD = d.VD;
+        a.K = d.K;
+        a.CD = d.CD;
+        const dim3 grid(d.VH * (d.VD / kSeqCols));
+        switch (d.KD / 64) {
+        case 1: hipLaunchKernelGGL(gdn_seq<1>, grid, dim3(kThreads), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(gdn_seq<2>, grid, dim3(kThreads), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(gdn_seq<4>, grid, dim3(kThreads), 0, st, a); break;
+        default: return refuse("GDN key head dim not in {64, 128, 256}");
+        }
+        const int pushed = min(n, d.K) * d.CD;
+        hipLaunchKernelGGL(gdn_ring_push, dim3((pushed + 255) / 256), dim3(256), 0, st, qkv, n, G.ring, G.head, d.K,
+                           d.CD);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail("GDN chunk launch", e);
+        G.head = (G.head + n) % d.K;
+        const GatedX gx = {z, dp + (size_t)s0 * prs + 2 * d.VH, prs, d.VD, d.eps};
+        const ColiVkTensor *to[1] = {tout};
+        float *const yo[1] = {dout + (size_t)s0 * Dout};
+        if (!gemm6(to, yo, 1, y, n, st, &gx)) return false;
+    }
+    return true;
+}
+
 static int gdn_rows(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_t, ColiVkTensor *gz_t,
                     const float *params, ColiVkTensor *out_t, float *out, const GdnDims &d, int Dout) {
     if (!ok() || !x || !params || !out || S < 1 || !gqkv_t || gqkv_t->I != D || !out_t || out_t->O != Dout)
@@ -1466,7 +1728,9 @@ static int gdn_rows(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_
     if (!dx || !dp || !dout || !h2d(dx, x, (size_t)S * D * 4, "gdn rows") ||
         !h2d(dp, params, (size_t)S * prs * 4, "gdn params"))
         return 0;
-    for (int s = 0; s < S; s++)
+    bool ran;
+    if (!gdn_chunks(layer, dx, dp, S, gqkv_t, gz_t, out_t, dout, d, stream(), &ran)) return 0;
+    for (int s = 0; !ran && s < S; s++)
         if (!gdn_block(layer, dx + (size_t)s * D, nullptr, dp + (size_t)s * prs, gqkv_t, gz_t, nullptr, nullptr,
                        out_t, dout + (size_t)s * Dout, false, d, stream()))
             return 0;

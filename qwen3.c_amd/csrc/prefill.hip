@@ -335,44 +335,99 @@ __device__ __forceinline__ void pf_wgroups(uint4 (&d)[4]) {
     pf_swap(d[2], d[3]);   // groups 4 S + 2, 4 S + 3
 }
 
-// Gate/up + SwiGLU.  Unit = 64 columns of h: wave w owns gate and up rows
-// 64 u + 16 w .. + 15.  Per pass of <= 32 rows of x, supersteps of 4 groups: the x digit
-// planes of the pass's rows for the superstep sit in LDS (each thread stages its row's
-// 12 x 16 bytes), the next superstep's x digits and then its weight slots are loaded
-// while this one computes, so the in-order wait for those x digits never covers the
-// weights.  Each (matrix, digit, 16-row tile) is two MFMAs per group, folded in fp32 with
-// the group's scale.  h = silu(gate) * up (c/qwen.c:780-786, silu c/qwen.c:173) goes out
-// as fp32 rows.
-__global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
+// Dense GEMM over S rows of x (prefill projections, c/shaders/qmatmul_mm.comp): Y[s][o] =
+// sum_i x[s][i] W[o][i] for an fmt6 tensor of group size 128.  A unit is 128 output rows
+// (two 16-row tiles per wave) and one pass of <= 32 rows of x; the units of one row block
+// run on one XCD (workgroups go to the 8 XCDs round-robin), where their weights stay in L2.
+struct GemmArgs {
+    const uint8_t *w;       // lanes layout
+    const float *sz;        // [O][I / 128] [scale, zero]
+    int O, I, rb, nl;
+    const int8_t *xd;       // x digit planes [3][S][I]
+    const int *xe;          // [S][I / 128]
+    const float *xsum;
+    int S, nu, npass;       // rows of x; row blocks ceil(O / 128); passes ceil(S / 32)
+    float *y;               // [S][O]
+};
+constexpr int kGR = 2 * kGU;   // dense: output rows per unit
+
+// Gate/up + SwiGLU (kDense false) and the dense GEMM (kDense true) share one body.
+// MoE unit = 64 columns of h: wave w owns gate and up rows 64 u + 16 w .. + 15.  Dense unit
+// = 128 rows: wave w owns rows 128 u + 16 w + 64 m .. + 15 (m = 0, 1) in place of gate and up.
+// Per pass of <= 32 rows of x, supersteps of 4 groups: the x digit planes of the pass's rows
+// for the superstep sit in LDS (each thread stages its row's 12 x 16 bytes), the next
+// superstep's x digits and then its weight slots are loaded while this one computes, so the
+// in-order wait for those x digits never covers the weights.  Each (matrix, digit, 16-row
+// tile) is two MFMAs per group, folded in fp32 with the group's scale.  MoE: h = silu(gate) *
+// up (c/qwen.c:780-786, silu c/qwen.c:173) goes out as fp32 rows; dense: the two row tiles.
+template <bool kDense>
+__device__ __forceinline__ void gu_body(const PfArgs &a, const GemmArgs &g) {
     __shared__ __attribute__((aligned(16))) int8_t sB[4][3][kPR][kPitch];
     __shared__ int sE[4][kPR];
     __shared__ float sQ[4][kPR];
-    extern __shared__ float4 sS4[];   // [D / 128][2][kGU] float2: scales of the unit's rows
+    extern __shared__ float4 sS4[];   // [ngD][2][kGU] float2: scales of the unit's rows
     float2 *sS = (float2 *)sS4;
-    const int nh = a.I / kGU, ngD = a.D / kGS, nss = (ngD + 3) / 4;
-    int e, u, p0, p1, pos0, n;
-    ExpertRec rec;
-    if (!pf_unit(a, nh, e, u, p0, p1, pos0, n, rec)) return;
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // scales of rows kGU u .. + kGU - 1 of gate and up, regrouped by group in LDS: the first
-    // kSV entries per thread are loaded with the first pass's x row and weights
-    const float2 *sgp = (const float2 *)rec.sg + (size_t)u * kGU * ngD, *sup = (const float2 *)rec.su + (size_t)u * kGU * ngD;
+    int e = 0, u, p0, p1, pos0, n, ngD, xD, xS;
+    __amdgpu_buffer_rsrc_t wr[2], xr;
+    uint32_t abase, a1off, whalf;   // matrix 1's slots at abase + a1off
+    const float2 *sgp, *sup;
+    int nv[2];   // valid scale entries of the two matrices' unit rows
+    if constexpr (kDense) {
+        const int b = blockIdx.x, r = b >> 3;
+        u = 8 * (r / g.npass) + (b & 7);
+        if (u >= g.nu) return;
+        p0 = r % g.npass;
+        p1 = p0 + 1;
+        pos0 = 0;
+        n = g.S;
+        ngD = g.I / kGS;
+        xD = g.I;
+        xS = g.S;
+        const __amdgpu_buffer_rsrc_t w = buf_rsrc(g.w, (uint32_t)g.O * g.rb);
+        wr[0] = wr[1] = w;
+        const int row0 = u * kGR + wave * 16 + j;
+        abase = (uint32_t)(row0 * g.rb + q * 16);
+        a1off = (uint32_t)(kGU * g.rb);
+        whalf = (uint32_t)g.nl * 16;
+        sgp = (const float2 *)g.sz + (size_t)u * kGR * ngD;
+        sup = sgp + (size_t)kGU * ngD;
+        nv[0] = min(max(g.O - u * kGR, 0), kGU) * ngD;
+        nv[1] = min(max(g.O - u * kGR - kGU, 0), kGU) * ngD;
+        xr = buf_rsrc(g.xd, (uint32_t)(3u * g.S * g.I));
+    } else {
+        ExpertRec rec;
+        if (!pf_unit(a, a.I / kGU, e, u, p0, p1, pos0, n, rec)) return;
+        ngD = a.D / kGS;
+        xD = a.D;
+        xS = a.S;
+        wr[0] = buf_rsrc(rec.wg, (uint32_t)a.I * a.rbG);
+        wr[1] = buf_rsrc(rec.wu, (uint32_t)a.I * a.rbG);
+        abase = (uint32_t)((u * kGU + wave * 16 + j) * a.rbG + q * 16);
+        a1off = 0;
+        whalf = (uint32_t)a.nlG * 16;
+        sgp = (const float2 *)rec.sg + (size_t)u * kGU * ngD;
+        sup = (const float2 *)rec.su + (size_t)u * kGU * ngD;
+        nv[0] = nv[1] = kGU * ngD;
+        xr = buf_rsrc(a.xd, (uint32_t)(3u * a.S * a.D));
+    }
+    const int nss = (ngD + 3) / 4;
+    const int *xe = kDense ? g.xe : a.xe;
+    const float *xsum = kDense ? g.xsum : a.xsum;
+    // scales of the unit's rows of the two matrices, regrouped by group in LDS: the first kSV
+    // entries per thread are loaded with the first pass's x row and weights
     constexpr int kSV = 2;
     auto s_store = [&](int v, float2 gv, float2 uv) {
-        const int r = v / ngD, g = v - r * ngD;
-        sS[(2 * g) * kGU + r] = gv;
-        sS[(2 * g + 1) * kGU + r] = uv;
+        const int r = v / ngD, gi = v - r * ngD;
+        sS[(2 * gi) * kGU + r] = gv;
+        sS[(2 * gi + 1) * kGU + r] = uv;
     };
-    const __amdgpu_buffer_rsrc_t wr[2] = {buf_rsrc(rec.wg, (uint32_t)a.I * a.rbG), buf_rsrc(rec.wu, (uint32_t)a.I * a.rbG)};
-    const uint32_t abase = (uint32_t)((u * kGU + wave * 16 + j) * a.rbG + q * 16), whalf = (uint32_t)a.nlG * 16;
     auto w_load = [&](int S, uint4 (&d)[2][4]) {
-        const uint32_t o = S < nss ? abase + 128u * S : kOOB;
-        pf_wload(wr[0], o, whalf, d[0]);
-        pf_wload(wr[1], o, whalf, d[1]);
+        pf_wload(wr[0], S < nss ? abase + 128u * S : kOOB, whalf, d[0]);
+        pf_wload(wr[1], S < nss ? abase + a1off + 128u * S : kOOB, whalf, d[1]);
     };
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(a.xd, (uint32_t)(3u * a.S * a.D));
-    const uint32_t plane = (uint32_t)a.S * a.D;
+    const uint32_t plane = (uint32_t)xS * xD;
     // staging thread: row sr of the pass, 16 columns at sc of every group and plane; the
     // threads with tid % 8 < 4 also carry exponent and sum of group tid % 8
     const int sr = tid >> 3, sc = (tid & 7) * 16, sg4 = tid & 7;
@@ -386,7 +441,9 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
         // issue order: this thread's row of x (the dependent chain), the first weights,
         // the scales (first pass), then the x digits once the row is known
         const int xi = r0 + min(sr, nr - 1);
-        const int xpair = e == a.E ? xi : a.plist[pos0 + xi];
+        int xrow;
+        if constexpr (kDense) xrow = xi;
+        else xrow = e == a.E ? xi : a.plist[pos0 + xi] / a.K;
         uint4 W[2][4];
         w_load(0, W);
         float2 sv[kSV][2];
@@ -394,21 +451,20 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
 #pragma unroll
             for (int i = 0; i < kSV; i++) {
                 const int v = tid + kPT * i;
-                sv[i][0] = v < kGU * ngD ? sgp[v] : make_float2(0.f, 0.f);
-                sv[i][1] = v < kGU * ngD ? sup[v] : make_float2(0.f, 0.f);
+                sv[i][0] = v < nv[0] ? sgp[v] : make_float2(0.f, 0.f);
+                sv[i][1] = v < nv[1] ? sup[v] : make_float2(0.f, 0.f);
             }
-        const int xrow = e == a.E ? xpair : xpair / a.K;
         auto x_load = [&](int S, XStage &st) {
 #pragma unroll
             for (int gl = 0; gl < 4; gl++) {
-                const int g = 4 * S + gl;
-                const uint32_t o = g < ngD ? (uint32_t)xrow * a.D + g * kGS + sc : kOOB;
+                const int gi = 4 * S + gl;
+                const uint32_t o = gi < ngD ? (uint32_t)xrow * xD + gi * kGS + sc : kOOB;
 #pragma unroll
                 for (int d = 0; d < 3; d++) st.v[gl][d] = buf_load16<kCached>(xr, o + d * plane);
             }
             const int gc = min(4 * S + (sg4 & 3), ngD - 1);
-            st.e = a.xe[(size_t)xrow * ngD + gc];
-            st.s = a.xsum[(size_t)xrow * ngD + gc];
+            st.e = xe[(size_t)xrow * ngD + gc];
+            st.s = xsum[(size_t)xrow * ngD + gc];
         };
         auto x_store = [&](const XStage &st) {
 #pragma unroll
@@ -424,7 +480,8 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
 #pragma unroll
             for (int i = 0; i < kSV; i++)
                 if (tid + kPT * i < kGU * ngD) s_store(tid + kPT * i, sv[i][0], sv[i][1]);
-            for (int v = tid + kPT * kSV; v < kGU * ngD; v += kPT) s_store(v, sgp[v], sup[v]);   // D > 2048
+            for (int v = tid + kPT * kSV; v < kGU * ngD; v += kPT)   // I > 2048
+                s_store(v, v < nv[0] ? sgp[v] : make_float2(0.f, 0.f), v < nv[1] ? sup[v] : make_float2(0.f, 0.f));
         }
         XStage xst;
         x_load(0, xst);
@@ -453,8 +510,8 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
                 pf_wgroups(C[1]);
 #pragma unroll
                 for (int gl = 0; gl < 4; gl++) {
-                    const int g = 4 * S + gl;
-                    if (g >= ngD) continue;   // uniform
+                    const int gi = 4 * S + gl;
+                    if (gi >= ngD) continue;   // uniform
                     pf_v4i av[2][2];   // [matrix][half]
 #pragma unroll
                     for (int m = 0; m < 2; m++) {
@@ -478,7 +535,7 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
                     float2 sz[2][4];
 #pragma unroll
                     for (int m = 0; m < 2; m++) {
-                        const float4 *sz4 = (const float4 *)&sS[(2 * g + m) * kGU + wave * 16 + 4 * q];
+                        const float4 *sz4 = (const float4 *)&sS[(2 * gi + m) * kGU + wave * 16 + 4 * q];
                         const float4 za = sz4[0], zb = sz4[1];
                         sz[m][0] = make_float2(za.x, za.y);
                         sz[m][1] = make_float2(za.z, za.w);
@@ -488,10 +545,10 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
 #pragma unroll
                     for (int tt = 0; tt < 2; tt++)
                         if (tt < NT) {
-                            const int xe = sE[gl][tt * 16 + j];
+                            const int xe_ = sE[gl][tt * 16 + j];
                             const float xs = sQ[gl][tt * 16 + j];
 #pragma unroll
-                            for (int m = 0; m < 2; m++) pf_fold(iacc[m][tt], sz[m], xe, xs, facc[m][tt]);
+                            for (int m = 0; m < 2; m++) pf_fold(iacc[m][tt], sz[m], xe_, xs, facc[m][tt]);
                         }
                 }
                 if (S + 1 < nss) {   // uniform
@@ -500,11 +557,25 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
                     __syncthreads();
                 }
             }
-            // lane holds h columns kGU u + 16 w + 4 q .. + 3 of x row tt * 16 + j
 #pragma unroll
             for (int tt = 0; tt < 2; tt++) {
                 const int x = tt * 16 + j;
-                if (tt < NT && x < nr) {
+                if (tt >= NT || x >= nr) continue;
+                if constexpr (kDense) {
+                    // rows 128 u + 64 m + 16 w + 4 q .. + 3 of x row r0 + x
+#pragma unroll
+                    for (int m = 0; m < 2; m++) {
+                        const int row = u * kGR + m * kGU + wave * 16 + 4 * q;
+                        float *yr = g.y + (size_t)(r0 + x) * g.O + row;
+                        if (row + 3 < g.O && (g.O & 3) == 0)
+                            *(float4 *)yr = make_float4(facc[m][tt][0], facc[m][tt][1], facc[m][tt][2], facc[m][tt][3]);
+                        else
+#pragma unroll
+                            for (int r = 0; r < 4; r++)
+                                if (row + r < g.O) yr[r] = facc[m][tt][r];
+                    }
+                } else {
+                    // h columns kGU u + 16 w + 4 q .. + 3 of x row tt * 16 + j
                     float hv[4];
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
@@ -522,11 +593,20 @@ __global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) {
     }
 }
 
+__global__ __launch_bounds__(kPT, 2) void pf_gateup(PfArgs a) { gu_body<false>(a, GemmArgs{}); }
+__global__ __launch_bounds__(kPT, 2) void gemm6_mfma(GemmArgs g) { gu_body<true>(PfArgs{}, g); }
+
 // Rows of n values (n % 128 == 0) -> digit planes [3][rows][n], ge / gsum [rows][n / 128]:
-// one thread per 8 columns.
-__global__ __launch_bounds__(256) void pf_digits(const float *__restrict__ src, int rows, int n,
-                                                 int8_t *__restrict__ planes, int *__restrict__ ge,
-                                                 float *__restrict__ gsum) {
+// one thread per 8 columns.  kGated: the row is first put through the GatedDeltaNet output
+// norm, per head of VD columns y * r_h * gnorm[d] * silu(z) with r_h = 1 / sqrt(mean(y^2)
+// + eps), the sum of squares in double (c/qwen.c:768-772); gnorm has a row stride (the
+// host packs it into each token's parameter row).  VD / 8 consecutive lanes hold one head
+// (VD a power of two, 8 <= VD <= 512), so the head sum is a butterfly over them.
+template <bool kGated>
+__global__ __launch_bounds__(256) void pf_digits_t(const float *__restrict__ src, int rows, int n,
+                                                   int8_t *__restrict__ planes, int *__restrict__ ge,
+                                                   float *__restrict__ gsum, const float *__restrict__ z,
+                                                   const float *__restrict__ gnorm, int gstride, int VD, float eps) {
     const int per = n / 8, i = blockIdx.x * 256 + threadIdx.x, row = i / per, c8 = i - row * per;
     const bool valid = row < rows;
     float v[8];
@@ -537,6 +617,22 @@ __global__ __launch_bounds__(256) void pf_digits(const float *__restrict__ src, 
     } else {
 #pragma unroll
         for (int c = 0; c < 8; c++) v[c] = 0.f;
+    }
+    if constexpr (kGated) {
+        double ss = 0;
+#pragma unroll
+        for (int c = 0; c < 8; c++) ss += (double)v[c] * v[c];
+        for (int o = 1; o < VD / 8; o <<= 1) ss += __shfl_xor(ss, o);
+        const float r = 1.f / sqrtf((float)(ss / VD) + eps);
+        if (valid) {
+            const float *zr = z + (size_t)row * n + 8 * c8;
+            const float *gw = gnorm + (size_t)row * gstride + (8 * c8) % VD;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {   // silu(z) with a hardware reciprocal (< 2 ulp)
+                const float zv = zr[c], sz = zv * __builtin_amdgcn_rcpf(1.f + expf(-zv));
+                v[c] = v[c] * r * gw[c] * sz;
+            }
+        }
     }
     const int ng = n / kGS, gi = (8 * c8) / kGS;
     const size_t r = valid ? row : 0;
@@ -814,8 +910,8 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     auto blocks = [&](int nu) { return ((nu * a.nsp + 7) & ~7) + nu * E8; };
     const int nh = I / kGU, nq = (D + kDR - 1) / kDR;
     hipLaunchKernelGGL(pf_gateup, dim3(blocks(nh)), dim3(kPT), (size_t)ngD * 2 * kGU * sizeof(float2), st, a);
-    hipLaunchKernelGGL(pf_digits, dim3((P * (I / 8) + 255) / 256), dim3(256), 0, st, a.h, P, I, (int8_t *)(b + o_hd),
-                       (int *)(b + o_he), (float *)(b + o_hs));
+    hipLaunchKernelGGL(pf_digits_t<false>, dim3((P * (I / 8) + 255) / 256), dim3(256), 0, st, a.h, P, I,
+                       (int8_t *)(b + o_hd), (int *)(b + o_he), (float *)(b + o_hs), nullptr, nullptr, 0, 0, 0.f);
     hipLaunchKernelGGL(pf_down, dim3(blocks(nq)), dim3(kPT), 0, st, a);
     hipLaunchKernelGGL(pf_combine, dim3(S), dim3(256), 0, st, a.y, ti, tv, tsh, pp, S, K, D, d_out);
     const hipError_t err = hipGetLastError();
@@ -823,7 +919,61 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     return true;
 }
 
-void prefill_shutdown() { scratch_free(&g_pf.buf, &g_pf.cap); }
+// ---------------------------------------------------------------- dense GEMM (host)
+static PfScratch g_gm;
+
+bool gemm6_ok(const ColiVkTensor *t) {
+    return tensor_live(t) && t->fmt == 6 && t->layout == kLayoutLanes && t->gs == kGS && t->I % kGS == 0 &&
+           t->I <= kGemmMaxI && t->O >= 1 && (size_t)(t->O + kGR) * t->row_bytes < (1ull << 32);
+}
+
+bool gemm6(const ColiVkTensor *const *t, float *const *d_y, int nt, const float *d_x, int S, hipStream_t st,
+           const GatedX *gx) {
+    if (nt < 1 || !d_x || S < 1) return false;
+    const int I = t[0]->I, ng = I / kGS;
+    for (int i = 0; i < nt; i++)
+        if (!gemm6_ok(t[i]) || t[i]->I != I || !d_y[i]) return false;
+    if ((size_t)3 * S * I >= (1u << 31)) return false;
+    if (gx && (!gx->z || !gx->gnorm || gx->VD < 8 || gx->VD > 512 || (gx->VD & (gx->VD - 1)) || I % gx->VD))
+        return false;
+    const size_t o_xe = al256((size_t)3 * S * I), o_xs = o_xe + al256((size_t)S * ng * 4),
+                 total = o_xs + al256((size_t)S * ng * 4);
+    if (!scratch(&g_gm.buf, &g_gm.cap, total)) return false;
+    uint8_t *b = (uint8_t *)g_gm.buf;
+    const dim3 dg((unsigned)(((size_t)S * (I / 8) + 255) / 256));
+    if (gx)
+        hipLaunchKernelGGL(pf_digits_t<true>, dg, dim3(256), 0, st, d_x, S, I, (int8_t *)b, (int *)(b + o_xe),
+                           (float *)(b + o_xs), gx->z, gx->gnorm, gx->gstride, gx->VD, gx->eps);
+    else
+        hipLaunchKernelGGL(pf_digits_t<false>, dg, dim3(256), 0, st, d_x, S, I, (int8_t *)b, (int *)(b + o_xe),
+                           (float *)(b + o_xs), nullptr, nullptr, 0, 0, 0.f);
+    for (int i = 0; i < nt; i++) {
+        GemmArgs g;
+        g.w = t[i]->w;
+        g.sz = t[i]->sz;
+        g.O = t[i]->O;
+        g.I = I;
+        g.rb = t[i]->row_bytes;
+        g.nl = t[i]->nl;
+        g.xd = (const int8_t *)b;
+        g.xe = (const int *)(b + o_xe);
+        g.xsum = (const float *)(b + o_xs);
+        g.S = S;
+        g.nu = (g.O + kGR - 1) / kGR;
+        g.npass = (S + kPR - 1) / kPR;
+        g.y = d_y[i];
+        const int blocks = 8 * ((g.nu + 7) / 8) * g.npass;
+        hipLaunchKernelGGL(gemm6_mfma, dim3(blocks), dim3(kPT), (size_t)ng * 2 * kGU * sizeof(float2), st, g);
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail("dense gemm launch", err);
+    return true;
+}
+
+void prefill_shutdown() {
+    scratch_free(&g_pf.buf, &g_pf.cap);
+    scratch_free(&g_gm.buf, &g_gm.cap);
+}
 
 }  // namespace coli
 

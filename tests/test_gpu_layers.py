@@ -83,17 +83,7 @@ def test_gqa_long_cache(lib, lorc, gen):
 
 
 # ---------------------------------------------------------------- GDN block
-def host_params(orc, W, x):
-    """[decay(VH) | beta(VH) | gnorm(VD)] as the engine packs them (c/qwen.c:679-688)."""
-    a = np.empty(W.VH, np.float32)
-    b = np.empty(W.VH, np.float32)
-    orc.orc_proj(_layers.C.byref(W.a.orc()), P(x), P(a))
-    orc.orc_proj(_layers.C.byref(W.b.orc()), P(x), P(b))
-    sp_in = (a + W.dtb).astype(np.float32)
-    sp = np.where(sp_in > 20, sp_in, np.log1p(np.exp(sp_in.astype(np.float64)))).astype(np.float32)
-    decay = np.exp(-np.exp(W.alog.astype(np.float64)) * sp).astype(np.float32)
-    beta = (1.0 / (1.0 + np.exp(-b.astype(np.float64)))).astype(np.float32)
-    return np.concatenate([decay, beta, W.gnorm]).astype(np.float32)
+host_params = _layers.gdn_host_params
 
 
 @pytest.mark.parametrize("shape", ["small", "cfg3"])
