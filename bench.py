@@ -363,6 +363,48 @@ def gdn_prefill_cfg3(lib, calls=5):
             "tokens_per_s": round(S / sec, 1), "calls": calls}
 
 
+def container_load(lib, mod):
+    """The fmt=6 container reader (coli_hip_st_experts): one configs[2] layer's 256 routed
+    experts (gate/up 512 x 2048, down 2048 x 512, gs 128; 453 MB of U8 nibbles + F32 .qs)
+    written in the converter's layout to a temporary directory, then read into the resident
+    expert table.  The files were just written, so the reads come from the page cache: the
+    figure is host memory -> HBM through the reader (pread threads, pinned staging, device
+    relayout), not disk bandwidth."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from safetensors.numpy import save_file
+    D, I, E, gs = K_HID, 512, 256, GS
+    rng = np.random.default_rng(0xF60)
+    tmp = tempfile.mkdtemp(prefix="coli_st_")
+    try:
+        nbytes = 0
+        names = ("gate_proj", "up_proj", "down_proj")
+        for shard in range(4):
+            t = {}
+            for e in range(shard * E // 4, (shard + 1) * E // 4):
+                for j, nm in enumerate(names):
+                    I_, O_ = (D, I) if j < 2 else (I, D)
+                    w = np.frombuffer(rng.bytes(O_ * I_ // 2), np.uint8).reshape(O_, I_ // 2)
+                    qs = np.abs(rng.normal(0, 0.02, (O_, 2 * (I_ // gs)))).astype(np.float32)
+                    t[f"model.layers.0.mlp.experts.{e}.{nm}.weight"] = w
+                    t[f"model.layers.0.mlp.experts.{e}.{nm}.weight.qs"] = qs
+                    nbytes += w.nbytes + qs.nbytes
+            save_file(t, os.path.join(tmp, f"out-layer-00-{shard}.safetensors"))
+        st = mod.Container(lib, tmp)
+        lib.eg_table_init(1, E, D, I, gs)
+        t0 = time.perf_counter()
+        st.experts(0, E, D, I, gs)
+        sec = time.perf_counter() - t0
+        st.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {"workload": "cfg2 layer: 256 routed experts from a 4-shard fmt6 container (page cache) "
+                        "into the resident expert table", "bytes": nbytes, "ms": round(sec * 1e3, 1),
+            "GBs": round(nbytes / sec / 1e9, 2), "reader_threads": int(os.environ.get("COLI_HIP_READ_THREADS", 0))
+            or min(os.cpu_count() or 1, 16)}
+
+
 class DecodeStack:
     """the 40-layer hybrid decode model with random-init weights generated on the
     device.  Layer i is gated GQA when (i + 1) % 4 == 0 (c/qwen.c:398), GatedDeltaNet
@@ -581,6 +623,7 @@ def main():
     out["gdn_prefill_cfg3"] = gdn_prefill_cfg3(lib)
     if not args.no_decode:
         out["decode_cfg3"] = decode_cfg3(lib, torch, dev, max(args.steps // 10, 5), 3)
+    out["container_load"] = container_load(lib, mod)
     if not args.no_cpu:
         cb = cpu_baselines()
         out["cpu_baseline"] = cpu_baseline(cb)

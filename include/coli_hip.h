@@ -275,6 +275,42 @@ int   coli_hip_kv_read(int layer, int row0, int n, float *K, float *V);
  * (slot conv_k - 1 newest) and recurrent state [VH][KD][VD] (c/qwen.c:749-767). */
 int   coli_hip_gdn_state_read(int layer, float *ring, float *S);
 
+/* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
+ * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32
+ * ".qs" tensor of [scale, zero] pairs per group) read straight into device tensors.
+ * coli_hip_st_open indexes every *.safetensors file of dir in name order and checks each
+ * header as c/st.h:241-331 does (length within the file and under 512 MiB, a JSON object,
+ * dtype / data_offsets / shape present and well-typed, offsets inside the file, no shape
+ * overflow, element count equal to the byte span for F32/BF16/F16); a bad shard makes it
+ * return NULL with a message, where the reference exits.  Host-only: open, count, find
+ * and the two reads need no device. */
+typedef struct ColiHipSt ColiHipSt;
+ColiHipSt *coli_hip_st_open(const char *dir);
+void  coli_hip_st_close(ColiHipSt *st);
+int   coli_hip_st_count(const ColiHipSt *st);
+/* dtype 0 BF16, 1 F16, 2 F32, 3 U8/I8; shape holds up to 8 sizes.  0 when absent. */
+int   coli_hip_st_find(const ColiHipSt *st, const char *name, int *dtype, int64_t *numel, int64_t *nbytes,
+                       int *ndim, int64_t *shape);
+/* c/st.h:399-442: a float tensor as f32, at most cap elements; the count or -1. */
+int64_t coli_hip_st_read_f32(const ColiHipSt *st, const char *name, float *out, int64_t cap);
+/* c/st.h:445-452: raw bytes, at most cap; the count or -1. */
+int64_t coli_hip_st_read_raw(const ColiHipSt *st, const char *name, void *out, int64_t cap);
+/* In place of reading a tensor to host memory and calling coli_vk_tensor_ensure
+ * (c/qwen.c:509-536, 1786-1789): fmt 6 reads name (U8 [O, ceil(I/2)]) and name.qs (F32
+ * [O, 2 ceil(I/gs)]), fmt 0 an F32/BF16/F16 [O, I] tensor as f32 rows; *tensor must be
+ * NULL.  1 on success. */
+int   coli_hip_st_tensor(const ColiHipSt *st, const char *name, ColiVkTensor **tensor, int fmt, int I, int O,
+                         int gs);
+/* The E routed experts of model layer `layer` (converter names
+ * model.layers.L.mlp.experts.E.{gate,up,down}_proj.weight[.qs], gate/up [I, D], down
+ * [D, I]) into slots (layer, 0..E-1) of the resident expert table, which
+ * coli_vk_eg_table_init must have sized; replaces c/qwen.c:1743-1805's per-expert
+ * expert_read + three coli_vk_tensor_ensure calls.  Every tensor is checked before any
+ * upload; batches are read by several threads (COLI_HIP_READ_THREADS, default the
+ * hardware threads, at most 16) into pinned buffers while the device converts the previous
+ * batch.  1 when every expert is resident. */
+int   coli_hip_st_experts(const ColiHipSt *st, int layer, int E, int D, int I, int gs);
+
 #ifdef __cplusplus
 }
 #endif

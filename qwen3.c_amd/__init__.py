@@ -71,6 +71,14 @@ _SIGS = {
     "coli_vk_gdn_conv_weight": (_I, [_I, _P, _I, _I]),
     "coli_vk_gdn_ba_weight": (_I, [_I, _P, _P, _P, _I, _I]),
     "coli_hip_gdn_state_read": (_I, [_I, _P, _P]),
+    "coli_hip_st_open": (_P, [C.c_char_p]),
+    "coli_hip_st_close": (None, [_P]),
+    "coli_hip_st_count": (_I, [_P]),
+    "coli_hip_st_find": (_I, [_P, C.c_char_p, _P, _P, _P, _P, _P]),
+    "coli_hip_st_read_f32": (C.c_int64, [_P, C.c_char_p, _P, C.c_int64]),
+    "coli_hip_st_read_raw": (C.c_int64, [_P, C.c_char_p, _P, C.c_int64]),
+    "coli_hip_st_tensor": (_I, [_P, C.c_char_p, _P, _I, _I, _I, _I]),
+    "coli_hip_st_experts": (_I, [_P, _I, _I, _I, _I, _I]),
     "coli_vk_gdn_full": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
     "coli_vk_gdn_full_seq": (_I, [_I, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
     "coli_vk_layer_norm_weight": (_I, [_I, _P, _P, _I]),
@@ -124,6 +132,61 @@ class Tensor:
 
     def nbytes(self):
         return int(self.lib.L.coli_vk_tensor_bytes(self.handle))
+
+
+class Container:
+    """A ColiHipSt* (fmt=6 safetensors container index).  Opening needs no device."""
+
+    DTYPES = {0: "BF16", 1: "F16", 2: "F32", 3: "U8"}
+
+    def __init__(self, lib, path):
+        self.lib = lib
+        self.h = lib.L.coli_hip_st_open(os.fsencode(path))
+        if not self.h:
+            raise ValueError(f"coli_hip_st_open({path}) refused the container")
+
+    def close(self):
+        if self.h:
+            self.lib.L.coli_hip_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self):
+        return int(self.lib.L.coli_hip_st_count(self.h))
+
+    def find(self, name):
+        """(dtype name, numel, nbytes, shape) or None."""
+        dt, ne, nb, nd = C.c_int(), C.c_int64(), C.c_int64(), C.c_int()
+        shape = (C.c_int64 * 8)()
+        if not self.lib.L.coli_hip_st_find(self.h, name.encode(), C.byref(dt), C.byref(ne), C.byref(nb),
+                                           C.byref(nd), shape):
+            return None
+        return self.DTYPES[dt.value], ne.value, nb.value, tuple(shape[i] for i in range(nd.value))
+
+    def read_f32(self, name, cap):
+        out = np.empty(max(cap, 1), np.float32)
+        n = self.lib.L.coli_hip_st_read_f32(self.h, name.encode(), _ptr(out), cap)
+        return None if n < 0 else out[:n]
+
+    def read_raw(self, name, cap):
+        out = np.empty(max(cap, 1), np.uint8)
+        n = self.lib.L.coli_hip_st_read_raw(self.h, name.encode(), _ptr(out), cap)
+        return None if n < 0 else out[:n]
+
+    def tensor(self, name, fmt, I, O, gs=0):
+        t = Tensor(self.lib, fmt, I, O, gs)
+        if not self.lib.L.coli_hip_st_tensor(self.h, name.encode(), t.ref, fmt, I, O, gs):
+            raise RuntimeError(f"coli_hip_st_tensor({name}) failed")
+        return t
+
+    def experts(self, layer, E, D, I, gs):
+        if not self.lib.L.coli_hip_st_experts(self.h, layer, E, D, I, gs):
+            raise RuntimeError(f"coli_hip_st_experts(layer {layer}) failed")
 
 
 class Lib:

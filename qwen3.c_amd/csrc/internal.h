@@ -117,6 +117,7 @@ void gemv_shutdown();
 void moe_shutdown();
 void prefill_shutdown();
 void layer_shutdown();
+void container_shutdown();
 void scratch_free(void **p, size_t *cap);
 void host_scratch_free(void **p, size_t *cap);
 

@@ -308,6 +308,7 @@ COLI_API void coli_vk_shutdown(void) {
     moe_shutdown();
     prefill_shutdown();
     layer_shutdown();
+    container_shutdown();
     scratch_free(&g_stage, &g_stage_cap);
     for (int i = 0; i < G.nblocks; i++) (void)hipFree(G.blocks[i].base);
     G.nblocks = 0;
