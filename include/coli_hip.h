@@ -274,6 +274,12 @@ int   coli_hip_kv_read(int layer, int row0, int n, float *K, float *V);
 /* A GDN layer's state in the reference's host layouts: conv ring [conv_k][conv_dim]
  * (slot conv_k - 1 newest) and recurrent state [VH][KD][VD] (c/qwen.c:749-767). */
 int   coli_hip_gdn_state_read(int layer, float *ring, float *S);
+/* Fused layer launches (one kernel for a decode token's GatedDeltaNet in-projection,
+ * recurrence and out-projection, where the shapes allow) on (1) or off (0: the separate
+ * kernels); returns the previous setting.  Both give the same results bit for bit.  No
+ * counterpart in the reference (its layer is separate dispatches).  Off by default (slower on
+ * MI355X at configs[3]); the environment variable COLI_HIP_FUSE=1 starts with it on. */
+int   coli_hip_layer_fuse(int on);
 
 /* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
  * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32

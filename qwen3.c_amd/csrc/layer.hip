@@ -72,7 +72,8 @@ struct ProjSeg {
     const float *sz;
     float *y;
     int O;
-    int g0;   // first row group of the segment in the launch's row-group space
+    int g0;                  // first row group of the segment in the launch's row-group space
+    unsigned long long *yt;  // fused layer kernel: the outputs as tagged words (epoch << 32 | bits)
 };
 
 struct ProjArgs {
@@ -85,6 +86,12 @@ struct ProjArgs {
     int VD;
     float eps;
     int add;           // 1: y[r] += acc (residual add), 0: y[r] = acc
+    // fused layer kernel: x (and z) as tagged words, polled until they carry `epoch`
+    const unsigned long long *xt, *zt;
+    unsigned long long *err;
+    uint32_t epoch;
+    const unsigned long long *done;   // > 0 words: the producers of x mark their end (see proj_body)
+    int ndone;
 };
 
 // Sum over aligned groups of n lanes (n a power of two <= 64, wave uniform), in every lane
@@ -151,22 +158,76 @@ struct SegSel {
     const float *sz;
     float *y;
     int O, g0;
+    unsigned long long *yt;
 };
 __device__ __forceinline__ SegSel seg_of(const ProjArgs &a, int g) {
-    SegSel s = {a.seg[0].w, a.seg[0].sz, a.seg[0].y, a.seg[0].O, a.seg[0].g0};
+    SegSel s = {a.seg[0].w, a.seg[0].sz, a.seg[0].y, a.seg[0].O, a.seg[0].g0, a.seg[0].yt};
 #pragma unroll
     for (int t = 1; t < kMaxSeg; t++)
-        if (t < a.nseg && g >= a.seg[t].g0) s = {a.seg[t].w, a.seg[t].sz, a.seg[t].y, a.seg[t].O, a.seg[t].g0};
+        if (t < a.nseg && g >= a.seg[t].g0)
+            s = {a.seg[t].w, a.seg[t].sz, a.seg[t].y, a.seg[t].O, a.seg[t].g0, a.seg[t].yt};
     return s;
+}
+
+// Two tagged rows (y and z of the gated norm) polled together.
+__device__ __forceinline__ bool prep_load_tagged2(const unsigned long long *xt, const unsigned long long *zt, int I,
+                                                  int ncols, XRegs &xr, XRegs &zr, uint32_t ep,
+                                                  unsigned long long *err) {
+    const int tid = threadIdx.x, nwords = ncols / 8;
+    for (int polls = 0;; polls++) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++) {
+            const int w = tid + k * kThreads;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i = w * 8 + c;
+                const bool on = w < nwords && i < I;
+                const unsigned long long v = on ? aload(xt + i) : 0ull, u = on ? aload(zt + i) : 0ull;
+                all &= !on || ((uint32_t)(v >> 32) == ep && (uint32_t)(u >> 32) == ep);
+                xr.v[k][c] = __uint_as_float((uint32_t)v);
+                zr.v[k][c] = __uint_as_float((uint32_t)u);
+            }
+        }
+        if (all) return true;
+        if (poll_give_up(err, ep, polls)) return false;
+    }
+}
+
+// prep_load from tagged words: every column's word is polled until it carries the epoch
+// (bounded; false when the launch has failed).  Columns at or past I are zero.
+__device__ __forceinline__ bool prep_load_tagged(const unsigned long long *xt, int I, int ncols, XRegs &xr, uint32_t ep,
+                                                 unsigned long long *err) {
+    const int tid = threadIdx.x, nwords = ncols / 8;
+    for (int polls = 0;; polls++) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < XRegs::kWords; k++) {
+            const int w = tid + k * kThreads;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i = w * 8 + c;
+                const bool on = w < nwords && i < I;
+                const unsigned long long v = on ? aload(xt + i) : 0ull;
+                all &= !on || (uint32_t)(v >> 32) == ep;
+                xr.v[k][c] = __uint_as_float((uint32_t)v);
+            }
+        }
+        if (all) return true;
+        if (poll_give_up(err, ep, polls)) return false;
+    }
 }
 
 // Row groups (RPW rows of one wave step) of all segments form one space; a segment
 // starts on a group boundary, so a wave step never mixes tensors.  U row steps per wave
 // are loaded before any is reduced (the loads of the next step go out while the current
 // one computes), as in the single-tensor GEMV.
-template <int LPR, int CU, int U, int XF>
-__global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
-    __shared__ XPrep P;
+// kTagIn (fused layer kernel, XF_GATED): x and z come as tagged words from earlier tiles;
+// the weights of the block's first row steps are then loaded before the wait.  kTagOut: the
+// outputs go out as tagged words.  bid / nb: this block's index among the nb blocks of the
+// projection.
+template <int LPR, int CU, int U, int XF, bool kTagIn, bool kTagOut>
+__device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XPrep &P) {
     constexpr int RPW = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -174,12 +235,14 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
     const int ncols = a.nl * kLaneChunks * 32;
     const uint32_t srb = (uint32_t)a.ng * 8u;
     XRegs xr, ar, br;
-    prep_load(a.x, a.I, ncols, xr);
-    if constexpr (XF != XF_PLAIN) xf_load<XF>(ar, br, a, ncols);
+    if constexpr (!kTagIn) {
+        prep_load(a.x, a.I, ncols, xr);
+        if constexpr (XF != XF_PLAIN) xf_load<XF>(ar, br, a, ncols);
+    }
     LaneX<CU> L;
     lane_geo<CU>(j, a.nl, a.I, a.gs, L);
-    const int nw = gridDim.x * kWaves;
-    const int gbase = blockIdx.x * kWaves + wave;
+    const int nw = nb * kWaves;
+    const int gbase = bid * kWaves + wave;
     uint4 wq[U][kLaneChunks];
     float2 sv[U][LaneX<CU>::NU];
     auto load = [&](int u, int g) {   // unconditional: out-of-range offsets past the last group
@@ -192,6 +255,38 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load(u, gbase + u * nw);
+    if constexpr (kTagIn) {   // the weights are in flight; now the inputs
+        // first the producers' done words, so that the block's many loads of x go out
+        // once, when x is complete
+        if (a.ndone > 0) {   // wave 0 waits for the producers' done words, then one pass of loads
+            if (threadIdx.x < 64) {
+                constexpr int kDone = 8;   // a.ndone <= 64 kDone
+                for (int polls = 0;; polls++) {
+                    bool all = true;
+#pragma unroll
+                    for (int k = 0; k < kDone; k++) {
+                        const int i = threadIdx.x + 64 * k;
+                        const unsigned long long v = i < a.ndone ? aload(a.done + i) : 0ull;
+                        all &= i >= a.ndone || (uint32_t)(v >> 32) == a.epoch;
+                    }
+                    if (__ballot(!all) == 0ull || poll_give_up(a.err, a.epoch, polls)) break;
+                }
+            }
+            __syncthreads();
+        }
+        if constexpr (XF == XF_GATED) {   // y and z in one pass of loads
+            prep_load_tagged2(a.xt, a.zt, a.I, ncols, xr, ar, a.epoch, a.err);
+            const int tid = threadIdx.x, nwords = ncols / 8;
+            const __amdgpu_buffer_rsrc_t r = buf_rsrc(a.xw, (uint32_t)a.VD * 4);
+#pragma unroll
+            for (int k = 0; k < XRegs::kWords; k++) {   // gnorm of the column's head position
+                const int w = tid + k * kThreads;
+                load8f(r, (w < nwords && w * 8 < a.I) ? ((w * 8) % a.VD) * 4 : (int)kOOB, br.v[k]);
+            }
+        } else {
+            prep_load_tagged(a.xt, a.I, ncols, xr, a.epoch, a.err);
+        }
+    }
     if constexpr (XF != XF_PLAIN) xf_apply<XF>(xr, ar, br, a, ncols);
     prep_x(xr, a.gs, ncols, P);
     lane_x<CU>(P, a.gs, L);
@@ -206,13 +301,23 @@ __global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
             const SegSel s = seg_of(a, g);
             const int r = (g - s.g0) * RPW + sg;
             if (j == LPR - 1 && r < s.O) {
-                if (a.add)
-                    s.y[r] += acc;
-                else
-                    s.y[r] = acc;
+                if constexpr (kTagOut) {
+                    tag_put(&s.yt[r], a.epoch, acc);
+                } else {
+                    if (a.add)
+                        s.y[r] += acc;
+                    else
+                        s.y[r] = acc;
+                }
             }
         }
     }
+}
+
+template <int LPR, int CU, int U, int XF>
+__global__ __launch_bounds__(kThreads) void proj_gemv(ProjArgs a) {
+    __shared__ XPrep P;
+    proj_body<LPR, CU, U, XF, false, false>(a, blockIdx.x, gridDim.x, P);
 }
 
 // ---------------------------------------------------------------- GatedDeltaNet core
@@ -260,16 +365,23 @@ struct GdnArgs {
     const float *alog, *dtb;
     float eps;
     int D, KH, KD, VH, VD, K, CD;
+    // fused layer kernel: qkv and the a/b dots as tagged words from the projection tiles,
+    // y out as tagged words
+    const unsigned long long *qkvt, *abt;
+    unsigned long long *yt, *done, *err;   // done[block]: the block's y words are out
+    uint32_t epoch;
 };
 
-template <int KPL>   // state elements per lane of a column (KD = 64 KPL)
-__global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
+// kTag (fused layer kernel): the inputs are polled from tagged words and y is published as
+// tagged words (the a/b path only; conv taps K <= kGdnMaxK).  bid: the block's index.
+template <int KPL, bool kTag>   // state elements per lane of a column (KD = 64 KPL)
+__device__ __forceinline__ void gdn_core_body(const GdnArgs &g, int bid) {
     __shared__ double s_red[kWaves];
     __shared__ float s_q[kGdnMaxKD], s_k[kGdnMaxKD], s_v[kGdnCols];
     __shared__ float s_ab[2][kWaves], s_nrm[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nsl = g.VD / kGdnCols;
-    const int h = blockIdx.x / nsl, c0 = (blockIdx.x % nsl) * kGdnCols;
+    const int h = bid / nsl, c0 = (bid % nsl) * kGdnCols;
     const int src = h / (g.VH / g.KH), KD = g.KD, key_dim = g.KH * KD;
 
     // the block's state columns: loads go out first
@@ -283,7 +395,9 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
 
     // decay / beta (c/qwen.c:722-728): host params, or a/b over in_ln(resid) here
     float decay, beta;
-    if (g.params) {
+    if (kTag) {   // from the a/b dots, polled with the conv inputs below
+        decay = beta = 0.f;
+    } else if (g.params) {
         decay = g.params[h];
         beta = g.params[g.VH + h];
     } else if (g.ab) {   // fmt 6 a/b: projected with qkv/z in one launch
@@ -348,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
             const int t = tid + i * kThreads;
             const bool on = t < nch;
             const int ch = on ? channel(t) : 0;
-            xin[i] = ld(rx, on, ch);
+            if (!kTag) xin[i] = ld(rx, on, ch);
             wlast[i] = ld(rw, on, ch * K + K - 1);
 #pragma unroll
             for (int q = 0; q + 1 < kGdnMaxK; q++) {
@@ -357,6 +471,28 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
                 cw[i][q] = ld(rw, on && q + 1 < K, ch * K + q);
                 rg[i][q] = ld(rr, on && q + 1 < K, slot * g.CD + ch);
             }
+        }
+        if (kTag) {   // this token's conv inputs and the a/b dots from the projection tiles
+            float av = 0.f, bv = 0.f;
+            for (int polls = 0;; polls++) {
+                const unsigned long long wa = aload(g.abt + h), wb = aload(g.abt + g.VH + h);
+                bool all = (uint32_t)(wa >> 32) == g.epoch && (uint32_t)(wb >> 32) == g.epoch;
+                av = __uint_as_float((uint32_t)wa);
+                bv = __uint_as_float((uint32_t)wb);
+#pragma unroll
+                for (int i = 0; i < kCh; i++) {
+                    const int t = tid + i * kThreads;
+                    const bool on = t < nch;
+                    const unsigned long long v = on ? aload(g.qkvt + channel(t)) : 0ull;
+                    all &= !on || (uint32_t)(v >> 32) == g.epoch;
+                    xin[i] = __uint_as_float((uint32_t)v);
+                }
+                if (all || poll_give_up(g.err, g.epoch, polls)) break;
+            }
+            const float sp_in = av + g.dtb[h];
+            const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
+            decay = expf(-expf(g.alog[h]) * sp);
+            beta = 1.f / (1.f + expf(-bv));
         }
 #pragma unroll
         for (int i = 0; i < kCh; i++) {
@@ -439,8 +575,20 @@ __global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
         float *col = g.S + ((size_t)h * g.VD + vd) * KD + lane * KPL;
 #pragma unroll
         for (int e = 0; e < KPL; e++) col[e] = sv[q][e];
-        if (lane == 0) g.y[(size_t)h * g.VD + vd] = yv;
+        if (lane == 0) {
+            if (kTag) tag_put(g.yt + (size_t)h * g.VD + vd, g.epoch, yv);
+            else g.y[(size_t)h * g.VD + vd] = yv;
+        }
     }
+    if (kTag) {   // one word for the consumers to poll (they still check every y word's tag)
+        __syncthreads();
+        if (tid == 0) tag_put(g.done + bid, g.epoch, 0.f);
+    }
+}
+
+template <int KPL>
+__global__ __launch_bounds__(kThreads) void gdn_core(GdnArgs g) {
+    gdn_core_body<KPL, false>(g, blockIdx.x);
 }
 
 // ---------------------------------------------------------------- GDN over a chunk of tokens
@@ -1183,9 +1331,10 @@ static int pow2_up(int n) {
     return l;
 }
 
-// y_s = W_s x' for the segments (same I, gs: they share the input row x' = XF(x)).
-static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *xw, const float *z, int VD, float eps,
-                 bool add, hipStream_t st) {
+// The arguments of a projection over the segments (same I, gs: they share the input row
+// x' = XF(x)); *lpr the lanes per row.  False (with a message) for shapes it cannot run.
+static bool proj_args(const SegIn *segs, int n, int xf, const float *x, const float *xw, const float *z, int VD,
+                      float eps, bool add, ProjArgs &a, int *lpr) {
     if (n < 1 || n > kMaxSeg) return refuse("projection segment count");
     const ColiVkTensor *t0 = segs[0].t;
     for (int i = 0; i < n; i++) {
@@ -1195,12 +1344,11 @@ static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *
         if (t->I != t0->I || t->gs != t0->gs || t->nl != t0->nl || t->row_bytes != t0->row_bytes)
             return refuse("fused projections differ in input geometry");
     }
-    ProjArgs a;
     memset(&a, 0, sizeof(a));
-    const int lpr = pow2_up(t0->nl), rpw = 64 / (lpr < 2 ? 2 : lpr);
+    const int l = pow2_up(t0->nl), rpw = 64 / (l < 2 ? 2 : l);
     int g = 0;
     for (int i = 0; i < n; i++) {
-        a.seg[i] = {segs[i].t->w, segs[i].t->sz, segs[i].y, segs[i].t->O, g};
+        a.seg[i] = {segs[i].t->w, segs[i].t->sz, segs[i].y, segs[i].t->O, g, nullptr};
         g += (segs[i].t->O + rpw - 1) / rpw;
     }
     a.nseg = n;
@@ -1220,13 +1368,51 @@ static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *
         const int wph = VD / 8;
         if (VD % 8 || wph < 1 || wph > 64 || (wph & (wph - 1)) || a.I % VD) return refuse("gated norm head size");
     }
-    const int l = lpr < 2 ? 2 : lpr;
-    const bool wide = t0->gs % (32 * kLaneChunks) == 0;   // a unit of kLaneChunks chunks lies in one group
+    *lpr = l < 2 ? 2 : l;
+    return true;
+}
+
+// y_s = W_s x' for the segments (same I, gs: they share the input row x' = XF(x)).
+static bool proj(const SegIn *segs, int n, int xf, const float *x, const float *xw, const float *z, int VD, float eps,
+                 bool add, hipStream_t st) {
+    ProjArgs a;
+    int l;
+    if (!proj_args(segs, n, xf, x, xw, z, VD, eps, add, a, &l)) return false;
+    const bool wide = segs[0].t->gs % (32 * kLaneChunks) == 0;   // a unit of kLaneChunks chunks lies in one group
     switch (xf) {
     case XF_PLAIN: return wide ? proj_lpr<kLaneChunks, XF_PLAIN>(a, l, st) : proj_lpr<1, XF_PLAIN>(a, l, st);
     case XF_NORM: return wide ? proj_lpr<kLaneChunks, XF_NORM>(a, l, st) : proj_lpr<1, XF_NORM>(a, l, st);
     default: return wide ? proj_lpr<kLaneChunks, XF_GATED>(a, l, st) : proj_lpr<1, XF_GATED>(a, l, st);
     }
+}
+
+// ---------------------------------------------------------------- fused GatedDeltaNet layer
+// One launch for in-projection -> recurrence -> out-projection of a decode token (the
+// reference records the same chain in one command buffer, c/backend_vulkan.c:1905-2017):
+// tiles [0, n1) the in-projection (qkv | z | a | b, in_ln of the residual in the x
+// prologue), [n1, n1 + nc) the recurrence blocks of gdn_core, then the out-projection
+// (gated norm prologue, residual add).  Each stage's outputs are tagged words (epoch << 32 |
+// bits) in one buffer, qkv | z | a,b | y | done, which the later tiles poll (the
+// out-projection first one done word per recurrence block, by one wave, so that its many
+// loads of y and z go out once); every wait is on tiles
+// of lower index, so with workgroups dispatched in index order every wait ends.  The
+// out-projection tiles issue their weight loads before they wait.  The residual the
+// in-projection reads is rewritten only by out-projection tiles, which run after every
+// in-projection tile has published (their prologues read it first).
+constexpr int kFuseU = 8;    // row steps per wave of the fused in-projection
+constexpr int kFuseU3 = 2;   // of the fused out-projection (short rows of work per tile after its wait)
+struct GdnFusedArgs {
+    ProjArgs p1, p3;
+    GdnArgs g;
+    int n1, nc;
+};
+template <int LPR1, int LPR3, int KPL>
+__global__ __launch_bounds__(kThreads) void gdn_fused(GdnFusedArgs f) {
+    __shared__ XPrep P;
+    const int t = blockIdx.x;
+    if (t < f.n1) proj_body<LPR1, kLaneChunks, kFuseU, XF_NORM, false, true>(f.p1, t, f.n1, P);
+    else if (t < f.n1 + f.nc) gdn_core_body<KPL, true>(f.g, t - f.n1);
+    else proj_body<LPR3, kLaneChunks, kFuseU3, XF_GATED, true, false>(f.p3, t - f.n1 - f.nc, (int)gridDim.x - f.n1 - f.nc, P);
 }
 
 // ---------------------------------------------------------------- GQA block
@@ -1319,6 +1505,119 @@ static RowMat rowmat(const ColiVkTensor *t) {
 
 // One token.  params != NULL: host-packed [decay | beta | gnorm] (device copy); otherwise
 // decay/beta from the a/b projections of in_ln(resid) and the layer's A_log/dt_bias/gnorm.
+// ---------------------------------------------------------------- fused layer launches
+// Tag buffer of the fused layer kernels (words qkv | z | a,b | y of one launch) and their
+// error word: (epoch << 32) | code, code 1 when a bounded wait gave up.
+struct LayerTags {
+    void *tag = nullptr, *err = nullptr;
+    size_t cap = 0, ecap = 0;
+    uint32_t epoch = 0;
+};
+static LayerTags g_lt;
+// Off by default: on MI355X the one-launch layer measures slower than the three launches
+// (about 24.5 us against 21 us per configs[3] layer; the out-projection tiles see their
+// inputs some 6 us after the last recurrence tile ends).  COLI_HIP_FUSE=1 turns it on.
+static int g_fuse = -1;   // -1: not read yet
+static bool fuse_on() {
+    if (g_fuse < 0) {
+        const char *v = getenv("COLI_HIP_FUSE");
+        g_fuse = v && *v == '1' ? 1 : 0;
+    }
+    return g_fuse == 1;
+}
+
+__global__ void zero_words(unsigned long long *w, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0ull;
+}
+
+// The shapes the fused kernel is instantiated for: the configs[3] GatedDeltaNet layer
+// (in-projection rows of 2048 columns, out-projection rows of 4096, key heads of 128, conv
+// taps <= kGdnMaxK, group size a multiple of 64).  Other shapes take the three launches.
+static bool gdn_fusable(const ColiVkTensor *tqkv, const ColiVkTensor *tout, const GdnDims &d) {
+    return tout && tout->fmt == 6 && tout->layout == kLayoutLanes && tqkv->gs % (32 * kLaneChunks) == 0 &&
+           tout->gs % (32 * kLaneChunks) == 0 && pow2_up(tqkv->nl) == 32 && pow2_up(tout->nl) == 64 && d.KD == 128 &&
+           d.K <= kGdnMaxK;
+}
+
+static bool gdn_fused_launch(GdnState &G, const float *src, const float *ln, ColiVkTensor *tqkv, ColiVkTensor *tz,
+                             ColiVkTensor *ta, ColiVkTensor *tb, ColiVkTensor *tout, float *dst, bool add, const GdnDims &d,
+                             hipStream_t st) {
+    const int VV = d.VH * d.VD;
+    const size_t nwords = (size_t)d.CD + VV + 2 * d.VH + VV + (size_t)d.VH * (d.VD / kGdnCols);
+    if (!scratch(&g_lt.tag, &g_lt.cap, nwords * 8) || !scratch(&g_lt.err, &g_lt.ecap, 256)) return false;
+    unsigned long long *tags = (unsigned long long *)g_lt.tag, *err = (unsigned long long *)g_lt.err;
+    unsigned long long *t_qkv = tags, *t_z = t_qkv + d.CD, *t_ab = t_z + VV, *t_y = t_ab + 2 * d.VH, *t_done = t_y + VV;
+    if (++g_lt.epoch == 0) {   // tags wrap: no old word may carry the new epoch
+        hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, tags, g_lt.cap / 8);
+        hipLaunchKernelGGL(zero_words, dim3(1), dim3(64), 0, st, err, (size_t)1);
+        g_lt.epoch = 1;
+    }
+    const uint32_t ep = g_lt.epoch;
+    GdnFusedArgs f;
+    memset(&f, 0, sizeof(f));
+    int l1, l3;
+    float *placeholder = (float *)tags;   // proj_args checks a destination; the tagged words replace it
+    const SegIn in[4] = {{tqkv, placeholder}, {tz, placeholder}, {ta, placeholder}, {tb, placeholder}};
+    if (!proj_args(in, 4, XF_NORM, src, ln, nullptr, 0, d.eps, false, f.p1, &l1)) return false;
+    f.p1.seg[0].yt = t_qkv;
+    f.p1.seg[1].yt = t_z;
+    f.p1.seg[2].yt = t_ab;
+    f.p1.seg[3].yt = t_ab + d.VH;
+    f.p1.epoch = ep;
+    f.p1.err = err;
+    const SegIn o[1] = {{tout, dst}};
+    if (!proj_args(o, 1, XF_GATED, nullptr, G.gnorm, nullptr, d.VD, d.eps, add, f.p3, &l3)) return false;
+    f.p3.xt = t_y;
+    f.p3.zt = t_z;
+    f.p3.done = t_done;
+    f.p3.ndone = d.VH * (d.VD / kGdnCols);
+    f.p3.epoch = ep;
+    f.p3.err = err;
+    GdnArgs &g = f.g;
+    g.ring = G.ring;
+    g.head = G.head;
+    g.convw = G.convw;
+    g.S = G.S;
+    g.alog = G.alog;
+    g.dtb = G.dtb;
+    g.eps = d.eps;
+    g.D = tqkv->I;
+    g.KH = d.KH;
+    g.KD = d.KD;
+    g.VH = d.VH;
+    g.VD = d.VD;
+    g.K = d.K;
+    g.CD = d.CD;
+    g.qkvt = t_qkv;
+    g.abt = t_ab;
+    g.yt = t_y;
+    g.done = t_done;
+    g.err = err;
+    g.epoch = ep;
+    f.n1 = (f.p1.ngroups + kWaves * kFuseU - 1) / (kWaves * kFuseU);
+    f.nc = d.VH * (d.VD / kGdnCols);
+    const int n3 = (f.p3.ngroups + kWaves * kFuseU3 - 1) / (kWaves * kFuseU3);
+    if (l1 != 32 || l3 != 64 || f.p3.ndone > 64 * 8) return refuse("fused GDN shape");
+    hipLaunchKernelGGL((gdn_fused<32, 64, 2>), dim3((unsigned)(f.n1 + f.nc + n3)), dim3(kThreads), 0, st, f);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("fused GDN launch", e);
+    G.head = G.head + 1 == G.K ? 0 : G.head + 1;   // the ring advanced by this token
+    return true;
+}
+
+// Error word of the fused layer launches since the last call (synchronizes): 0 none, 1 a
+// bounded wait gave up, -1 runtime error.  Reading clears it.
+static int layer_error_take() {
+    if (!g_lt.err) return 0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    unsigned long long v = 0;
+    if (hipMemcpy(&v, g_lt.err, 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if ((uint32_t)v == 0) return 0;
+    const unsigned long long z = 0;
+    if (hipMemcpy(g_lt.err, &z, 8, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    return (int)(uint32_t)v;
+}
+
 static bool gdn_block(int gi, const float *src, const float *ln, const float *params, ColiVkTensor *tqkv,
                       ColiVkTensor *tz, ColiVkTensor *ta, ColiVkTensor *tb, ColiVkTensor *tout, float *dst, bool add,
                       const GdnDims &d, hipStream_t st) {
@@ -1346,6 +1645,8 @@ static bool gdn_block(int gi, const float *src, const float *ln, const float *pa
                t->nl == tqkv->nl && t->row_bytes == tqkv->row_bytes;
     };
     const bool ab_proj = !params && lanes_like(ta) && lanes_like(tb) && lanes_like(tz) && tqkv->fmt == 6;
+    if (ab_proj && ln && fuse_on() && gdn_fusable(tqkv, tout, d))
+        return gdn_fused_launch(G, src, ln, tqkv, tz, ta, tb, tout, dst, add, d, st);
     const SegIn in[4] = {{tqkv, qkv}, {tz, z}, {ta, ab}, {tb, ab + d.VH}};
     if (!proj(in, ab_proj ? 4 : 2, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, st))
         return false;
@@ -1448,6 +1749,9 @@ void layer_shutdown() {
         g_ln[i] = LnState();
     }
     for (int i = 0; i < W_COUNT; i++) scratch_free(&g_w[i].p, &g_w[i].cap);
+    scratch_free(&g_lt.tag, &g_lt.cap);
+    scratch_free(&g_lt.err, &g_lt.ecap);
+    g_lt.epoch = 0;
     scratch_free((void **)&g_str.d_resid, &g_str.resid_cap);
     scratch_free((void **)&g_str.d_y, &g_str.dy_cap);
     scratch_free((void **)&g_str.d_fnw, &g_str.fnw_cap);
@@ -1879,6 +2183,12 @@ COLI_API int coli_vk_stream_begin(const float *x, int D) {
 // G.ready = 0), that disables the device and the call returns 0, so the engine takes its
 // host path.  The stream must be idle (every caller has synchronised).
 static bool stream_moe_ok(const char *who) {
+    const int le = layer_error_take();
+    if (le != 0) {
+        fprintf(stderr, "[HIP] %s: fused layer kernel reported %s\n", who,
+                le == 1 ? "a bounded wait that gave up" : "a runtime error");
+        return fail(who, hipErrorLaunchFailure);
+    }
     const int e = moe_error_take();
     if (e == 0) return true;
     fprintf(stderr, "[HIP] %s: fused MoE reported %s\n", who,
@@ -2034,4 +2344,12 @@ COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
     const int n = g_str.hist_K[layer] < K ? g_str.hist_K[layer] : K;
     for (int k = 0; k < n; k++) idx_out[k] = g_str.h_hist[layer * kMaxK + k];
     return n;
+}
+
+// Test hook: fused layer launches on (1) or off (0, the separate kernels); returns the
+// previous setting.  Both give the same results bit for bit.
+COLI_API int coli_hip_layer_fuse(int on) {
+    const int prev = fuse_on() ? 1 : 0;
+    g_fuse = on ? 1 : 0;
+    return prev;
 }

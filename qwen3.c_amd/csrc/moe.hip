@@ -35,7 +35,6 @@ namespace coli {
 
 constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
 constexpr int kGSteps = 2;                // gate/up row steps per tile
-constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
 constexpr int kRouteReps = 4;             // copies of the route block (readers spread over them)
 constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1], K <= 8
 
@@ -64,36 +63,6 @@ struct MoeArgs {
     int nD, nC;                           // down tiles per slot (kDRows rows), combine tiles
     MoeGeom g;
 };
-
-// ---------------------------------------------------------------- tagged words
-__device__ __forceinline__ unsigned long long aload(const unsigned long long *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void tag_put(unsigned long long *p, uint32_t epoch, float v) {
-    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-// The error word holds (epoch << 32) | code of a launch that failed (code 1: a bounded wait
-// gave up, 2: a route held an out-of-range expert id).  A wait gives up past kPollLimit
-// polls, or at its 16th poll once its own launch has failed; the word is read on every 16th
-// poll only (each read is one more memory round trip between a poll and the next).  The
-// epoch stamp means no launch has to clear the word: an earlier launch's failure never
-// matches.
-__device__ __forceinline__ void err_set(unsigned long long *err, uint32_t epoch, int code) {
-    __hip_atomic_store(err, ((unsigned long long)epoch << 32) | (uint32_t)code, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool poll_give_up(unsigned long long *err, uint32_t epoch, int polls) {
-    if (polls > kPollLimit ||
-        ((polls & 15) == 15 &&
-         (uint32_t)(__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == epoch)) {
-        err_set(err, epoch, 1);
-        return true;
-    }
-    if (polls < 8) __builtin_amdgcn_s_sleep(1);   // back off: the line may be in demand
-    else __builtin_amdgcn_s_sleep(8);
-    return false;
-}
 
 // tag-buffer regions
 __device__ __forceinline__ unsigned long long *route_of(const MoeArgs &a, int rep) {

@@ -77,6 +77,38 @@ __device__ __forceinline__ float wave_sum_dppf(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+constexpr int kPollLimit = 1 << 16;       // bounded polls (each ~0.3-2 us)
+
+// ---------------------------------------------------------------- tagged words
+__device__ __forceinline__ unsigned long long aload(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tag_put(unsigned long long *p, uint32_t epoch, float v) {
+    __hip_atomic_store(p, ((unsigned long long)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// The error word holds (epoch << 32) | code of a launch that failed (code 1: a bounded wait
+// gave up, 2: a route held an out-of-range expert id).  A wait gives up past kPollLimit
+// polls, or at its 16th poll once its own launch has failed; the word is read on every 16th
+// poll only (each read is one more memory round trip between a poll and the next).  The
+// epoch stamp means no launch has to clear the word: an earlier launch's failure never
+// matches.
+__device__ __forceinline__ void err_set(unsigned long long *err, uint32_t epoch, int code) {
+    __hip_atomic_store(err, ((unsigned long long)epoch << 32) | (uint32_t)code, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool poll_give_up(unsigned long long *err, uint32_t epoch, int polls) {
+    if (polls > kPollLimit ||
+        ((polls & 15) == 15 &&
+         (uint32_t)(__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 32) == epoch)) {
+        err_set(err, epoch, 1);
+        return true;
+    }
+    if (polls < 8) __builtin_amdgcn_s_sleep(1);   // back off: the line may be in demand
+    else __builtin_amdgcn_s_sleep(8);
+    return false;
+}
+
 // ---------------------------------------------------------------- certified routing
 // The reference computes a router logit as a sequential fp32 sum of rounded products
 // (c/qwen.c:178-189; int8 rows :230-238, acc * scale after the sum).  The device's logit L
