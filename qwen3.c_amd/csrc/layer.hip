@@ -785,6 +785,7 @@ __global__ void gdn_ring_push(const float *__restrict__ qkv, int n, float *__res
 
 // ---------------------------------------------------------------- GQA attention
 constexpr int kAttT = 32;       // positions per chunk (block)
+constexpr int kAttW = 8;        // waves of an attn_part block
 constexpr int kAttMaxG = 16;    // query heads per kv head
 constexpr int kAttMaxHD = 512;
 constexpr int kAttMaxHR = 64;   // rotary pairs (rot / 2)
@@ -879,10 +880,12 @@ __device__ __forceinline__ void norm_rope_row(float *x, float *gdst, const float
 // needs is loaded at the start (one memory round trip), then the q rows of the group (and
 // the new key row, in the chunk holding pos) are normed and rotated, scores computed,
 // the chunk softmax taken and P.V accumulated.
-template <int DPL>
-__global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
-    constexpr int kSteps = kAttT / (kWaves * 4);   // position steps per wave (4 positions each)
-    constexpr int kVPer = kAttMaxHD / kThreads;    // head dims per thread in P.V
+template <int DPL, int AW>
+__global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
+    constexpr int kT = 64 * AW;                 // threads of the block (AW waves)
+    constexpr int kSteps = kAttT / (AW * 4);   // position steps per wave (4 positions each)
+    constexpr int kPV = kT > 256 ? 256 : kT;    // P.V threads per head half (AW 8: two halves of the heads)
+    constexpr int kVPer = kAttMaxHD / kPV;      // head dims per thread in P.V
     __shared__ __attribute__((aligned(16))) float s_q[kAttMaxG][kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_k[kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_p[kAttMaxG][kAttT];
@@ -893,7 +896,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     const int t0 = sp * kAttT, t1 = min(t0 + kAttT, a.pos + 1), n = t1 - t0;
     const bool owns_pos = a.pos >= t0 && a.pos < t1;
     // K rows of the score steps (16 lanes per position, DPL dims each) and V columns of
-    // P.V (thread d: dims d + kThreads * i), all in flight together
+    // P.V (thread pvt: dims pvt + kPV * i), all in flight together
     // (branch-free buffer loads: out-of-range offsets read 0, so no load waits behind a
     // data-dependent branch)
     const int pl = lane >> 4, part = lane & 15;
@@ -904,7 +907,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     float kv[kSteps][DPL];
 #pragma unroll
     for (int st = 0; st < kSteps; st++) {
-        const int t = t0 + (st * kWaves + wave) * 4 + pl;
+        const int t = t0 + (st * AW + wave) * 4 + pl;
         const bool ld = t < t1 && t != a.pos;
 #pragma unroll
         for (int e = 0; e < DPL; e += 4) {
@@ -918,11 +921,12 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     }
     // V: the cached rows, and this token's v for the position pos (selected below); dims
     // slots past hd are skipped uniformly
+    const int pvt = tid % kPV, half = tid / kPV;   // P.V: dims of thread pvt, heads of half
     float vv[kAttT][kVPer];
 #pragma unroll
     for (int i = 0; i < kVPer; i++) {
-        if (i > 0 && i * kThreads >= hd) continue;   // uniform; a guarded body keeps the unroll
-        const int d = tid + i * kThreads;
+        if (i > 0 && i * kPV >= hd) continue;   // uniform; a guarded body keeps the unroll
+        const int d = pvt + i * kPV;
         const float nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                        rn, owns_pos && d < hd ? d * 4 : (int)kOOB, 0, 0));
 #pragma unroll
@@ -936,15 +940,15 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     }
     {   // the wave's first two q rows and, in the chunk holding pos, the new key row: all
         // their loads first, then the norms (rows past two per wave follow one by one)
-        const int g0 = wave, g1 = wave + kWaves;
-        const bool own_k = owns_pos && wave == kWaves - 1;
+        const int g0 = wave, g1 = wave + AW;
+        const bool own_k = owns_pos && wave == AW - 1;
         RowLd r0, r1, rk;
         if (g0 < G) row_load(r0, a.q + (size_t)(kh * G + g0) * 2 * hd, a.qn, a);
         if (g1 < G) row_load(r1, a.q + (size_t)(kh * G + g1) * 2 * hd, a.qn, a);
         if (own_k) row_load(rk, a.k + (size_t)kh * hd, a.kn, a);
         if (g0 < G) row_finish(s_q[g0], nullptr, r0, a);
         if (g1 < G) row_finish(s_q[g1], nullptr, r1, a);
-        for (int gg = wave + 2 * kWaves; gg < G; gg += kWaves)
+        for (int gg = wave + 2 * AW; gg < G; gg += AW)
             norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
         if (own_k) {   // the new key row and value row (c/qwen.c:605-614)
             const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
@@ -957,7 +961,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     // from LDS once for all the wave's steps
 #pragma unroll
     for (int st = 0; st < kSteps; st++) {
-        const int t = t0 + (st * kWaves + wave) * 4 + pl;
+        const int t = t0 + (st * AW + wave) * 4 + pl;
         if (t < t1 && t == a.pos)
 #pragma unroll
             for (int e = 0; e < DPL; e++) kv[st][e] = s_k[part * DPL + e];
@@ -974,7 +978,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
         }
 #pragma unroll
         for (int st = 0; st < kSteps; st++) {
-            const int t = t0 + (st * kWaves + wave) * 4 + pl;
+            const int t = t0 + (st * AW + wave) * 4 + pl;
             float sc = 0.f;
 #pragma unroll
             for (int e = 0; e < DPL; e++) sc = fmaf(qf[e], kv[st][e], sc);
@@ -986,7 +990,7 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
     // chunk max and sum of exp per head: 32 lanes per head, lane = position; positions past
     // the chunk get p = 0
     static_assert(kAttT == 32, "one position per lane of a half wave");
-    for (int gg = tid >> 5; gg < G; gg += kThreads / 32) {
+    for (int gg = tid >> 5; gg < G; gg += kT / 32) {
         const int t = tid & 31;
         const float sc = t < n ? s_p[gg][t] : -INFINITY;
         float m = sc;
@@ -1003,13 +1007,14 @@ __global__ __launch_bounds__(kThreads) void attn_part(AttnArgs a) {
         }
     }
     __syncthreads();
-    // P.V: thread d of the head dims, all G heads
+    // P.V: thread pvt of the head dims; with two halves, half h takes heads h G / 2 ..
     float *pb = a.part + ((size_t)kh * a.nsplit + sp) * G * (hd + 2);
+    const int nh = kT > kPV ? (G + 1) / 2 : G, g_lo = half * nh, g_hi = min(G, g_lo + nh);
 #pragma unroll
     for (int i = 0; i < kVPer; i++) {   // guarded bodies, no breaks: the loops unroll fully
-        const int d = tid + i * kThreads;
-        if (i * kThreads >= hd) continue;   // uniform
-        for (int gg = 0; gg < G; gg++) {   // p as float4 broadcasts, positions in order
+        const int d = pvt + i * kPV;
+        if (i * kPV >= hd) continue;   // uniform
+        for (int gg = g_lo; gg < g_hi; gg++) {   // p as float4 broadcasts, positions in order
             float acc = 0.f;
 #pragma unroll
             for (int t4 = 0; t4 < kAttT; t4 += 4) {
@@ -1470,10 +1475,10 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
         a.sn[j] = (float)sin((double)ang);
     }
     switch (hd / 16) {
-    case 4: hipLaunchKernelGGL(attn_part<4>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
-    case 8: hipLaunchKernelGGL(attn_part<8>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
-    case 16: hipLaunchKernelGGL(attn_part<16>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
-    case 32: hipLaunchKernelGGL(attn_part<32>, dim3(KH * nsplit), dim3(kThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((attn_part<4, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((attn_part<8, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
+    case 16: hipLaunchKernelGGL((attn_part<16, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((attn_part<32, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
     default: return refuse("head dim not in {64, 128, 256, 512}");
     }
     hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kThreads), 0, st, a);
