@@ -29,14 +29,22 @@ def rel_to_max(got, ref):
 
 
 # ---------------------------------------------------------------- GQA block
-@pytest.mark.parametrize("shape", ["small", "cfg3"])
+GQA_SHAPES = {   # D, H, KH, hd, rot, gs, max_t, layer
+    "small": (256, 4, 2, 64, 16, 64, 16, 3),
+    "cfg3": (2048, 16, 2, 256, 64, 128, 64, 4),
+    # query heads per kv head 1, 3 and 16: the partial kernel's P.V splits a group's heads
+    # over two thread halves (odd groups, an empty half, the largest group)
+    "mha": (256, 4, 4, 64, 16, 64, 40, 140),
+    "g3": (256, 6, 2, 64, 32, 64, 40, 141),
+    "g16": (512, 32, 2, 128, 32, 128, 40, 142),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(GQA_SHAPES))
 def test_gqa_full(lib, lorc, gen, shape):
     """coli_vk_gqa_full over consecutive positions (one call per token and one call of
     several tokens), KV mirror rows checked against the oracle's cache."""
-    if shape == "small":
-        D, H, KH, hd, rot, gs, max_t, layer = 256, 4, 2, 64, 16, 64, 16, 3
-    else:
-        D, H, KH, hd, rot, gs, max_t, layer = 2048, 16, 2, 256, 64, 128, 64, 4
+    D, H, KH, hd, rot, gs, max_t, layer = GQA_SHAPES[shape]
     W = _layers.GqaWeights(gen, gen.stream(0x9A00, layer), D, H, KH, hd, rot, gs)
     tq, tk, tv, to = (m.upload(lib) for m in (W.q, W.k, W.v, W.o))
     lib.kv_ensure(layer, KH * max_t, hd, hd)
