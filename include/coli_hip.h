@@ -280,6 +280,12 @@ int   coli_hip_gdn_state_read(int layer, float *ring, float *S);
  * counterpart in the reference (its layer is separate dispatches).  Off by default (slower on
  * MI355X at configs[3]); the environment variable COLI_HIP_FUSE=1 starts with it on. */
 int   coli_hip_layer_fuse(int on);
+/* Routing certification of every decode route (each top-k candidate's logit recomputed as
+ * the reference's sequential fp32 sum and ranked by it) on (1), or only of routes whose
+ * device logits leave the order ambiguous (0, the default); returns the previous setting.
+ * Both give the reference's picks.  A test hook with no counterpart in the reference (it
+ * computes only the sequential logits). */
+int   coli_hip_moe_cert_all(int on);
 
 /* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
  * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32

@@ -72,6 +72,7 @@ _SIGS = {
     "coli_vk_gdn_ba_weight": (_I, [_I, _P, _P, _P, _I, _I]),
     "coli_hip_gdn_state_read": (_I, [_I, _P, _P]),
     "coli_hip_layer_fuse": (_I, [_I]),
+    "coli_hip_moe_cert_all": (_I, [_I]),
     "coli_hip_st_open": (_P, [C.c_char_p]),
     "coli_hip_st_close": (None, [_P]),
     "coli_hip_st_count": (_I, [_P]),
@@ -405,6 +406,10 @@ class Lib:
     def layer_fuse(self, on):
         """Fused layer launches on/off (test hook); returns the previous setting."""
         return bool(self.L.coli_hip_layer_fuse(1 if on else 0))
+
+    def moe_cert_all(self, on):
+        """Certify every decode route on/off (test hook); returns the previous setting."""
+        return bool(self.L.coli_hip_moe_cert_all(1 if on else 0))
 
     def gdn_reset(self):
         self.L.coli_vk_gdn_reset()

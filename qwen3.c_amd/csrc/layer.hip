@@ -1186,7 +1186,8 @@ __global__ __launch_bounds__(kThreads) void router_lb(const float *__restrict__ 
 // certified against the reference's sequential logits (route_certify); x = the router input.
 __global__ __launch_bounds__(64) void route_row(const float *__restrict__ lb, const float *__restrict__ x,
                                                 const uint8_t *__restrict__ rw, const float *__restrict__ rs,
-                                                int rfmt, int rrb, int D, int E, int K, int *idx, float *val) {
+                                                int rfmt, int rrb, int D, int E, int K, int *idx, float *val,
+                                                int cert_all) {
     __shared__ RouteLds R;
     __shared__ CertLds C;
     for (int e = threadIdx.x; e < E; e += 64) {
@@ -1196,9 +1197,15 @@ __global__ __launch_bounds__(64) void route_row(const float *__restrict__ lb, co
     }
     wave_lds_order();
     route_wave(R, E, K, C.l, C.b);
+    if (cert_all) {   // test hook: every candidate gets its reference logit
+        if (threadIdx.x == 0) {
+            R.amb = 1;
+            R.thr = -INFINITY;
+        }
+        wave_lds_order();
+    }
     route_certify_wave(
-        R, C, K, D, rfmt == 1, rs, [&](float *xn) { stage_input_wave(x, nullptr, D, 0.f, xn); },
-        [&](int e) { return rw + (size_t)e * rrb; });
+        R, C, K, D, rfmt == 1, rs, rw, rrb, E, [&](float *xn) { stage_input_wave(x, nullptr, D, 0.f, xn); });
     if (threadIdx.x < K) {
         idx[threadIdx.x] = R.idx[threadIdx.x];
         val[threadIdx.x] = R.val[threadIdx.x] / R.vsum;
@@ -2299,7 +2306,7 @@ static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float 
     int *di = (int *)(dl + 2 * E);
     float *dv = dl + 2 * E + kMaxK;
     hipLaunchKernelGGL(route_row, dim3(1), dim3(64), 0, stream(), dl, dn, router->w, router->sz, router->fmt,
-                       router->row_bytes, g_str.D, E, topk, di, dv);
+                       router->row_bytes, g_str.D, E, topk, di, dv, moe_cert_all());
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("route launch", e) ? 1 : 0;
     if (!host_scratch((void **)&g_str.h_nrm, &g_str.hnrm_cap, (size_t)(g_str.D + 2 * kMaxK) * 4)) return 0;

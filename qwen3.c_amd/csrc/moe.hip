@@ -51,6 +51,7 @@ struct MoeArgs {
     int K;
     float *out;                           // [D]
     int accumulate;                       // out += (residual stream) instead of out =
+    int cert_all;                         // test hook: certify every route (all candidates)
     int *idx_out;                         // optional [K]
     float *val_out;                       // optional [K + 1] (renormed weights, then shgt)
     unsigned long long *tagv;             // logits [E + 1] | crude / tight bounds [E + 1] each |
@@ -266,28 +267,20 @@ __device__ __forceinline__ float4 int8x4(uint32_t q) {
 // norm weight the zero-centred RMSNorm of x (c/qwen.c:326-330: double sum of squares,
 // x r (1 + w) in the reference's order).  Router and route tiles run this same code, so
 // they see the same row bit for bit.
-__device__ __forceinline__ void stage_input(const float *x, const float *xw, int D, float eps, float *xn, double *s_red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (!xw) {
-        for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = x[i];
-        __syncthreads();
-        return;
+// The normed input row into LDS (xn[0, D)) from x and the norm weights as loaded by prep_load
+// (issued before any other load of the tile, so only these are waited for): norm_apply,
+// the G tiles' staging, so the router's input and the experts' are the same bits.
+__device__ __forceinline__ void stage_input(XRegs &xr, const XRegs &wr, int D, float eps, float *xn, double *s_red) {
+    norm_apply(xr, wr, D, D, eps, s_red);
+#pragma unroll
+    for (int k = 0; k < XRegs::kWords; k++) {
+        const int w = threadIdx.x + k * kThreads;
+        if (w < D / 8) {
+            *(float4 *)(xn + 8 * w) = make_float4(xr.v[k][0], xr.v[k][1], xr.v[k][2], xr.v[k][3]);
+            *(float4 *)(xn + 8 * w + 4) = make_float4(xr.v[k][4], xr.v[k][5], xr.v[k][6], xr.v[k][7]);
+        }
     }
-    double ss = 0;
-    for (int i = threadIdx.x; i < D; i += kThreads) {
-        const float v = x[i];
-        xn[i] = v;
-        ss += (double)v * v;
-    }
-    ss = wave_sum_dpp(ss);
-    __syncthreads();
-    if (lane == 0) s_red[wave] = ss;
-    __syncthreads();
-    double t = 0;
-    for (int k = 0; k < kWaves; k++) t += s_red[k];
-    const float rs = 1.f / sqrtf((float)(t / D) + eps);
-    for (int i = threadIdx.x; i < D; i += kThreads) xn[i] = xn[i] * rs * (1.f + xw[i]);
-    __syncthreads();
+    lds_barrier();
 }
 
 // Bounds of the logits: crude (published with the logits) and tight (published later), the
@@ -320,8 +313,13 @@ __device__ __forceinline__ void tile_router(const MoeArgs &a, int r0, double *s_
                 wv[c] = int8x4((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, c0 + (lane + c * 64) * 4, 0, kStream));
         }
     };
+    // x and the norm weights first (range 0 without a norm: no memory access), then the row
+    XRegs xr, wr;
+    const int nI = a.xw ? D : 0;
+    prep_load(a.x, nI, D, xr);
+    prep_load(a.xw ? a.xw : a.x, nI, D, wr);
     load_row(0, w);
-    if (a.xw) stage_input(a.x, a.xw, D, a.eps, xn, s_red);
+    if (a.xw) stage_input(xr, wr, D, a.eps, xn, s_red);
     if (!live) return;
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)D * 4u);
     auto load_x = [&](int c0, float4 (&xq)[kRouterRC]) {
@@ -403,9 +401,16 @@ __device__ __forceinline__ void tile_route_n(const MoeArgs &a, RouteLds &R, Cert
         }
         wave_lds_order();
     }
+    if (a.cert_all) {   // test hook: every candidate gets its reference logit
+        if (lane == 0) {
+            R.amb = 1;
+            R.thr = -INFINITY;
+        }
+        wave_lds_order();
+    }
     route_certify_wave(
-        R, C, K, a.g.D, a.rfmt == 1, a.rs, [&](float *xn) { stage_input_wave(a.x, a.xw, a.g.D, a.eps, xn); },
-        [&](int e) { return a.rw + (size_t)e * a.rrb; });
+        R, C, K, a.g.D, a.rfmt == 1, a.rs, a.rw, a.rrb, a.E,
+        [&](float *xn) { stage_input_wave(a.x, a.xw, a.g.D, a.eps, xn); });
     // lane (copy c, word k) writes word k of copy c: words [0, K) expert ids, [K, 2K)
     // renormed weights, 2K the shared gate
     const float sm = R.vsum;
@@ -433,7 +438,7 @@ __device__ __forceinline__ void tile_route(const MoeArgs &a, RouteLds &R, CertLd
 
 // ---------------------------------------------------------------- LDS of the kernel
 struct RouterLds {
-    float xn[kLaneMaxI];   // the (normed) input row
+    __attribute__((aligned(16))) float xn[kLaneMaxI];   // the (normed) input row
 };
 struct RouteTileLds {
     RouteLds r;
@@ -731,6 +736,7 @@ static bool moe_args(int layer, const ColiVkTensor *router, int K, const float *
     a.K = K;
     a.out = d_out;
     a.accumulate = accumulate;
+    a.cert_all = moe_cert_all();
     a.idx_out = d_idx;
     a.val_out = d_val;
     a.g = T.geom;
@@ -749,6 +755,18 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.err = (unsigned long long *)((uint8_t *)g_ms.misc + 64);
     a.epoch = next_epoch(&g_ms.epoch, a.tagv, g_ms.tag_cap / 8, a.err, st);
     return dispatch_shape<LaunchMoe>(a.g, a, st) || (ok() && reject("expert shape not compiled"));
+}
+
+static int g_cert_all = 0;
+int moe_cert_all() { return g_cert_all; }
+
+// Test hook: every route certified (each candidate's reference logit computed and ranked) on
+// (1) or only the ambiguous ones (0, the default); returns the previous setting.  Both give
+// the reference's picks.
+COLI_API int coli_hip_moe_cert_all(int on) {
+    const int prev = g_cert_all;
+    g_cert_all = on ? 1 : 0;
+    return prev;
 }
 
 bool moe_ready(int layer) {

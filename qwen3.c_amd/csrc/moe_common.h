@@ -121,7 +121,7 @@ __device__ __forceinline__ bool poll_give_up(unsigned long long *err, uint32_t e
 // block of 4 columns: |S_k| <= |S_b| + (sum of the block's |p|), S_b the prefix before the
 // block, computed in fp32 (its rounding, < 32 n u A over all blocks, is added).  A routing
 // decision between experts whose intervals [L - B, L + B] do not overlap is the
-// reference's; route_certify_wave recomputes l_ref exactly (seq_logit) for every candidate whose
+// reference's; route_certify_wave recomputes l_ref exactly for every candidate whose
 // interval meets the decision boundary.
 __device__ __forceinline__ float router_bound(float L, float sum_abs_prefix, float A, int n, float scale) {
     const float u = 0x1p-24f, nu = (float)n * u;
@@ -218,41 +218,6 @@ __device__ __forceinline__ float router_row(int D, float scale, bool int8, float
         }
     pre = 4.f * wave_sum_dppf(pre);
     return router_bound(L, pre + 4.f * A, A, D, int8 ? scale : 1.f);
-}
-
-// The reference's logit of one router row (c/qwen.c:178-189: acc += x[i] * w[i] in index
-// order, fp32, no contraction; int8 rows :230-238, then acc * scale).  x in LDS; rows are
-// 16-byte aligned (device rows are padded to 16 bytes).
-__device__ __forceinline__ float seq_logit(const float *x, const uint8_t *row, bool int8, int D, float scale) {
-    float acc = 0.f;
-    int i0 = 0;
-    for (; i0 + 64 <= D; i0 += 64) {
-        float w[64];
-        if (!int8) {
-            const float4 *r4 = (const float4 *)(row + (size_t)i0 * 4);
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float4 v = r4[j];
-                w[4 * j] = v.x, w[4 * j + 1] = v.y, w[4 * j + 2] = v.z, w[4 * j + 3] = v.w;
-            }
-        } else {
-            const int4 *r4 = (const int4 *)(row + i0);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int4 v = r4[j];
-                const int q[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int b = 0; b < 16; b++) w[16 * j + b] = (float)(int8_t)(q[b / 4] >> (8 * (b % 4)));
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 64; j++) acc = __fadd_rn(acc, __fmul_rn(x[i0 + j], w[j]));
-    }
-    for (; i0 < D; i0++) {
-        const float w = int8 ? (float)(int8_t)row[i0] : ((const float *)row)[i0];
-        acc = __fadd_rn(acc, __fmul_rn(x[i0], w));
-    }
-    return int8 ? __fmul_rn(acc, scale) : acc;
 }
 
 struct CertLds {
@@ -456,10 +421,11 @@ __device__ __forceinline__ void route_wave(RouteLds &R, int E, int K, const floa
 }
 
 // The router's input row into LDS by one wave, bit for bit what the block form stage_input
-// (moe.hip) stages: x itself, or the zero-centred RMSNorm of x with weight xw
-// (c/qwen.c:326-330).  The block form sums squares per thread t over i = t + 256 k, per wave
-// by wave_sum_dpp, then the 4 wave sums in order; lane l here plays threads l + 64 w of the
-// 4 waves w, so every addition happens in the same order.
+// (moe.hip, norm_apply over XRegs) stages: x itself, or the zero-centred RMSNorm of x with
+// weight xw (c/qwen.c:326-330).  The block form's thread t sums the squares of its words
+// t + kThreads k (8 columns each, k ascending), per wave by wave_sum_dpp, then the 4 wave
+// sums in order; lane l here plays threads l + 64 w of the 4 waves w, so every addition
+// happens in the same order.  All loads are issued before the first use.
 __device__ __forceinline__ void stage_input_wave(const float *x, const float *xw, int D, float eps, float *xn) {
     const int lane = threadIdx.x & 63;
     if (!xw) {
@@ -467,46 +433,196 @@ __device__ __forceinline__ void stage_input_wave(const float *x, const float *xw
         wave_lds_order();
         return;
     }
+    constexpr int kW = XRegs::kWords;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x), (short)0, D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(xw), (short)0, D * 4, 0x00020000);
+    // x: the squares summed, x kept in xn; then the norm weights (two round trips, few registers)
     double ws[kWaves];
+    {
+        float xv[kWaves][kW][8];
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-        double ss = 0;
-        for (int i = lane + 64 * w; i < D; i += kThreads) {
-            const float v = x[i];
-            ss += (double)v * v;
+        for (int w = 0; w < kWaves; w++)
+#pragma unroll
+            for (int k = 0; k < kW; k++) {
+                const int wd = lane + 64 * w + kThreads * k;
+                load8f(rx, wd < D / 8 ? wd * 32 : (int)0x80000000, xv[w][k]);
+            }
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            double ss = 0;
+#pragma unroll
+            for (int k = 0; k < kW; k++) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) ss += (double)xv[w][k][c] * xv[w][k][c];   // zeros past D add 0
+                const int wd = lane + 64 * w + kThreads * k;
+                if (wd < D / 8) {   // xn: 16-byte aligned
+                    *(float4 *)(xn + 8 * wd) = make_float4(xv[w][k][0], xv[w][k][1], xv[w][k][2], xv[w][k][3]);
+                    *(float4 *)(xn + 8 * wd + 4) = make_float4(xv[w][k][4], xv[w][k][5], xv[w][k][6], xv[w][k][7]);
+                }
+            }
+            ws[w] = wave_sum_dpp(ss);
         }
-        ws[w] = wave_sum_dpp(ss);
     }
     double t = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; w++) t += ws[w];
     const float rs = 1.f / sqrtf((float)(t / D) + eps);
-    for (int i = lane; i < D; i += 64) xn[i] = x[i] * rs * (1.f + xw[i]);
+    float wv[kWaves][kW][8];
+#pragma unroll
+    for (int w = 0; w < kWaves; w++)
+#pragma unroll
+        for (int k = 0; k < kW; k++) {
+            const int wd = lane + 64 * w + kThreads * k;
+            load8f(rw, wd < D / 8 ? wd * 32 : (int)0x80000000, wv[w][k]);
+        }
+    wave_lds_order();
+#pragma unroll
+    for (int w = 0; w < kWaves; w++)
+#pragma unroll
+        for (int k = 0; k < kW; k++) {
+            const int wd = lane + 64 * w + kThreads * k;
+            if (wd < D / 8) {
+                float4 *o = (float4 *)(xn + 8 * wd);
+                const float4 a = o[0], b = o[1];
+                o[0] = make_float4(a.x * rs * (1.f + wv[w][k][0]), a.y * rs * (1.f + wv[w][k][1]),
+                                   a.z * rs * (1.f + wv[w][k][2]), a.w * rs * (1.f + wv[w][k][3]));
+                o[1] = make_float4(b.x * rs * (1.f + wv[w][k][4]), b.y * rs * (1.f + wv[w][k][5]),
+                                   b.z * rs * (1.f + wv[w][k][6]), b.w * rs * (1.f + wv[w][k][7]));
+            }
+        }
     wave_lds_order();
 }
 
 // After route_wave with bounds, on the same wave: when a decision was ambiguous (R.amb),
 // every candidate whose interval reaches the lowest pick's lower end (the picks among them)
-// gets its reference logit (seq_logit, one lane each), and the K best of those by (l_ref
-// desc, index asc) are the picks: an expert outside that set is below all K current picks
-// in exact arithmetic too.  Equal reference logits give equal p, so the reference's tie
-// rule (lower index) holds; distinct logits whose p round equal are the documented
-// exact-tie class.  The weights stay p / sum p from the device logits.  stage_x(C.x) fills
-// the input row (this wave only); row(e) is router row e.  Returns at once when nothing was
-// ambiguous.
-template <typename StageX, typename Row>
+// gets its reference logit, and the K best of those by (l_ref desc, index asc) are the picks:
+// an expert outside that set is below all K current picks in exact arithmetic too.  Equal
+// reference logits give equal p, so the reference's tie rule (lower index) holds; distinct
+// logits whose p round equal are the documented exact-tie class.  The weights stay p / sum p
+// from the device logits.  stage_x(C.x) fills the input row (this wave only); router row e
+// is rw + e rrb (E rows, f32 or int8).  Returns at once when nothing was ambiguous.
+//
+// The reference logit (c/qwen.c:178-189, int8 :230-238) is the sequential fp32 sum of the
+// rounded products x[i] w[i] in index order, then times the int8 row scale.  The rows go in
+// groups of kCertRows: per chunk of kCertCols columns the wave loads the group's weights
+// (kCertPF chunks ahead, one buffer descriptor over the router matrix), writes the rounded
+// products to LDS (R.cand, free after route_wave) and lane j adds row j's in index order.
+constexpr int kCertRows = 16, kCertCols = 64, kCertPF = 4, kCertPS = kCertCols + 4;
+// The reference logits of S's rows [g0, g0 + ng) (S = sl, ranks into R.cid) into R.clo.  I8:
+// int8 rows (times scales[e] after the sum), else f32; a template parameter so that the
+// loads carry no per-load branch and the prefetched chunks stay in flight.
+template <bool I8>
+__device__ __forceinline__ void cert_group(RouteLds &R, const CertLds &C, const int *sl, int g0, int ng, int D,
+                                           const float *scales, __amdgpu_buffer_rsrc_t rr, int rrb) {
+    const int lane = threadIdx.x & 63;
+    const int cl = 4 * (lane & 15);   // the lane's 4 columns of a chunk; rows 4 q + lane / 16
+    float *P = (float *)R.cand;
+    int base[4];                      // byte offset of the lane's row q, -1 past the group
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int j = 4 * q + (lane >> 4);
+        base[q] = j < ng ? R.cid[sl[g0 + j]] * rrb : -1;
+    }
+    // chunk c0's weights of the lane's 4 rows; columns past D read 0 without memory access
+    auto load_chunk = [&](int c0, float4 (&wv)[4]) {
+        const int col = c0 + cl;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int off = base[q] >= 0 && col < D ? base[q] + (I8 ? col : 4 * col) : (int)0x80000000;
+            if constexpr (I8) {
+                const uint32_t v = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0);
+                wv[q] = make_float4(__int_as_float(v), 0.f, 0.f, 0.f);   // converted at use
+            } else {
+                const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
+                wv[q] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+            }
+        }
+    };
+    // chunk c0 (n columns): the products into P, then lane j < ng adds row j's in order;
+    // `next` (a chunk kCertPF ahead, or past D) is loaded into wv once wv is consumed
+    float acc = 0.f;
+    auto step = [&](float4 (&wv)[4], int c0, int n, bool next) {
+        const float4 xv = *(const float4 *)(C.x + c0 + cl);   // past D: not summed below
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float4 w = wv[q];
+            if constexpr (I8) {
+                const uint32_t v = __float_as_uint(w.x);
+                w = make_float4((float)(int8_t)v, (float)(int8_t)(v >> 8), (float)(int8_t)(v >> 16), (float)(int8_t)(v >> 24));
+            }
+            *(float4 *)(P + (4 * q + (lane >> 4)) * kCertPS + cl) =
+                make_float4(__fmul_rn(xv.x, w.x), __fmul_rn(xv.y, w.y), __fmul_rn(xv.z, w.z), __fmul_rn(xv.w, w.w));
+        }
+        if (next) load_chunk(c0 + kCertPF * kCertCols, wv);
+        wave_lds_order();
+        if (lane < ng) {
+            const float *pr = P + lane * kCertPS;
+            if (n == kCertCols) {   // each half's reads issued before its first add
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float4 p[kCertCols / 8];
+#pragma unroll
+                    for (int i = 0; i < kCertCols / 8; i++) p[i] = *(const float4 *)(pr + h * (kCertCols / 2) + 4 * i);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < kCertCols / 8; i++)
+                        acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, p[i].x), p[i].y), p[i].z), p[i].w);
+                }
+            } else {
+                for (int i = 0; i < n; i++) acc = __fadd_rn(acc, pr[i]);
+            }
+        }
+        wave_lds_order();
+    };
+    static_assert(kCertPF == 4, "four named chunk buffers");
+    float4 w0[4], w1[4], w2[4], w3[4];
+    load_chunk(0, w0);
+    load_chunk(kCertCols, w1);
+    load_chunk(2 * kCertCols, w2);
+    load_chunk(3 * kCertCols, w3);
+    int c0 = 0;
+    for (; c0 + 4 * kCertCols <= D; c0 += 4 * kCertCols) {   // full rounds: no conditions
+        step(w0, c0, kCertCols, true);
+        step(w1, c0 + kCertCols, kCertCols, true);
+        step(w2, c0 + 2 * kCertCols, kCertCols, true);
+        step(w3, c0 + 3 * kCertCols, kCertCols, true);
+    }
+    // the last < 4 chunks are in w0, w1, w2 (wave-uniform conditions)
+    if (c0 < D) step(w0, c0, min(kCertCols, D - c0), false);
+    if (c0 + kCertCols < D) step(w1, c0 + kCertCols, min(kCertCols, D - c0 - kCertCols), false);
+    if (c0 + 2 * kCertCols < D) step(w2, c0 + 2 * kCertCols, min(kCertCols, D - c0 - 2 * kCertCols), false);
+    if (lane < ng) {
+        const int r = sl[g0 + lane];
+        R.clo[r] = I8 ? __fmul_rn(acc, scales[R.cid[r]]) : acc;
+    }
+}
+
+template <typename StageX>
 __device__ __forceinline__ void route_certify_wave(RouteLds &R, CertLds &C, int K, int D, bool int8, const float *scales,
-                                   StageX stage_x, Row row) {
+                                                   const uint8_t *rw, int rrb, int E, StageX stage_x) {
+    static_assert(sizeof(float) * kCertRows * kCertPS <= sizeof(R.cand), "product chunk fits R.cand");
     if (!R.amb) return;
     const int lane = threadIdx.x & 63, nc = R.ncand;
     const float thr = R.thr;
     stage_x(C.x);
+    // S: the ranks r < nc whose interval reaches thr, in rank order, into C.b (free now)
+    int *sl = (int *)C.b;
+    int ns = 0;
+    for (int r0 = 0; r0 < nc; r0 += 64) {
+        const int r = r0 + lane;
+        const bool f = r < nc && R.chi[r] >= thr;
+        const unsigned long long mk = __ballot(f);
+        if (f) sl[ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u))] = r;
+        ns += __popcll(mk);
+    }
     wave_lds_order();
-    for (int r = lane; r < nc; r += 64)   // reference logits over the lower ends
-        if (R.chi[r] >= thr) {
-            const int e = R.cid[r];
-            R.clo[r] = seq_logit(C.x, row(e), int8, D, int8 ? scales[e] : 1.f);
-        }
+    const __amdgpu_buffer_rsrc_t rr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(rw), (short)0, E * rrb, 0x00020000);
+    for (int g0 = 0; g0 < ns; g0 += kCertRows) {
+        const int ng = min(kCertRows, ns - g0);
+        if (int8) cert_group<true>(R, C, sl, g0, ng, D, scales, rr, rrb);
+        else cert_group<false>(R, C, sl, g0, ng, D, scales, rr, rrb);
+    }
     wave_lds_order();
     for (int r = lane; r < nc; r += 64) {
         if (!(R.chi[r] >= thr)) continue;
@@ -531,6 +647,8 @@ __device__ __forceinline__ void route_certify_wave(RouteLds &R, CertLds &C, int 
 }
 
 // the expert table of a layer (moe.hip): false if it is not complete
+// the certification test hook's setting (coli_hip_moe_cert_all)
+int moe_cert_all();
 bool moe_layer(int layer, const ExpertRec **d_rec, const float **d_shgate, MoeGeom *geom, int *E);
 
 }  // namespace coli

@@ -65,10 +65,67 @@ def test_neartie_decode_block(lib, orc, gen, torch_dev, lay, seed):
     assert lib.moe_error() == 0
 
 
-def test_neartie_stream(lib, orc, gen, lay):
+def _decode(lib, torch, dev, rt, x):
+    dx = torch.from_numpy(x).to(dev)
+    out = torch.zeros(D, device=dev)
+    di = torch.full((K,), -1, dtype=torch.int32, device=dev)
+    dv = torch.zeros(K + 1, device=dev)
+    torch.cuda.synchronize()
+    lib.moe_decode_dev(0, rt, K, dx.data_ptr(), out.data_ptr(), False, di.data_ptr(), dv.data_ptr())
+    lib.sync()
+    return out.cpu().numpy(), di.cpu().numpy(), dv.cpu().numpy()
+
+
+@pytest.mark.parametrize("rfmt", [0, 1])
+def test_certify_all_decode_block(lib, orc, gen, torch_dev, lay, rfmt):
+    """Every route certified (coli_hip_moe_cert_all): each top-K candidate's logit recomputed
+    as the reference's sequential sum (two groups of 16 rows at E = 256) and ranked by it.
+    Ids must be the reference's, and the block output, ids and weights bit-identical to the
+    default launch (which certifies only ambiguous routes).  f32 router, and an int8 router
+    with power-of-two scales, whose reference logits equal the f32 sums of q * s exactly."""
+    import torch
+    _moe._active[0] = None
+    lib.eg_table_init(1, E, D, I, GS)
+    lay.register(lib, 0)
+    if rfmt == 0:
+        W = lay.mw.router
+        rt = lay.router
+    else:
+        rt, W = lay.int8_router(lib, gen, 0xB7A0)
+    cases = [gen.normal(D, 0xB7B0 + t) for t in range(4)]
+    xt = gen.normal(D, 0xB7C0)   # plus one near-tie row pair
+    Wt = _neartie.near_tie_router(orc, gen, xt, E, D, K, 0xB7C1) if rfmt == 0 else None
+    prev = lib.moe_cert_all(False)
+    try:
+        for t, x in enumerate(cases + ([xt] if Wt is not None else [])):
+            w, r = (Wt, lib.tensor(Wt, None, 0, D, E)) if t == len(cases) else (W, rt)
+            lib.moe_cert_all(False)
+            o0, i0, v0 = _decode(lib, torch, torch_dev, r, x)
+            lib.moe_cert_all(True)
+            o1, i1, v1 = _decode(lib, torch, torch_dev, r, x)
+            ri, rv = _oracle_route(orc, x, w)
+            assert np.array_equal(i1, ri), (t, i1, ri)
+            assert np.array_equal(i0, i1) and np.array_equal(v0, v1) and np.array_equal(o0, o1), t
+            np.testing.assert_allclose(v1[:K], rv, rtol=1e-5, atol=1e-7)
+    finally:
+        lib.moe_cert_all(prev)
+    assert lib.moe_error() == 0
+
+
+@pytest.mark.parametrize("cert_all", [False, True])
+def test_neartie_stream(lib, orc, gen, lay, cert_all):
     """One GatedDeltaNet layer (position 0) whose post-attention norm feeds the router.  A
     first host-routed pass reads the device's normed row back; the near-tie router is built
-    for that row; the same token then runs host-routed and fused (after gdn_reset)."""
+    for that row; the same token then runs host-routed and fused (after gdn_reset).  With
+    cert_all every route (host-routed route_row and the fused block) is certified."""
+    prev = lib.moe_cert_all(cert_all)
+    try:
+        _neartie_stream(lib, orc, gen, lay)
+    finally:
+        lib.moe_cert_all(prev)
+
+
+def _neartie_stream(lib, orc, gen, lay):
     _layers.bind(orc)
     gdn = dict(KH=2, KD=64, VH=4, VD=32, K=4, gs=128)
     first = 80
