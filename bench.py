@@ -479,8 +479,10 @@ class DecodeStack:
             else:
                 lib.gdn_route_pipe(li, *t, router, n, self.K, self.GKH, self.KD, self.VH, self.VD, self.CD, self.CK,
                                    self.EPS)
-        idx, _ = lib.stream_norm_argmax(self.lm, self.EPS)
+        # the reference engine's order: drain (c/qwen.c:1282), then the device final norm +
+        # lm_head + argmax (:1437-1441)
         lib.stream_end(self.D, read=False)
+        idx, _ = lib.stream_norm_argmax(self.lm, self.EPS)
         return idx
 
     def alg_bytes(self):

@@ -106,6 +106,12 @@ bool moe_ready(int layer);
 // an out-of-range expert id.  moe_error_take reads and clears it (synchronises the device);
 // -1 on a runtime error.
 int moe_error_take();
+// The MoE error words of the current device (NULL where absent), the decision on values read
+// from them once the launches finished (moe_error_take's, without its synchronisation and
+// reads), and the count of launches that can set them.
+void moe_error_words(const unsigned long long **w0, const unsigned long long **w1);
+int moe_error_settle(const unsigned long long v[2]);
+uint64_t moe_launches();
 // Device address of the no-alloc MoE scratch array, looked up once per device with that
 // device current (coli_vk_init).  false: the no-alloc entry point refuses on that device.
 bool moe_noalloc_init(int dev);

@@ -1524,6 +1524,7 @@ struct LayerTags {
     void *tag = nullptr, *err = nullptr;
     size_t cap = 0, ecap = 0;
     uint32_t epoch = 0;
+    uint64_t launches = 0;   // fused launches (they can set the error word)
 };
 static LayerTags g_lt;
 // Off by default: on MI355X the one-launch layer measures slower than the three launches
@@ -1565,6 +1566,7 @@ static bool gdn_fused_launch(GdnState &G, const float *src, const float *ln, Col
         g_lt.epoch = 1;
     }
     const uint32_t ep = g_lt.epoch;
+    g_lt.launches++;
     GdnFusedArgs f;
     memset(&f, 0, sizeof(f));
     int l1, l3;
@@ -1721,7 +1723,11 @@ struct StreamState {
     int fused_last = 0;           // the last route_pipe ran the MoE on the device
     int pending = 0;              // top-k ids of fused layers await stream_end
     int hist_K[kMaxLayers];       // ids recorded per layer in this stream (0 = none)
-    int h_hist[kMaxLayers * kMaxK];
+    struct {                      // stream_end's read-back: the id history, then error words
+        int hist[kMaxLayers * kMaxK];
+        unsigned long long err[3];
+    } rb;
+    uint64_t chk_moe = ~0ull, chk_layer = ~0ull;   // launch counts at the last clean check
     float *h_nrm = nullptr;       // host copy of the last non-fused route's nrm
     size_t hnrm_cap = 0;
 };
@@ -2193,34 +2199,94 @@ COLI_API int coli_vk_stream_begin(const float *x, int D) {
 // A fused MoE launch whose bounded wait gave up (or that met a bad expert id) leaves the
 // residual wrong: like a failed fence wait in the reference (c/backend_vulkan.c:1094-1124,
 // G.ready = 0), that disables the device and the call returns 0, so the engine takes its
-// host path.  The stream must be idle (every caller has synchronised).
-static bool stream_moe_ok(const char *who) {
-    const int le = layer_error_take();
+// host path.  The launches that can fail so (the fused layer kernel, the MoE block in both
+// entry points) leave a code in an error word.  A check is skipped when none of them ran
+// since the last clean one; otherwise err_gather copies the words, stream-ordered after the
+// launches, next to the data the caller reads back anyway, so one copy carries both.
+static void err_mark() {
+    g_str.chk_moe = moe_launches();
+    g_str.chk_layer = g_lt.launches;
+}
+static bool err_clean() { return g_str.chk_moe == moe_launches() && g_str.chk_layer == g_lt.launches; }
+
+__global__ void err_gather(const unsigned long long *l, const unsigned long long *m0, const unsigned long long *m1,
+                           unsigned long long *out) {
+    if (threadIdx.x == 0) {
+        out[0] = l ? __hip_atomic_load(l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        out[1] = m0 ? __hip_atomic_load(m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        out[2] = m1 ? __hip_atomic_load(m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+}
+
+static bool err_gather_launch(unsigned long long *d_out) {
+    const unsigned long long *m0, *m1;
+    moe_error_words(&m0, &m1);
+    hipLaunchKernelGGL(err_gather, dim3(1), dim3(64), 0, stream(), (const unsigned long long *)g_lt.err, m0, m1,
+                       d_out);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess || fail("error word gather", e);
+}
+
+static bool err_report(const char *who, int le, int e) {
     if (le != 0) {
         fprintf(stderr, "[HIP] %s: fused layer kernel reported %s\n", who,
                 le == 1 ? "a bounded wait that gave up" : "a runtime error");
         return fail(who, hipErrorLaunchFailure);
     }
-    const int e = moe_error_take();
-    if (e == 0) return true;
+    if (e == 0) {
+        err_mark();
+        return true;
+    }
     fprintf(stderr, "[HIP] %s: fused MoE reported %s\n", who,
             e == 1 ? "a bounded wait that gave up" : e == 2 ? "an out-of-range expert id" : "a runtime error");
     return fail(who, hipErrorLaunchFailure);
 }
 
+// The check on words gathered by err_gather (v[0] the layer kernel's, v[1..2] the MoE's),
+// read back with the stream idle; the words that hold a failure are cleared.
+static bool stream_err_ok(const char *who, const unsigned long long v[3]) {
+    int le = (int)(uint32_t)v[0];
+    if (le != 0) {
+        const unsigned long long z = 0;
+        if (!g_lt.err || hipMemcpy(g_lt.err, &z, 8, hipMemcpyHostToDevice) != hipSuccess) le = -1;
+    }
+    return err_report(who, le, le != 0 ? 0 : moe_error_settle(v + 1));
+}
+
+// The same check reading the words itself (synchronises the device).
+static bool stream_moe_ok(const char *who) {
+    const int le = layer_error_take();
+    return err_report(who, le, le != 0 ? 0 : moe_error_take());
+}
+
 COLI_API int coli_vk_stream_end(float *x, int D) {
     if (!g_str.live || D != g_str.D) return 0;
+    if (!ok()) {   // disabled by an earlier failure: every later call returns 0
+        g_str.live = 0;
+        g_str.pending = 0;
+        return 0;
+    }
+    // one read-back after the drain: the id history of the fused layers (when pending) and
+    // the error words (when a launch could have set one since the last check)
+    const bool chk = !err_clean();
+    int *dh = hist_dev();   // kMaxLayers * kMaxK ids, then (in the buffer's slack) 3 error words
+    if (!dh) return 0;
+    unsigned long long *d_err = (unsigned long long *)(dh + kMaxLayers * kMaxK);
+    if (chk && !err_gather_launch(d_err)) return 0;
     if (!sync_stream("stream end")) return 0;
-    if (!stream_moe_ok("stream end")) {
+    static_assert(offsetof(decltype(g_str.rb), err) == sizeof(g_str.rb.hist), "history then error words");
+    if (g_str.pending) {
+        if (hipMemcpy(&g_str.rb, dh, chk ? sizeof(g_str.rb) : sizeof(g_str.rb.hist), hipMemcpyDeviceToHost) != hipSuccess)
+            return 0;
+    } else if (chk) {
+        if (hipMemcpy(g_str.rb.err, d_err, sizeof(g_str.rb.err), hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    }
+    if (chk && !stream_err_ok("stream end", g_str.rb.err)) {
         g_str.live = 0;
         g_str.pending = 0;
         return 0;
     }
     if (x && hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    if (g_str.pending) {
-        int *dh = hist_dev();
-        if (!dh || hipMemcpy(g_str.h_hist, dh, sizeof(g_str.h_hist), hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    }
     g_str.live = 0;
     return 1;
 }
@@ -2247,7 +2313,7 @@ COLI_API const float *coli_vk_stream_nrm(void) { return g_str.live && !g_str.fus
 
 COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
     if (!ok() || !x || !g_str.d_resid || D != g_str.D || D < 1) return 0;
-    if (!sync_stream("copy resid") || !stream_moe_ok("copy resid")) return 0;
+    if (!sync_stream("copy resid") || (!err_clean() && !stream_moe_ok("copy resid"))) return 0;
     return hipMemcpy(x, g_str.d_resid, (size_t)D * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
 }
 
@@ -2266,16 +2332,25 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
                                         int I, int O, int gs, float eps, int *idx, float *val) {
     if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
     if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
-    if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, (size_t)I * 4 + 64)) return 0;
+    // xn [I] | result: 16 ints (idx at 0, value bits at 8) | 3 error words (8-aligned)
+    const size_t roff = ((size_t)I * 4 + 7) & ~(size_t)7;
+    if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, roff + 64 + 24)) return 0;
     float *xn = g_str.d_xn;
-    int *d_iv = (int *)(xn + I);
+    int *d_iv = (int *)((uint8_t *)xn + roff);
+    unsigned long long *d_err = (unsigned long long *)(d_iv + 16);
     if (!rmsnorm_zc(g_str.d_resid, g_str.d_fnw, xn, I, eps, stream())) return 0;
     TopkOut tk = {1, d_iv, (float *)(d_iv + 8)};
     if (!gemv(*tensor, xn, nullptr, 1, stream(), &tk)) return 0;
-    int res[16];
-    if (!sync_stream("stream_norm_argmax") || hipMemcpy(res, d_iv, 64, hipMemcpyDeviceToHost) != hipSuccess)
+    const bool chk = !err_clean();
+    if (chk && !err_gather_launch(d_err)) return 0;
+    struct {
+        int res[16];
+        unsigned long long err[3];
+    } hb;
+    if (!sync_stream("stream_norm_argmax") || hipMemcpy(&hb, d_iv, chk ? sizeof(hb) : 64, hipMemcpyDeviceToHost) != hipSuccess)
         return 0;
-    if (!stream_moe_ok("stream_norm_argmax")) return 0;
+    if (chk && !stream_err_ok("stream_norm_argmax", hb.err)) return 0;
+    const int *res = hb.res;
     if (res[0] < 0 || res[0] >= O) return 0;   // no valid winner: the engine's host scan decides
     *idx = res[0];
     if (val) memcpy(val, &res[8], 4);
@@ -2354,7 +2429,7 @@ COLI_API int coli_vk_stream_ix_pending(void) { return g_str.pending ? 1 : 0; }
 COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
     if (!g_str.pending || g_str.live || layer < 0 || layer >= kMaxLayers || !idx_out) return 0;
     const int n = g_str.hist_K[layer] < K ? g_str.hist_K[layer] : K;
-    for (int k = 0; k < n; k++) idx_out[k] = g_str.h_hist[layer * kMaxK + k];
+    for (int k = 0; k < n; k++) idx_out[k] = g_str.rb.hist[layer * kMaxK + k];
     return n;
 }
 

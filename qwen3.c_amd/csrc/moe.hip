@@ -605,6 +605,11 @@ struct EgTable {
 };
 static EgTable g_eg;
 
+// launches that can set an error word (both entry points), for the callers that skip a
+// check when none ran since the last one
+static uint64_t g_moe_launches = 0;
+uint64_t moe_launches() { return g_moe_launches; }
+
 struct MoeScratch {
     void *tag = nullptr;
     size_t tag_cap = 0;
@@ -754,6 +759,7 @@ bool moe_decode(int layer, const ColiVkTensor *router, int K, const float *d_x, 
     a.tagv = (unsigned long long *)g_ms.tag;
     a.err = (unsigned long long *)((uint8_t *)g_ms.misc + 64);
     a.epoch = next_epoch(&g_ms.epoch, a.tagv, g_ms.tag_cap / 8, a.err, st);
+    g_moe_launches++;
     return dispatch_shape<LaunchMoe>(a.g, a, st) || (ok() && reject("expert shape not compiled"));
 }
 
@@ -837,33 +843,48 @@ static bool moe_decode_noalloc(int layer, const ColiVkTensor *router, int K, con
     a.err = n.ptr;
     a.tagv = n.ptr + kErrWords;
     a.epoch = next_epoch(&n.epoch, a.tagv, kTagWords, a.err, st);
+    g_moe_launches++;
     return dispatch_shape<LaunchMoe>(a.g, a, st) || (ok() && reject("expert shape not compiled"));
 }
 
 // The failure code a word holds (its low 32 bits), or 0.
 static int err_code(unsigned long long w) { return (int)(uint32_t)w; }
 
+// The error words of the current device: the scratch launches' and the no-alloc launches'
+// (NULL where not allocated).
+void moe_error_words(const unsigned long long **w0, const unsigned long long **w1) {
+    *w0 = g_ms.misc ? (const unsigned long long *)((uint8_t *)g_ms.misc + 64) : nullptr;
+    *w1 = nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) *w1 = g_na[dev].ptr;
+}
+
+// The code of the words' values v[0..1] (read with the launches finished): the first failure,
+// each word that holds one cleared; -1 on a runtime error.
+int moe_error_settle(const unsigned long long v[2]) {
+    const unsigned long long *w[2];
+    moe_error_words(&w[0], &w[1]);
+    int code = 0;
+    for (int i = 0; i < 2; i++) {
+        if (!w[i] || !err_code(v[i])) continue;
+        if (!code) code = err_code(v[i]);
+        const unsigned long long z = 0;
+        if (hipMemcpy(const_cast<unsigned long long *>(w[i]), &z, 8, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return code;
+}
+
 // 0 = no error since the last call; 1 = a poll gave up; 2 = a route held a bad expert id.
 // Covers the scratch launches and the no-alloc launches of the current device.
 int moe_error_take() {
-    unsigned long long *words[2] = {g_ms.misc ? (unsigned long long *)((uint8_t *)g_ms.misc + 64) : nullptr,
-                                    nullptr};
-    int dev = -1;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) words[1] = g_na[dev].ptr;
-    if (!words[0] && !words[1]) return 0;
+    const unsigned long long *w[2];
+    moe_error_words(&w[0], &w[1]);
+    if (!w[0] && !w[1]) return 0;
     if (hipDeviceSynchronize() != hipSuccess) return -1;
-    int code = 0;
-    for (unsigned long long *w : words) {
-        if (!w) continue;
-        unsigned long long v = 0;
-        if (hipMemcpy(&v, w, 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
-        if (err_code(v)) {
-            if (!code) code = err_code(v);
-            const unsigned long long z = 0;
-            if (hipMemcpy(w, &z, 8, hipMemcpyHostToDevice) != hipSuccess) return -1;
-        }
-    }
-    return code;
+    unsigned long long v[2] = {0, 0};
+    for (int i = 0; i < 2; i++)
+        if (w[i] && hipMemcpy(&v[i], w[i], 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return moe_error_settle(v);
 }
 
 // Host-forced failure for tests: the error word is stamped with the next scratch launch's

@@ -40,8 +40,13 @@ def _child(body, env=None, timeout=240):
     return r.stdout
 
 
-def test_moe_give_up_disables_stream():
+@pytest.mark.parametrize("argmax_first", [False, True])
+def test_moe_give_up_disables_stream(argmax_first):
+    """The engine's order (stream_end, then stream_norm_argmax) and the reverse: whichever
+    call reads back first after the failing launches reports it (the error words ride on its
+    read-back), and every later call returns 0."""
     out = _child("""
+        argmax_first = %r
         import _stack, _layers
         from _moe import Layer
         L = Layer(lib, gen, 0xF100, 256, 128, 32, 64)
@@ -66,16 +71,20 @@ def test_moe_give_up_disables_stream():
         for i in range(4):
             st.pipe_layer(lib, i, 1, 8, L.router)
         import ctypes as C
-        r_end = lib.L.coli_vk_stream_end(None, 256)
         i2, v2 = C.c_int(-7), C.c_float()
-        r_arg = lib.L.coli_vk_stream_norm_argmax(lm.ref, None, None, 6, 256, 512, 64, 1e-6, C.byref(i2), C.byref(v2))
+        if argmax_first:
+            r_arg = lib.L.coli_vk_stream_norm_argmax(lm.ref, None, None, 6, 256, 512, 64, 1e-6, C.byref(i2), C.byref(v2))
+            r_end = lib.L.coli_vk_stream_end(None, 256)
+        else:
+            r_end = lib.L.coli_vk_stream_end(None, 256)
+            r_arg = lib.L.coli_vk_stream_norm_argmax(lm.ref, None, None, 6, 256, 512, 64, 1e-6, C.byref(i2), C.byref(v2))
         x = np.empty(256, np.float32)
         r_cp = lib.L.coli_vk_stream_copy_resid(_util.P(x), 256)
         print("results", r_end, r_arg, r_cp, i2.value, lib.available(), flush=True)
         assert r_end == 0 and r_arg == 0 and r_cp == 0 and i2.value == -7
         assert not lib.available()
         print("ok", flush=True)
-    """)
+    """ % argmax_first)
     assert "ok" in out
 
 
