@@ -812,17 +812,24 @@ struct RowLd {
     static constexpr int kPer = kAttMaxHD / 64, kPairs = (kAttMaxHR + 63) / 64;
     float v[kPer], wv[kPer], lo[kPairs], hi[kPairs], wl[kPairs], wh[kPairs], cs[kPairs], sn[kPairs];
 };
-__device__ __forceinline__ void row_load(RowLd &R, const float *src, const float *w, const AttnArgs &a) {
+// NQ: the 64-column slots to load (hd / 64, known to the caller at compile time; the others
+// read as 0).  live = false: every load reads 0 without a memory access.  No branch sits
+// around a load, so the compiler's wait counts stay exact and nothing waits early.
+template <int NQ = RowLd::kPer>
+__device__ __forceinline__ void row_load(RowLd &R, const float *src, const float *w, const AttnArgs &a,
+                                         bool live = true) {
+    static_assert(NQ >= 1 && NQ <= RowLd::kPer, "slots");
     const int lane = threadIdx.x & 63, hd = a.hd, hr = a.rot / 2;
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, (uint32_t)hd * 4), rw = buf_rsrc(w, (uint32_t)hd * 4);
+    const uint32_t nb = live ? (uint32_t)hd * 4 : 0u;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, nb), rw = buf_rsrc(w, nb);
     auto ld = [](__amdgpu_buffer_rsrc_t r, bool on, int i) {   // unconditional: out of range reads 0
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, on ? i * 4 : (int)kOOB, 0, 0));
     };
 #pragma unroll
     for (int q = 0; q < RowLd::kPer; q++) {
         const int d = lane + 64 * q;
-        R.v[q] = ld(rs, d < hd, d);
-        R.wv[q] = ld(rw, d < hd, d);
+        R.v[q] = q < NQ ? ld(rs, d < hd, d) : 0.f;
+        R.wv[q] = q < NQ ? ld(rw, d < hd, d) : 0.f;
     }
 #pragma unroll
     for (int p = 0; p < RowLd::kPairs; p++) {
@@ -870,16 +877,18 @@ __device__ __forceinline__ void row_finish(float *x, float *gdst, const RowLd &R
         }
     }
 }
+template <int NQ = RowLd::kPer>
 __device__ __forceinline__ void norm_rope_row(float *x, float *gdst, const float *src, const float *w, const AttnArgs &a) {
     RowLd R;
-    row_load(R, src, w, a);
+    row_load<NQ>(R, src, w, a);
     row_finish(x, gdst, R, a);
 }
 
-// One block per (kv head, chunk of kAttT positions).  Every K and V element the block
-// needs is loaded at the start (one memory round trip), then the q rows of the group (and
-// the new key row, in the chunk holding pos) are normed and rotated, scores computed,
-// the chunk softmax taken and P.V accumulated.
+// One block per (kv head, chunk of kAttT positions).  The q rows of the group (and the new
+// key row, in the chunk holding pos) are loaded first, then every K and V element the block
+// needs (one memory round trip); the q rows are normed and rotated while
+// K and V arrive, scores computed, the chunk softmax taken and P.V accumulated.  The block
+// barriers are LDS-only, so no phase waits for loads it does not use.
 template <int DPL, int AW>
 __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
     constexpr int kT = 64 * AW;                 // threads of the block (AW waves)
@@ -889,8 +898,9 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float s_q[kAttMaxG][kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_k[kAttMaxHD];
     __shared__ __attribute__((aligned(16))) float s_p[kAttMaxG][kAttT];
+    __shared__ __attribute__((aligned(16))) float s_v[kAttT][kAttMaxHD];
     __shared__ float s_m[kAttMaxG], s_l[kAttMaxG];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.H / a.KH, hd = a.hd;
     const int kh = blockIdx.x / a.nsplit, sp = blockIdx.x % a.nsplit;
     const int t0 = sp * kAttT, t1 = min(t0 + kAttT, a.pos + 1), n = t1 - t0;
@@ -899,6 +909,16 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
     // P.V (thread pvt: dims pvt + kPV * i), all in flight together
     // (branch-free buffer loads: out-of-range offsets read 0, so no load waits behind a
     // data-dependent branch)
+    // the wave's first q row and, in the chunk holding pos, the new key row: their loads go
+    // out first (the norms need them first; no branch: absent rows read 0 without memory
+    // access); rows past one per wave follow one by one.  A wave keeps under the 63 loads
+    // the wait counter tracks, or issue stalls until the first ones return.
+    const int g0 = wave;
+    const bool own_k = owns_pos && wave == AW - 1;
+    RowLd r0, rkr;
+    constexpr int NQ = DPL / 4;   // hd = 16 DPL
+    row_load<NQ>(r0, a.q + (size_t)(kh * G + min(g0, G - 1)) * 2 * hd, a.qn, a, g0 < G);
+    row_load<NQ>(rkr, a.k + (size_t)kh * hd, a.kn, a, own_k);
     const int pl = lane >> 4, part = lane & 15;
     const uint32_t cache_b = (uint32_t)a.max_t * (uint32_t)hd * 4u;
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.Kc + (size_t)kh * a.max_t * hd, cache_b);
@@ -919,44 +939,31 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
             kv[st][e + 3] = __int_as_float(v4.w);
         }
     }
-    // V: the cached rows, and this token's v for the position pos (selected below); dims
-    // slots past hd are skipped uniformly
-    const int pvt = tid % kPV, half = tid / kPV;   // P.V: dims of thread pvt, heads of half
-    float vv[kAttT][kVPer];
+    // V: the chunk's cached rows (this token's v for the position pos) as 16-byte loads,
+    // written to LDS once the scores are done; P.V reads them from there
+    constexpr int kV4 = kAttT * kAttMaxHD / 4 / kT;   // float4 slots per thread (kT % (hd / 4) == 0:
+    const int hd4 = hd / 4;                             // a thread's dims are the same in every slot)
+    const __amdgpu_buffer_rsrc_t rnv = buf_rsrc(a.v + (size_t)kh * hd, (uint32_t)hd * 4u);
+    const int c4 = tid % hd4;
+    const coli_v4i nv = __builtin_amdgcn_raw_buffer_load_b128(rnv, owns_pos ? 16 * c4 : (int)kOOB, 0, 0);
+    float4 vq[kV4];
 #pragma unroll
-    for (int i = 0; i < kVPer; i++) {
-        if (i > 0 && i * kPV >= hd) continue;   // uniform; a guarded body keeps the unroll
-        const int d = pvt + i * kPV;
-        const float nv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                       rn, owns_pos && d < hd ? d * 4 : (int)kOOB, 0, 0));
-#pragma unroll
-        for (int t = 0; t < kAttT; t++) {
-            const int tt = t0 + t;
-            const bool on = t < n && d < hd && tt != a.pos;
-            const float c = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                          rv, on ? (tt * hd + d) * 4 : (int)kOOB, 0, 0));
-            vv[t][i] = tt == a.pos ? nv : c;
-        }
+    for (int j = 0; j < kV4; j++) {
+        if (j > 0 && j * kT >= kAttT * hd4) continue;   // uniform; a guarded body keeps the unroll
+        const int t = (tid + j * kT) / hd4, tt = t0 + t;
+        const int off = t < n && tt != a.pos ? (tt * hd + 4 * c4) * 4 : (int)kOOB;
+        const coli_v4i c = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);   // pos: selected at the LDS write
+        vq[j] = make_float4(__int_as_float(c.x), __int_as_float(c.y), __int_as_float(c.z), __int_as_float(c.w));
     }
-    {   // the wave's first two q rows and, in the chunk holding pos, the new key row: all
-        // their loads first, then the norms (rows past two per wave follow one by one)
-        const int g0 = wave, g1 = wave + AW;
-        const bool own_k = owns_pos && wave == AW - 1;
-        RowLd r0, r1, rk;
-        if (g0 < G) row_load(r0, a.q + (size_t)(kh * G + g0) * 2 * hd, a.qn, a);
-        if (g1 < G) row_load(r1, a.q + (size_t)(kh * G + g1) * 2 * hd, a.qn, a);
-        if (own_k) row_load(rk, a.k + (size_t)kh * hd, a.kn, a);
-        if (g0 < G) row_finish(s_q[g0], nullptr, r0, a);
-        if (g1 < G) row_finish(s_q[g1], nullptr, r1, a);
-        for (int gg = wave + 2 * AW; gg < G; gg += AW)
-            norm_rope_row(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
-        if (own_k) {   // the new key row and value row (c/qwen.c:605-614)
-            const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
-            row_finish(s_k, a.Kc + row, rk, a);
-            for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
-        }
+    if (g0 < G) row_finish(s_q[g0], nullptr, r0, a);
+    for (int gg = wave + AW; gg < G; gg += AW)
+        norm_rope_row<NQ>(s_q[gg], nullptr, a.q + (size_t)(kh * G + gg) * 2 * hd, a.qn, a);
+    if (own_k) {   // the new key row and value row (c/qwen.c:605-614)
+        const size_t row = ((size_t)kh * a.max_t + a.pos) * hd;
+        row_finish(s_k, a.Kc + row, rkr, a);
+        for (int d = lane; d < hd; d += 64) a.Vc[row + d] = a.v[(size_t)kh * hd + d];
     }
-    __syncthreads();
+    lds_barrier();
     // scores: 16 lanes per position, 4 positions per wave step; each q fragment is read
     // from LDS once for all the wave's steps
 #pragma unroll
@@ -986,7 +993,7 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
             if (part == 15 && t < t1) s_p[gg][t - t0] = sc * a.scale;
         }
     }
-    __syncthreads();
+    lds_barrier();
     // chunk max and sum of exp per head: 32 lanes per head, lane = position; positions past
     // the chunk get p = 0
     static_assert(kAttT == 32, "one position per lane of a half wave");
@@ -1006,23 +1013,35 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
             s_l[gg] = l;
         }
     }
-    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kV4; j++) {
+        if (j > 0 && j * kT >= kAttT * hd4) continue;
+        const int t = (tid + j * kT) / hd4;
+        *(float4 *)&s_v[t][4 * c4] = t0 + t == a.pos ? make_float4(__int_as_float(nv.x), __int_as_float(nv.y),
+                                                                     __int_as_float(nv.z), __int_as_float(nv.w))
+                                                      : vq[j];
+    }
+    lds_barrier();
     // P.V: thread pvt of the head dims; with two halves, half h takes heads h G / 2 ..
+    const int pvt = tid % kPV, half = tid / kPV;
     float *pb = a.part + ((size_t)kh * a.nsplit + sp) * G * (hd + 2);
     const int nh = kT > kPV ? (G + 1) / 2 : G, g_lo = half * nh, g_hi = min(G, g_lo + nh);
 #pragma unroll
     for (int i = 0; i < kVPer; i++) {   // guarded bodies, no breaks: the loops unroll fully
         const int d = pvt + i * kPV;
         if (i * kPV >= hd) continue;   // uniform
+        float vv[kAttT];
+#pragma unroll
+        for (int t = 0; t < kAttT; t++) vv[t] = d < hd ? s_v[t][d] : 0.f;
         for (int gg = g_lo; gg < g_hi; gg++) {   // p as float4 broadcasts, positions in order
             float acc = 0.f;
 #pragma unroll
             for (int t4 = 0; t4 < kAttT; t4 += 4) {
                 const float4 p = *(const float4 *)&s_p[gg][t4];
-                acc = fmaf(p.x, vv[t4][i], acc);
-                acc = fmaf(p.y, vv[t4 + 1][i], acc);
-                acc = fmaf(p.z, vv[t4 + 2][i], acc);
-                acc = fmaf(p.w, vv[t4 + 3][i], acc);
+                acc = fmaf(p.x, vv[t4], acc);
+                acc = fmaf(p.y, vv[t4 + 1], acc);
+                acc = fmaf(p.z, vv[t4 + 2], acc);
+                acc = fmaf(p.w, vv[t4 + 3], acc);
             }
             if (d < hd) pb[(size_t)gg * (hd + 2) + d] = acc;
         }
