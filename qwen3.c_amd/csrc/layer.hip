@@ -245,6 +245,8 @@ __device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XP
     const int gbase = bid * kWaves + wave;
     uint4 wq[U][kLaneChunks];
     float2 sv[U][LaneX<CU>::NU];
+    float yo[U];   // a.add: the output row's old value, loaded with the step's weights (a load
+                   // issued after the dot would wait for every prefetched weight load)
     auto load = [&](int u, int g) {   // unconditional: out-of-range offsets past the last group
         const bool on = g < a.ngroups;
         const SegSel s = seg_of(a, on ? g : a.ngroups - 1);
@@ -252,6 +254,10 @@ __device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XP
         const uint32_t wtot = (uint32_t)s.O * (uint32_t)a.row_bytes, stot = (uint32_t)s.O * srb;
         lane_load<CU>(buf_rsrc(s.w, wtot), buf_rsrc(s.sz, stot), on ? min(r * (uint32_t)a.row_bytes, wtot) : kOOB,
                       on ? min(r * srb, stot) : kOOB, L, wq[u], sv[u]);
+        if constexpr (!kTagOut)
+            yo[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  buf_rsrc(s.y, (uint32_t)s.O * 4u),
+                                                  on && a.add && j == LPR - 1 && r < (uint32_t)s.O ? r * 4 : kOOB, 0, 0));
     };
 #pragma unroll
     for (int u = 0; u < U; u++) load(u, gbase + u * nw);
@@ -296,6 +302,8 @@ __device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XP
             const int g = g0 + u * nw;
             if (g >= a.ngroups) break;
             const float part = lane_row<CU>(wq[u], sv[u], L);
+            float old = 0.f;
+            if constexpr (!kTagOut) old = yo[u];
             load(u, g + nw * U);
             const float acc = seg_sum<LPR>(part);
             const SegSel s = seg_of(a, g);
@@ -304,10 +312,7 @@ __device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XP
                 if constexpr (kTagOut) {
                     tag_put(&s.yt[r], a.epoch, acc);
                 } else {
-                    if (a.add)
-                        s.y[r] += acc;
-                    else
-                        s.y[r] = acc;
+                    s.y[r] = a.add ? old + acc : acc;
                 }
             }
         }
@@ -393,50 +398,19 @@ __device__ __forceinline__ void gdn_core_body(const GdnArgs &g, int bid) {
         for (int e = 0; e < KPL; e++) sv[q][e] = col[e];
     }
 
-    // decay / beta (c/qwen.c:722-728): host params, or a/b over in_ln(resid) here
-    float decay, beta;
-    if (kTag) {   // from the a/b dots, polled with the conv inputs below
-        decay = beta = 0.f;
-    } else if (g.params) {
-        decay = g.params[h];
-        beta = g.params[g.VH + h];
-    } else if (g.ab) {   // fmt 6 a/b: projected with qkv/z in one launch
-        const float sp_in = g.ab[h] + g.dtb[h];
-        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
-        decay = expf(-expf(g.alog[h]) * sp);
-        beta = 1.f / (1.f + expf(-g.ab[g.VH + h]));
-    } else {
-        float r = 0.f;
-        if (!g.xin) {
-            double ss = 0;
-            for (int i = tid; i < g.D; i += kThreads) ss += (double)g.resid[i] * g.resid[i];
-            ss = block_sum_d(ss, s_red);
-            r = 1.f / sqrtf((float)(ss / g.D) + g.eps);
-        }
-        float da = 0.f, db = 0.f;
-        for (int i = tid; i < g.D; i += kThreads) {
-            const float xv = g.xin ? g.xin[i] : g.resid[i] * r * (1.f + g.in_ln[i]);
-            da = fmaf(rowmat_w(g.a, h, i), xv, da);
-            db = fmaf(rowmat_w(g.b, h, i), xv, db);
-        }
-        da = wave_sum_f(da);
-        db = wave_sum_f(db);
-        if (lane == 0) {
-            s_ab[0][wave] = da;
-            s_ab[1][wave] = db;
-        }
-        __syncthreads();
-        float ta = 0.f, tb = 0.f;
-        for (int w = 0; w < kWaves; w++) {
-            ta += s_ab[0][w];
-            tb += s_ab[1][w];
-        }
-        if (g.a.fmt == 1) ta *= g.a.sz[h];
-        if (g.b.fmt == 1) tb *= g.b.sz[h];
-        const float sp_in = ta + g.dtb[h];
-        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
-        decay = expf(-expf(g.alog[h]) * sp);
-        beta = 1.f / (1.f + expf(-tb));
+    // the a/b dots and their parameters (c/qwen.c:722-728) load with the state; decay and
+    // beta are computed after the conv, whose loads then go out without waiting for these
+    float decay = 0.f, beta = 0.f;
+    const bool abp = !kTag && !g.params && g.ab;
+    float pa, pb, pdtb, palog;
+    {
+        const uint32_t nab = abp ? (uint32_t)g.VH * 8u : 0u, np = abp || kTag ? (uint32_t)g.VH * 4u : 0u;
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(abp ? g.ab : g.dtb, nab), rd = buf_rsrc(g.dtb, np),
+                                     rl = buf_rsrc(g.alog, np);
+        pa = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, h * 4, 0, 0));
+        pb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, (g.VH + h) * 4, 0, 0));
+        pdtb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, h * 4, 0, 0));
+        palog = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, h * 4, 0, 0));
     }
 
     // conv1d + SiLU of the channels this block reads (c/qwen.c:697-707): q and k of the
@@ -489,9 +463,9 @@ __device__ __forceinline__ void gdn_core_body(const GdnArgs &g, int bid) {
                 }
                 if (all || poll_give_up(g.err, g.epoch, polls)) break;
             }
-            const float sp_in = av + g.dtb[h];
+            const float sp_in = av + pdtb;
             const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
-            decay = expf(-expf(g.alog[h]) * sp);
+            decay = expf(-expf(palog) * sp);
             beta = 1.f / (1.f + expf(-bv));
         }
 #pragma unroll
@@ -530,6 +504,51 @@ __device__ __forceinline__ void gdn_core_body(const GdnArgs &g, int bid) {
         if (t >= 2 * KD || owns_qk) g.ring[(size_t)g.head * g.CD + ch] = xn;
     }
     __syncthreads();
+    // decay / beta (c/qwen.c:722-728): host params, the a/b dots of the projection launch, or
+    // a/b over in_ln(resid) here (the fused kernel's came with the conv inputs)
+    if (kTag) {
+    } else if (g.params) {
+        decay = g.params[h];
+        beta = g.params[g.VH + h];
+    } else if (g.ab) {   // fmt 6 a/b: projected with qkv/z in one launch
+        const float sp_in = pa + pdtb;
+        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
+        decay = expf(-expf(palog) * sp);
+        beta = 1.f / (1.f + expf(-pb));
+    } else {
+        float r = 0.f;
+        if (!g.xin) {
+            double ss = 0;
+            for (int i = tid; i < g.D; i += kThreads) ss += (double)g.resid[i] * g.resid[i];
+            ss = block_sum_d(ss, s_red);
+            r = 1.f / sqrtf((float)(ss / g.D) + g.eps);
+        }
+        float da = 0.f, db = 0.f;
+        for (int i = tid; i < g.D; i += kThreads) {
+            const float xv = g.xin ? g.xin[i] : g.resid[i] * r * (1.f + g.in_ln[i]);
+            da = fmaf(rowmat_w(g.a, h, i), xv, da);
+            db = fmaf(rowmat_w(g.b, h, i), xv, db);
+        }
+        da = wave_sum_f(da);
+        db = wave_sum_f(db);
+        if (lane == 0) {
+            s_ab[0][wave] = da;
+            s_ab[1][wave] = db;
+        }
+        __syncthreads();
+        float ta = 0.f, tb = 0.f;
+        for (int w = 0; w < kWaves; w++) {
+            ta += s_ab[0][w];
+            tb += s_ab[1][w];
+        }
+        if (g.a.fmt == 1) ta *= g.a.sz[h];
+        if (g.b.fmt == 1) tb *= g.b.sz[h];
+        const float sp_in = ta + g.dtb[h];
+        const float sp = sp_in > 20.f ? sp_in : log1pf(expf(sp_in));
+        decay = expf(-expf(g.alog[h]) * sp);
+        beta = 1.f / (1.f + expf(-tb));
+    }
+
     // l2norm of q and k (c/qwen.c:713-721)
     float sq = 0.f, sk = 0.f;
     if (wave == 0) {
