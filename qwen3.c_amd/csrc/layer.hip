@@ -1186,7 +1186,7 @@ __global__ void rms_rows(const float *__restrict__ x, const float *__restrict__ 
 __global__ __launch_bounds__(kThreads) void router_lb(const float *__restrict__ x, const uint8_t *__restrict__ rw,
                                                       const float *__restrict__ rs, int rfmt, int rrb, int E, int D,
                                                       float *__restrict__ lg, float *__restrict__ bd) {
-    const int lane = threadIdx.x & 63, r = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (r >= E) return;   // wave uniform
     const bool int8 = rfmt == 1;
     const __amdgpu_buffer_rsrc_t rr = buf_rsrc(rw + (size_t)r * rrb, int8 ? (uint32_t)D : (uint32_t)D * 4u);

@@ -263,10 +263,6 @@ __device__ __forceinline__ float4 int8x4(uint32_t q) {
     return make_float4((float)(int8_t)q, (float)(int8_t)(q >> 8), (float)(int8_t)(q >> 16), (float)(int8_t)(q >> 24));
 }
 
-// The router's input row into LDS (all threads; ends with a barrier): x itself, or with a
-// norm weight the zero-centred RMSNorm of x (c/qwen.c:326-330: double sum of squares,
-// x r (1 + w) in the reference's order).  Router and route tiles run this same code, so
-// they see the same row bit for bit.
 // The normed input row into LDS (xn[0, D)) from x and the norm weights as loaded by prep_load
 // (issued before any other load of the tile, so only these are waited for): norm_apply,
 // the G tiles' staging, so the router's input and the experts' are the same bits.
