@@ -1768,6 +1768,8 @@ struct StreamState {
     uint64_t chk_moe = ~0ull, chk_layer = ~0ull;   // launch counts at the last clean check
     float *h_nrm = nullptr;       // host copy of the last non-fused route's nrm
     size_t hnrm_cap = 0;
+    float *h_x = nullptr;         // pinned staging of stream_begin's row (copied without a sync)
+    size_t hx_cap = 0;
 };
 static StreamState g_str;
 
@@ -2224,8 +2226,16 @@ static int *hist_dev() { return (int *)wbuf(W_HIST, (size_t)kMaxLayers * kMaxK);
 
 COLI_API int coli_vk_stream_begin(const float *x, int D) {
     if (!ok() || !x || D < 1) return 0;
-    if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4)) return 0;
-    if (!h2d(g_str.d_resid, x, (size_t)D * 4, "stream begin")) return 0;
+    // the row goes through pinned staging with an async copy: the token's first launches
+    // queue behind it at once.  The staging is rewritten only with the stream idle (a live
+    // stream is drained first; a finished token was drained by its read-backs).
+    if (g_str.live && !sync_stream("stream begin")) return 0;
+    if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4) ||
+        !host_scratch((void **)&g_str.h_x, &g_str.hx_cap, (size_t)D * 4))
+        return 0;
+    memcpy(g_str.h_x, x, (size_t)D * 4);
+    const hipError_t e = hipMemcpyAsync(g_str.d_resid, g_str.h_x, (size_t)D * 4, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("stream begin", e) ? 1 : 0;
     g_str.D = D;
     g_str.live = 1;
     g_str.pending = 0;
