@@ -1074,43 +1074,60 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
 constexpr int kAttMaxSplit = 4096;
 
 // One block per query head: merges the chunks (max, rescaled sums) and applies the
-// sigmoid gate.  Wave w takes chunks w, w + 4, ...; lane l takes dims 4 l .. 4 l + 3 (and
-// + 256 for hd = 512); the 4 wave partials are summed in LDS in wave order.
-__global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
+// sigmoid gate.  kMW waves; wave w takes chunks w, w + kMW, ...; lane l takes dims
+// 4 l .. 4 l + 3 (and + 256 for hd = 512); the wave partials are summed in LDS in wave order.
+// Each chunk's (m, l) and the context rows of a wave's first kMPre chunks are loaded together
+// (one memory round trip: the rows do not depend on the max), as branch-free buffer loads.
+constexpr int kMW = 8, kMT = 64 * kMW, kMPre = 16;
+__global__ __launch_bounds__(kMT) void attn_merge(AttnArgs a) {
     __shared__ float s_w[kAttMaxSplit];
-    __shared__ float s_red[kWaves];
-    __shared__ __attribute__((aligned(16))) float s_acc[kWaves][kAttMaxHD];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ float s_red[kMW];
+    __shared__ __attribute__((aligned(16))) float s_acc[kMW][kAttMaxHD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = blockIdx.x, G = a.H / a.KH, kh = h / G, gg = h % G, hd = a.hd;
     const int ns = (a.pos + 1 + kAttT - 1) / kAttT;
     const float *pb = a.part + ((size_t)kh * a.nsplit) * G * (hd + 2) + (size_t)gg * (hd + 2);
     const size_t stride = (size_t)G * (hd + 2);
-    // the gate row of the output first (read at the very end), then each chunk's (m, l):
-    // with ns <= kThreads one chunk per thread, kept in registers for the weights
-    constexpr int kGPer = kAttMaxHD / kThreads;
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(pb, (uint32_t)(((size_t)(ns - 1) * stride + hd + 2) * 4));
+    auto ldp = [&](size_t i, bool on) {   // float i of the partials (0 without memory access when !on)
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, on ? (int)(i * 4) : (int)kOOB, 0, 0));
+    };
+    // the gate row of the output, each chunk's (m, l) (ns <= kMT: one chunk per thread, kept
+    // in registers for the weights) and the first kMPre chunk rows of the wave's first dims
+    constexpr int kGPer = (kAttMaxHD + kMT - 1) / kMT;
     const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.q + (size_t)h * 2 * hd + hd, (uint32_t)hd * 4u);
     float gv[kGPer];
 #pragma unroll
     for (int i = 0; i < kGPer; i++) {
-        const int d = tid + i * kThreads;
+        const int d = tid + i * kMT;
         gv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, d < hd ? d * 4 : (int)kOOB, 0, 0));
     }
-    const bool one = ns <= kThreads;
-    float m = -INFINITY, mv = -INFINITY, lv = 0.f;
-    if (one) {
-        if (tid < ns) {
-            mv = pb[tid * stride + hd];
-            lv = pb[tid * stride + hd + 1];
+    const bool one = ns <= kMT;
+    const float mv = ldp((size_t)tid * stride + hd, one && tid < ns);
+    const float lv = ldp((size_t)tid * stride + hd + 1, one && tid < ns);
+    float4 pre[kMPre];
+    {
+        const int d0 = lane * 4;
+#pragma unroll
+        for (int u = 0; u < kMPre; u++) {
+            const int s = wave + u * kMW;
+            const bool on = s < ns && d0 < hd;
+            const uint32_t o = on ? (uint32_t)(((size_t)s * stride + d0) * 4) : kOOB;
+            const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)o, 0, 0);
+            pre[u] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
         }
-        m = mv;
+    }
+    float m = -INFINITY;
+    if (one) {
+        if (tid < ns) m = mv;
     } else {
-        for (int s = tid; s < ns; s += kThreads) m = fmaxf(m, pb[s * stride + hd]);
+        for (int s = tid; s < ns; s += kMT) m = fmaxf(m, pb[s * stride + hd]);
     }
     m = wave_max_f(m);
     if (lane == 0) s_red[wave] = m;
-    __syncthreads();
+    lds_barrier();
     m = s_red[0];
-    for (int w = 1; w < kWaves; w++) m = fmaxf(m, s_red[w]);
+    for (int w = 1; w < kMW; w++) m = fmaxf(m, s_red[w]);
     float l = 0.f;
     if (one) {
         if (tid < ns) {
@@ -1119,36 +1136,46 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
             l = lv * w;
         }
     } else {
-        for (int s = tid; s < ns; s += kThreads) {
+        for (int s = tid; s < ns; s += kMT) {
             const float w = expf(pb[s * stride + hd] - m);
             s_w[s] = w;
             l += pb[s * stride + hd + 1] * w;
         }
     }
     l = wave_sum_f(l);
-    __syncthreads();
+    lds_barrier();
     if (lane == 0) s_red[wave] = l;
-    __syncthreads();
+    lds_barrier();
     l = 0.f;
-    for (int w = 0; w < kWaves; w++) l += s_red[w];
+    for (int w = 0; w < kMW; w++) l += s_red[w];
     const float inv = 1.f / l;
     for (int d0 = lane * 4; d0 < hd; d0 += 256) {   // hd % 64 == 0: whole float4s
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         int s = wave;
-        for (; s + 15 * kWaves < ns; s += 16 * kWaves) {   // 16 chunks' loads in flight
+        if (d0 == lane * 4) {   // the prefetched rows (uniform: the first dims pass)
+#pragma unroll
+            for (int u = 0; u < kMPre; u++, s += kMW) {
+                const float w = s < ns ? s_w[s] : 0.f;
+                acc.x = fmaf(pre[u].x, w, acc.x);
+                acc.y = fmaf(pre[u].y, w, acc.y);
+                acc.z = fmaf(pre[u].z, w, acc.z);
+                acc.w = fmaf(pre[u].w, w, acc.w);
+            }
+        }
+        for (; s + 15 * kMW < ns; s += 16 * kMW) {   // 16 chunks' loads in flight
             float4 v[16];
 #pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = *(const float4 *)(pb + (size_t)(s + u * kWaves) * stride + d0);
+            for (int u = 0; u < 16; u++) v[u] = *(const float4 *)(pb + (size_t)(s + u * kMW) * stride + d0);
 #pragma unroll
             for (int u = 0; u < 16; u++) {
-                const float w = s_w[s + u * kWaves];
+                const float w = s_w[s + u * kMW];
                 acc.x = fmaf(v[u].x, w, acc.x);
                 acc.y = fmaf(v[u].y, w, acc.y);
                 acc.z = fmaf(v[u].z, w, acc.z);
                 acc.w = fmaf(v[u].w, w, acc.w);
             }
         }
-        for (; s < ns; s += kWaves) {
+        for (; s < ns; s += kMW) {
             const float4 v = *(const float4 *)(pb + (size_t)s * stride + d0);
             const float w = s_w[s];
             acc.x = fmaf(v.x, w, acc.x);
@@ -1158,12 +1185,14 @@ __global__ __launch_bounds__(kThreads) void attn_merge(AttnArgs a) {
         }
         *(float4 *)&s_acc[wave][d0] = acc;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int i = 0; i < kGPer; i++) {
-        const int d = tid + i * kThreads;
+        const int d = tid + i * kMT;
         if (d < hd) {
-            const float acc = ((s_acc[0][d] + s_acc[1][d]) + s_acc[2][d]) + s_acc[3][d];
+            float acc = s_acc[0][d];
+#pragma unroll
+            for (int w = 1; w < kMW; w++) acc += s_acc[w][d];
             a.ctx[(size_t)h * hd + d] = acc * inv * (1.f / (1.f + expf(-gv[i])));
         }
     }
@@ -1526,7 +1555,7 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     case 32: hipLaunchKernelGGL((attn_part<32, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
     default: return refuse("head dim not in {64, 128, 256, 512}");
     }
-    hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kMT), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("attention launch", e);
     const SegIn o[1] = {{to, dst}};
