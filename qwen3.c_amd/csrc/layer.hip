@@ -942,7 +942,6 @@ __global__ __launch_bounds__(64 * AW) void attn_part(AttnArgs a) {
     const uint32_t cache_b = (uint32_t)a.max_t * (uint32_t)hd * 4u;
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(a.Kc + (size_t)kh * a.max_t * hd, cache_b);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(a.Vc + (size_t)kh * a.max_t * hd, cache_b);
-    const __amdgpu_buffer_rsrc_t rn = buf_rsrc(a.v + (size_t)kh * hd, (uint32_t)hd * 4u);
     float kv[kSteps][DPL];
 #pragma unroll
     for (int st = 0; st < kSteps; st++) {
