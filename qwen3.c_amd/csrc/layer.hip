@@ -62,6 +62,8 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+// silu(z) of the gated norm, with a hardware reciprocal (< 2 ulp)
+__device__ __forceinline__ float silu_gate(float z) { return z * __builtin_amdgcn_rcpf(1.f + expf(-z)); }
 
 // ---------------------------------------------------------------- projections
 constexpr int kMaxSeg = 4;
@@ -74,6 +76,7 @@ struct ProjSeg {
     int O;
     int g0;                  // first row group of the segment in the launch's row-group space
     unsigned long long *yt;  // fused layer kernel: the outputs as tagged words (epoch << 32 | bits)
+    int act;                 // 1: the segment stores silu(row) (GDN's z, the gated norm's gate)
 };
 
 struct ProjArgs {
@@ -82,7 +85,7 @@ struct ProjArgs {
     int I, gs, ng, nl, row_bytes;
     const float *x;    // XF_PLAIN: the input row; XF_NORM: the residual; XF_GATED: raw y
     const float *xw;   // XF_NORM: norm weight [I] (zero-centred); XF_GATED: gnorm [VD]
-    const float *z;    // XF_GATED: the z projection [I]
+    const float *z;    // XF_GATED: silu of the z projection [I] (its in-projection segment has act)
     int VD;
     float eps;
     int add;           // 1: y[r] += acc (residual add), 0: y[r] = acc
@@ -108,7 +111,8 @@ __device__ __forceinline__ double seg_sum_d(double v, int n) {
 // XF_NORM: x[i] * r * (1 + w[i]), r = 1/sqrt(mean(x^2) + eps) over the I columns
 // (c/qwen.c:326-330, double sum of squares).  XF_GATED: per head of VD columns,
 // y * r_h * gnorm[d] * silu(z) (c/qwen.c:768-772).  Zero columns past I stay zero.  The
-// operands (w; or z and gnorm) were loaded into ar / br together with x.
+// operands (w; or silu(z) and gnorm) were loaded into ar / br together with x.  silu(z) is
+// applied once, by the store of z's in-projection (silu_gate), not by every block here.
 template <int XF>
 __device__ __forceinline__ void xf_apply(XRegs &xr, const XRegs &ar, const XRegs &br, const ProjArgs &a, int ncols) {
     const int tid = threadIdx.x, nwords = ncols / 8;
@@ -126,10 +130,9 @@ __device__ __forceinline__ void xf_apply(XRegs &xr, const XRegs &ar, const XRegs
             ss = seg_sum_d(ss, wph);
             const float r = 1.f / sqrtf((float)(ss / a.VD) + a.eps);
 #pragma unroll
-            for (int c = 0; c < 8; c++) {   // silu(z) with a hardware reciprocal (< 2 ulp)
+            for (int c = 0; c < 8; c++) {
                 const int i = w * 8 + c;
-                const float z = ar.v[k][c], sz = z * __builtin_amdgcn_rcpf(1.f + expf(-z));
-                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * br.v[k][c] * sz;
+                if (w < nwords && i < a.I) xr.v[k][c] = xr.v[k][c] * r * br.v[k][c] * ar.v[k][c];
             }
         }
     }
@@ -159,13 +162,14 @@ struct SegSel {
     float *y;
     int O, g0;
     unsigned long long *yt;
+    int act;
 };
 __device__ __forceinline__ SegSel seg_of(const ProjArgs &a, int g) {
-    SegSel s = {a.seg[0].w, a.seg[0].sz, a.seg[0].y, a.seg[0].O, a.seg[0].g0, a.seg[0].yt};
+    SegSel s = {a.seg[0].w, a.seg[0].sz, a.seg[0].y, a.seg[0].O, a.seg[0].g0, a.seg[0].yt, a.seg[0].act};
 #pragma unroll
     for (int t = 1; t < kMaxSeg; t++)
         if (t < a.nseg && g >= a.seg[t].g0)
-            s = {a.seg[t].w, a.seg[t].sz, a.seg[t].y, a.seg[t].O, a.seg[t].g0, a.seg[t].yt};
+            s = {a.seg[t].w, a.seg[t].sz, a.seg[t].y, a.seg[t].O, a.seg[t].g0, a.seg[t].yt, a.seg[t].act};
     return s;
 }
 
@@ -310,9 +314,10 @@ __device__ __forceinline__ void proj_body(const ProjArgs &a, int bid, int nb, XP
             const int r = (g - s.g0) * RPW + sg;
             if (j == LPR - 1 && r < s.O) {
                 if constexpr (kTagOut) {
-                    tag_put(&s.yt[r], a.epoch, acc);
+                    tag_put(&s.yt[r], a.epoch, s.act ? silu_gate(acc) : acc);
                 } else {
-                    s.y[r] = a.add ? old + acc : acc;
+                    const float v = a.add ? old + acc : acc;
+                    s.y[r] = s.act ? silu_gate(v) : v;
                 }
             }
         }
@@ -1353,6 +1358,7 @@ static float *wbuf(int slot, size_t n) {
 struct SegIn {
     const ColiVkTensor *t;
     float *y;
+    int act;   // the segment stores silu(row)
 };
 
 // Row steps per wave, all loaded before the first is reduced: the smallest of 2..8 that
@@ -1428,7 +1434,7 @@ static bool proj_args(const SegIn *segs, int n, int xf, const float *x, const fl
     const int l = pow2_up(t0->nl), rpw = 64 / (l < 2 ? 2 : l);
     int g = 0;
     for (int i = 0; i < n; i++) {
-        a.seg[i] = {segs[i].t->w, segs[i].t->sz, segs[i].y, segs[i].t->O, g, nullptr};
+        a.seg[i] = {segs[i].t->w, segs[i].t->sz, segs[i].y, segs[i].t->O, g, nullptr, segs[i].act};
         g += (segs[i].t->O + rpw - 1) / rpw;
     }
     a.nseg = n;
@@ -1639,7 +1645,7 @@ static bool gdn_fused_launch(GdnState &G, const float *src, const float *ln, Col
     memset(&f, 0, sizeof(f));
     int l1, l3;
     float *placeholder = (float *)tags;   // proj_args checks a destination; the tagged words replace it
-    const SegIn in[4] = {{tqkv, placeholder}, {tz, placeholder}, {ta, placeholder}, {tb, placeholder}};
+    const SegIn in[4] = {{tqkv, placeholder}, {tz, placeholder, 1}, {ta, placeholder}, {tb, placeholder}};
     if (!proj_args(in, 4, XF_NORM, src, ln, nullptr, 0, d.eps, false, f.p1, &l1)) return false;
     f.p1.seg[0].yt = t_qkv;
     f.p1.seg[1].yt = t_z;
@@ -1729,7 +1735,7 @@ static bool gdn_block(int gi, const float *src, const float *ln, const float *pa
     const bool ab_proj = !params && lanes_like(ta) && lanes_like(tb) && lanes_like(tz) && tqkv->fmt == 6;
     if (ab_proj && ln && fuse_on() && gdn_fusable(tqkv, tout, d))
         return gdn_fused_launch(G, src, ln, tqkv, tz, ta, tb, tout, dst, add, d, st);
-    const SegIn in[4] = {{tqkv, qkv}, {tz, z}, {ta, ab}, {tb, ab + d.VH}};
+    const SegIn in[4] = {{tqkv, qkv}, {tz, z, 1}, {ta, ab}, {tb, ab + d.VH}};   // z as silu(z)
     if (!proj(in, ab_proj ? 4 : 2, ln ? XF_NORM : XF_PLAIN, src, ln, nullptr, 0, d.eps, false, st))
         return false;
     GdnArgs g;
