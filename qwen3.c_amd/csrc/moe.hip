@@ -36,7 +36,8 @@ namespace coli {
 constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
 constexpr int kGSteps = 2;                // gate/up row steps per tile
 constexpr int kRouteReps = 4;             // copies of the route block (readers spread over them)
-constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1], K <= 8
+constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1] | ... | prov [K], K <= 8
+constexpr int kProvOff = 24;              // the provisional ids' words within a copy
 
 struct MoeArgs {
     const float *x;                       // [D] expert input (post-attention RMSNorm), or the
@@ -228,30 +229,48 @@ __device__ __forceinline__ void down_slot(const MoeGeom &g, const ExpertRec &rec
 // ---------------------------------------------------------------- gate/up rows
 // h[r] = silu(gate r . x) * (up r . x) for the tile's rows (c/qwen.c:780-786, silu :173).
 // All of the tile's weight loads are issued before the first row is reduced.
-template <int LPR, int CU, typename Emit>
-__device__ __forceinline__ void gateup_rows(const LaneX<CU> &L, const ExpertRec &rec, const MoeGeom &g, int r0,
-                                            Emit emit) {
-    constexpr int RPW = 64 / LPR, NU = LaneX<CU>::NU;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane % LPR, seg = lane / LPR;
+// gateup_load issues the tile's loads, gateup_dot reduces them (split so that a tile can
+// check its expert while the loads are in flight).
+template <int CU>
+struct GateUpW {
+    uint4 wg[kGSteps][kLaneChunks], wu[kGSteps][kLaneChunks];
+    float2 sg[kGSteps][LaneX<CU>::NU], su[kGSteps][LaneX<CU>::NU];
+};
+template <int LPR, int CU>
+__device__ __forceinline__ void gateup_load(const LaneX<CU> &L, const ExpertRec &rec, const MoeGeom &g, int r0,
+                                            GateUpW<CU> &W) {
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, seg = lane / LPR;
     const uint32_t wtot = (uint32_t)g.I * g.rbG, stot = (uint32_t)g.I * g.ngD * 8;
     const __amdgpu_buffer_rsrc_t rgw = buf_rsrc(rec.wg, wtot), rgs = buf_rsrc(rec.sg, stot);
     const __amdgpu_buffer_rsrc_t ruw = buf_rsrc(rec.wu, wtot), rus = buf_rsrc(rec.su, stot);
-    uint4 wg[kGSteps][kLaneChunks], wu[kGSteps][kLaneChunks];
-    float2 sg[kGSteps][NU], su[kGSteps][NU];
 #pragma unroll
     for (int st = 0; st < kGSteps; st++) {
         const int r = r0 + (st * kWaves + wave) * RPW + seg;
         const uint32_t rc = (uint32_t)(r < g.I ? r : g.I);   // row I reads 0 (past the end)
-        lane_load<CU>(rgw, rgs, rc * g.rbG, rc * g.ngD * 8, L, wg[st], sg[st]);
-        lane_load<CU>(ruw, rus, rc * g.rbG, rc * g.ngD * 8, L, wu[st], su[st]);
+        lane_load<CU>(rgw, rgs, rc * g.rbG, rc * g.ngD * 8, L, W.wg[st], W.sg[st]);
+        lane_load<CU>(ruw, rus, rc * g.rbG, rc * g.ngD * 8, L, W.wu[st], W.su[st]);
     }
+}
+template <int LPR, int CU, typename Emit>
+__device__ __forceinline__ void gateup_dot(const LaneX<CU> &L, const MoeGeom &g, int r0, const GateUpW<CU> &W,
+                                           Emit emit) {
+    constexpr int RPW = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j = lane % LPR, seg = lane / LPR;
 #pragma unroll
     for (int st = 0; st < kGSteps; st++) {
         const int r = r0 + (st * kWaves + wave) * RPW + seg;
-        const float gv = seg_sum<LPR>(lane_row<CU>(wg[st], sg[st], L));
-        const float uv = seg_sum<LPR>(lane_row<CU>(wu[st], su[st], L));
+        const float gv = seg_sum<LPR>(lane_row<CU>(W.wg[st], W.sg[st], L));
+        const float uv = seg_sum<LPR>(lane_row<CU>(W.wu[st], W.su[st], L));
         if (j == LPR - 1 && r < g.I) emit(r, gv / (1.f + expf(-gv)) * uv);
     }
+}
+template <int LPR, int CU, typename Emit>
+__device__ __forceinline__ void gateup_rows(const LaneX<CU> &L, const ExpertRec &rec, const MoeGeom &g, int r0,
+                                            Emit emit) {
+    GateUpW<CU> W;
+    gateup_load<LPR, CU>(L, rec, g, r0, W);
+    gateup_dot<LPR, CU>(L, g, r0, W, emit);
 }
 
 // ---------------------------------------------------------------- R: router rows
@@ -379,7 +398,7 @@ __device__ __forceinline__ void tile_route_n(const MoeArgs &a, RouteLds &R, Cert
     }
     gate = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gate), E & 63));
     wave_lds_order();
-    route_wave(R, E, K, C.l, C.b);   // with the crude bounds
+    route_wave(R, E, K, C.l, C.b, RouteProv{route_of(a, 0) + kProvOff, kRouteStride, kRouteReps, a.epoch});   // crude bounds
     if (R.amb) {   // the tight bounds of the candidates (published by now), and the check again
         const int nc = R.ncand;
         for (int r = lane; r < nc; r += 64) {
@@ -455,20 +474,31 @@ __device__ __forceinline__ void tile_gateup(const MoeArgs &a, const XPrep &P, in
     LaneX<CU> L;   // x digits of the lane first: they do not depend on the route
     lane_geo<CU>(j, g.nlG, g.D, g.gs, L);
     lane_x<CU>(P, g.gs, L);
-    if (threadIdx.x == 0) {
-        int e = a.E;
-        if (slot < a.K) e = __float_as_int(tag_get(&route_of(a, blockIdx.x % kRouteReps)[slot], a.epoch, a.err));
+    // A routed tile starts its loads on the route tile's provisional pick, then checks the
+    // final route (published later, after the certification) while they are in flight; only
+    // when the certification changed this slot's pick does it load again.
+    const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
+    auto pick = [&](int w) {
+        int e = __float_as_int(tag_get(&route[w], a.epoch, a.err));
         if (e < 0 || e > a.E) {
             err_set(a.err, a.epoch, 2);
             e = a.E;
         }
-        *s_e = e;
-    }
+        return e;
+    };
+    if (threadIdx.x == 0) s_e[0] = slot < a.K ? pick(kProvOff + slot) : a.E;
     __syncthreads();
-    const ExpertRec rec = a.rec[*s_e];
+    const int e0 = s_e[0];
+    GateUpW<CU> W;
+    gateup_load<LPR, CU>(L, a.rec[e0], g, r0, W);
+    if (slot < a.K) {   // block uniform
+        if (threadIdx.x == 0) s_e[1] = pick(slot);
+        __syncthreads();
+        if (s_e[1] != e0) gateup_load<LPR, CU>(L, a.rec[s_e[1]], g, r0, W);
+    }
     unsigned long long *hs = h_of(a, slot);
     const uint32_t ep = a.epoch;
-    gateup_rows<LPR, CU>(L, rec, g, r0, [&](int r, float h) { tag_put(&hs[r], ep, h); });
+    gateup_dot<LPR, CU>(L, g, r0, W, [&](int r, float h) { tag_put(&hs[r], ep, h); });
 }
 
 // ---------------------------------------------------------------- D and C tiles
@@ -553,7 +583,7 @@ __device__ __forceinline__ void tile_combine(const MoeArgs &a, int r0, float *s_
 template <int LPRG, int TPRD>
 __global__ __launch_bounds__(kThreads, 3) void moe_block_kernel(MoeArgs a) {
     __shared__ MoeLds S;
-    __shared__ int s_e[1];
+    __shared__ int s_e[2];
     __shared__ ExpertRec s_rec[1];
     __shared__ float s_w[kMaxSlots];
     __shared__ double s_red[kWaves];

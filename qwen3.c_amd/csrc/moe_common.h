@@ -304,8 +304,18 @@ __device__ __forceinline__ int key_rank(const unsigned long long *keys, int n8, 
 // intervals meet or another candidate's interval reaches the lowest pick's lower end
 // (R.thr): then route_certify_wave decides with the reference's logits.  The candidates
 // by rank go to R.cid / R.clo / R.chi.
+// Where route_wave publishes its provisional picks: the K expert ids by (e desc, index asc),
+// before the exact tie path and the certification may change them, as tagged words
+// w[c * stride + k] for copies c < reps.  w == nullptr: none.
+struct RouteProv {
+    unsigned long long *w;
+    int stride, reps;
+    uint32_t epoch;
+};
+
 template <int kPer>   // experts per lane: E <= 64 kPer
-__device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const float *lg, const float *bd) {
+__device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const float *lg, const float *bd,
+                                             const RouteProv &pv) {
     const int lane = threadIdx.x & 63;
     float ev[kPer];
     float m = -1e30f;   // the reference's initial max
@@ -369,6 +379,9 @@ __device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const fl
         }
     }
     wave_lds_order();
+    if (pv.w)   // nc >= 8 >= K: R.top[0, K) is filled
+        for (int q = lane; q < pv.reps * K; q += 64)
+            tag_put(pv.w + (size_t)(q / K) * pv.stride + q % K, pv.epoch, __int_as_float(key_expert(R.top[q % K])));
     int amb = 0;
     float thr = -INFINITY;
     if (bd) amb = cert_check(R, K, nc, &thr);
@@ -414,10 +427,11 @@ __device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const fl
 }
 
 // route_wave_n for the number of experts per lane that E needs (E <= kMaxE)
-__device__ __forceinline__ void route_wave(RouteLds &R, int E, int K, const float *lg = nullptr, const float *bd = nullptr) {
-    if (E <= 256) route_wave_n<4>(R, E, K, lg, bd);
-    else if (E <= 512) route_wave_n<8>(R, E, K, lg, bd);
-    else route_wave_n<16>(R, E, K, lg, bd);
+__device__ __forceinline__ void route_wave(RouteLds &R, int E, int K, const float *lg = nullptr, const float *bd = nullptr,
+                                           const RouteProv &pv = RouteProv{nullptr, 0, 0, 0u}) {
+    if (E <= 256) route_wave_n<4>(R, E, K, lg, bd, pv);
+    else if (E <= 512) route_wave_n<8>(R, E, K, lg, bd, pv);
+    else route_wave_n<16>(R, E, K, lg, bd, pv);
 }
 
 // The router's input row into LDS by one wave, bit for bit what the block form stage_input
