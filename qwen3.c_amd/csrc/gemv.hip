@@ -32,12 +32,14 @@ struct TopkArgs {
     int *out_i;                  // fused top-k: the k best (value desc, index asc)
     float *out_v;
     int *err;                    // fused top-k: set to 1 when a bounded poll gives up
+    const float *xw;             // argmax: x := zero-centred RMSNorm of x with weight xw (none if null)
+    float eps;
 };
 
 // ---- argmax as a 64-bit key: [63:56] launch epoch, [55:24] order-preserving bits of the
 // value, [23:0] 0xFFFFFF - row.  The maximum key is the best (value desc, row asc) of the
 // launch; a stale key of an earlier launch (lower epoch) always loses.  Rows < 2^24.
-constexpr int kArgSlots = 16;   // blocks spread their atomicMax over 16 slots (contention)
+static_assert(kArgSlots == 16, "blocks spread their atomicMax over 16 slots (contention)");
 __device__ __forceinline__ unsigned long long arg_key(uint32_t epoch, float v, uint32_t row) {
     const uint32_t u = __float_as_uint(v);
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -343,9 +345,11 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
     const uint32_t wtot = (uint32_t)O * (uint32_t)row_bytes, srb = (uint32_t)ng * 8u, stot = (uint32_t)O * srb;
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(W, wtot), rs = buf_rsrc(SZ, stot);
     const int ncols = nl * kLaneChunks * 32;
-    XRegs xr;
+    XRegs xr, wr;
     prep_load(x, I, ncols, xr);   // x first: in-order load counters then let the
-    LaneX<CU> L;                  // weight prefetch stay in flight through the prologue
+    if constexpr (MODE == 1)      // weight prefetch stay in flight through the prologue
+        prep_load(tk.xw ? tk.xw : x, tk.xw ? I : 0, ncols, wr);   // no norm: reads 0, no memory access
+    LaneX<CU> L;
     lane_geo<CU>(j, nl, I, gs, L);
 
     // slot u of this wave walks rows r = (rg0 + u*nw + it*nw*U) * RPW + seg
@@ -363,6 +367,11 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
         sro[u] = rr[u] * srb;
         lane_load<CU>(rw, rs, min(wro[u], wtot), min(sro[u], stot), L, wq[u], sv[u]);
     }
+    if constexpr (MODE == 1)
+        if (tk.xw) {   // c/qwen.c:326-330 (the final norm before lm_head)
+            __shared__ double s_red[kWaves];
+            norm_apply(xr, wr, I, ncols, tk.eps, s_red);
+        }
     prep_x(xr, gs, ncols, P);
     lane_x<CU>(P, gs, L);
 
@@ -684,23 +693,25 @@ bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t 
 
 // GEMV whose blocks also fold their best row into the argmax slots (fmt 6 lanes layout,
 // O < 2^24).  *epoch receives the launch tag; the slots hold the result after the kernel.
+// xw != NULL: x is normed first (zero-centred RMSNorm, weight xw, in each block's x
+// prologue).  The kArgSpare words after the slots are the caller's.
 bool gemv_argmax(const ColiVkTensor *t, const float *d_x, float *d_y, hipStream_t st, uint32_t *epoch,
-                 const unsigned long long **slots) {
+                 unsigned long long **slots, const float *xw, float eps) {
     if (t->layout != kLayoutLanes || t->O >= (1 << 24)) return false;
     if (!d_y) {
         if (!scratch(&g_logits, &g_logits_cap, (size_t)t->O * 4)) return false;
         d_y = (float *)g_logits;
     }
-    if (!scratch(&g_slots, &g_slots_cap, kArgSlots * 8)) return false;   // zeroed when allocated
+    if (!scratch(&g_slots, &g_slots_cap, (kArgSlots + kArgSpare) * 8)) return false;   // zeroed when allocated
     g_epoch = (g_epoch + 1) & 0xFFu;
     if (g_epoch == 0) {   // tags wrap: clear the slots so no old key outranks the new tag
         hipLaunchKernelGGL(argmax_reset, dim3(1), dim3(64), 0, st, (unsigned long long *)g_slots);
         g_epoch = 1;
     }
-    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch, nullptr, nullptr, nullptr};
+    const TopkArgs ta = {1, nullptr, nullptr, (unsigned long long *)g_slots, g_epoch, nullptr, nullptr, nullptr, xw, eps};
     if (!launch_lanes_mode<1>(t, d_x, d_y, st, ta)) return false;
     *epoch = g_epoch;
-    *slots = (const unsigned long long *)g_slots;
+    *slots = (unsigned long long *)g_slots;
     return true;
 }
 
@@ -714,7 +725,7 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
     }
     if (want_k && tk->k == 1 && t->layout == kLayoutLanes && t->O < (1 << 24)) {
         uint32_t ep;
-        const unsigned long long *sl;
+        unsigned long long *sl;
         if (!gemv_argmax(t, d_x, d_y, st, &ep, &sl)) return false;
         hipLaunchKernelGGL(argmax_decode, dim3(1), dim3(64), 0, st, sl, ep, tk->idx, tk->val);
         const hipError_t e = hipGetLastError();
@@ -838,7 +849,7 @@ COLI_API int coli_vk_matmul_argmax(ColiVkTensor **tensor, const void *weights, c
     if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
     if (!stage_x(x, (size_t)I * 4)) return 0;
     uint32_t ep;
-    const unsigned long long *sl;
+    unsigned long long *sl;
     if (gemv_argmax(*tensor, (const float *)g_st.dx, nullptr, stream(), &ep, &sl)) {
         unsigned long long keys[kArgSlots];
         if (!fetch(keys, sl, sizeof(keys), "matmul_argmax")) return 0;

@@ -78,6 +78,15 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
 // k best (value desc, index asc) of d_v[0, n), k <= 8
 bool topk(const float *d_v, int n, int k, int *d_idx, float *d_val, hipStream_t st);
 bool rmsnorm_zc(const float *d_x, const float *d_w, float *d_y, int D, float eps, hipStream_t st);
+// GEMV (fmt 6 lanes layout, O < 2^24) whose blocks fold their best row into kArgSlots
+// tagged keys (*slots, the launch tag in *epoch); with xw, x is first normed (zero-centred
+// RMSNorm, weight xw) in the kernel's x prologue.  The kArgSpare words after the keys are
+// the caller's (read back with them).  argmax_decode_host: the keys -> (idx, val), false
+// when no key of the launch is there.
+constexpr int kArgSlots = 16, kArgSpare = 8;
+bool gemv_argmax(const ColiVkTensor *t, const float *d_x, float *d_y, hipStream_t st, uint32_t *epoch,
+                 unsigned long long **slots, const float *xw = nullptr, float eps = 0.f);
+bool argmax_decode_host(const unsigned long long *keys, uint32_t epoch, int *idx, float *val);
 
 // Dense GEMM on MFMA over S rows of x (prefill.hip): d_y[i] [S][O_i] = x . t[i]^T for nt
 // fmt6 tensors of group size 128 sharing I (one digit decomposition of x serves all).  gx:

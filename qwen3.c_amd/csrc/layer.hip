@@ -2416,6 +2416,26 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
                                         int I, int O, int gs, float eps, int *idx, float *val) {
     if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
     if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
+    if ((*tensor)->layout == kLayoutLanes && O < (1 << 24)) {
+        // one launch: the norm in the GEMV's x prologue, argmax keys, and the error words
+        // gathered after the keys; the host decodes the keys from the one read-back
+        uint32_t ep;
+        unsigned long long *sl;
+        if (!gemv_argmax(*tensor, g_str.d_resid, nullptr, stream(), &ep, &sl, g_str.d_fnw, eps)) return 0;
+        const bool chk = !err_clean();
+        if (chk && !err_gather_launch(sl + kArgSlots)) return 0;
+        unsigned long long hb[kArgSlots + 3];
+        if (!sync_stream("stream_norm_argmax") ||
+            hipMemcpy(hb, sl, (kArgSlots + (chk ? 3 : 0)) * 8, hipMemcpyDeviceToHost) != hipSuccess)
+            return 0;
+        if (chk && !stream_err_ok("stream_norm_argmax", hb + kArgSlots)) return 0;
+        int i;
+        float v;
+        if (!argmax_decode_host(hb, ep, &i, &v) || i < 0 || i >= O) return 0;   // the engine's host scan decides
+        *idx = i;
+        if (val) *val = v;
+        return 1;
+    }
     // xn [I] | result: 16 ints (idx at 0, value bits at 8) | 3 error words (8-aligned)
     const size_t roff = ((size_t)I * 4 + 7) & ~(size_t)7;
     if (!scratch((void **)&g_str.d_xn, &g_str.xn_cap, roff + 64 + 24)) return 0;
