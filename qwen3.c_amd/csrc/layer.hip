@@ -1797,10 +1797,9 @@ struct StreamState {
     int fused_last = 0;           // the last route_pipe ran the MoE on the device
     int pending = 0;              // top-k ids of fused layers await stream_end
     int hist_K[kMaxLayers];       // ids recorded per layer in this stream (0 = none)
-    struct {                      // stream_end's read-back: the id history, then error words
-        int hist[kMaxLayers * kMaxK];
-        unsigned long long err[3];
-    } rb;
+    int hist_hi = 0;              // 1 + the highest layer with recorded ids
+    int *h_rb = nullptr;          // pinned: stream_end's read-back, laid out as the device history
+    size_t hrb_cap = 0;
     uint64_t chk_moe = ~0ull, chk_layer = ~0ull;   // launch counts at the last clean check
     float *h_nrm = nullptr;       // host copy of the last non-fused route's nrm
     size_t hnrm_cap = 0;
@@ -2258,7 +2257,12 @@ COLI_API int coli_vk_gdn_full_route(int layer, const float *x_in, const float *r
 // weights the caller reads back (the engine then issues the experts, c/qwen.c:934-998).
 COLI_API int coli_vk_stream_available(void) { return ok() ? 1 : 0; }
 
-static int *hist_dev() { return (int *)wbuf(W_HIST, (size_t)kMaxLayers * kMaxK); }
+// The device history of the fused layers' top-k ids: kHistHead ints (3 error words, gathered
+// there by stream_end), then kTopK ids per layer (fused layers have K <= kTopK).  stream_end
+// reads back the words up to the highest recorded layer in one copy.
+constexpr int kHistHead = 8;
+static size_t hist_ints() { return kHistHead + (size_t)kMaxLayers * kTopK; }
+static int *hist_dev() { return (int *)wbuf(W_HIST, hist_ints()); }
 
 COLI_API int coli_vk_stream_begin(const float *x, int D) {
     if (!ok() || !x || D < 1) return 0;
@@ -2277,6 +2281,7 @@ COLI_API int coli_vk_stream_begin(const float *x, int D) {
     g_str.pending = 0;
     g_str.fused_last = 0;
     memset(g_str.hist_K, 0, sizeof(g_str.hist_K));
+    g_str.hist_hi = 0;
     return 1;
 }
 
@@ -2350,22 +2355,16 @@ COLI_API int coli_vk_stream_end(float *x, int D) {
         g_str.pending = 0;
         return 0;
     }
-    // one read-back after the drain: the id history of the fused layers (when pending) and
-    // the error words (when a launch could have set one since the last check)
+    // one read-back after the drain: the error words (when a launch could have set one since
+    // the last check) and the id history of the fused layers (when pending)
     const bool chk = !err_clean();
-    int *dh = hist_dev();   // kMaxLayers * kMaxK ids, then (in the buffer's slack) 3 error words
-    if (!dh) return 0;
-    unsigned long long *d_err = (unsigned long long *)(dh + kMaxLayers * kMaxK);
-    if (chk && !err_gather_launch(d_err)) return 0;
+    int *dh = hist_dev();
+    if (!dh || !host_scratch((void **)&g_str.h_rb, &g_str.hrb_cap, hist_ints() * 4)) return 0;
+    if (chk && !err_gather_launch((unsigned long long *)dh)) return 0;
     if (!sync_stream("stream end")) return 0;
-    static_assert(offsetof(decltype(g_str.rb), err) == sizeof(g_str.rb.hist), "history then error words");
-    if (g_str.pending) {
-        if (hipMemcpy(&g_str.rb, dh, chk ? sizeof(g_str.rb) : sizeof(g_str.rb.hist), hipMemcpyDeviceToHost) != hipSuccess)
-            return 0;
-    } else if (chk) {
-        if (hipMemcpy(g_str.rb.err, d_err, sizeof(g_str.rb.err), hipMemcpyDeviceToHost) != hipSuccess) return 0;
-    }
-    if (chk && !stream_err_ok("stream end", g_str.rb.err)) {
+    const size_t nb = g_str.pending ? (kHistHead + (size_t)g_str.hist_hi * kTopK) * 4 : chk ? 24 : 0;
+    if (nb && hipMemcpy(g_str.h_rb, dh, nb, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    if (chk && !stream_err_ok("stream end", (const unsigned long long *)g_str.h_rb)) {
         g_str.live = 0;
         g_str.pending = 0;
         return 0;
@@ -2470,12 +2469,15 @@ static int pipe_tail(int ln_layer, ColiVkTensor *router, int E, int topk, float 
     float *dn = wbuf(W_NRM, g_str.D), *dl = wbuf(W_LOGIT, (size_t)2 * E + 2 * kMaxK);
     int *dh = hist_dev();
     if (!dn || !dl || !dh || topk < 1 || topk > kTopK || E > kMaxE) return 0;   // device top-k: K <= 8
+    if (ln_layer < 0 || ln_layer >= kMaxLayers) return 0;
     // fused: the MoE block norms the residual itself (post_ln) and adds into it
     if (moe_ready(ln_layer) && moe_decode(ln_layer, router, topk, g_str.d_resid, g_str.d_resid, 1,
-                                          dh + (size_t)ln_layer * kMaxK, nullptr, stream(), g_ln[ln_layer].post_ln, eps)) {
+                                          dh + kHistHead + (size_t)ln_layer * kTopK, nullptr, stream(), g_ln[ln_layer].post_ln,
+                                          eps)) {
         g_str.fused_last = 1;
         g_str.pending = 1;
         g_str.hist_K[ln_layer] = topk;
+        if (ln_layer >= g_str.hist_hi) g_str.hist_hi = ln_layer + 1;
         return 1;
     }
     if (!ok()) return 0;
@@ -2533,7 +2535,7 @@ COLI_API int coli_vk_stream_ix_pending(void) { return g_str.pending ? 1 : 0; }
 COLI_API int coli_vk_stream_ix_hist(int layer, int *idx_out, int K) {
     if (!g_str.pending || g_str.live || layer < 0 || layer >= kMaxLayers || !idx_out) return 0;
     const int n = g_str.hist_K[layer] < K ? g_str.hist_K[layer] : K;
-    for (int k = 0; k < n; k++) idx_out[k] = g_str.rb.hist[layer * kMaxK + k];
+    for (int k = 0; k < n; k++) idx_out[k] = g_str.h_rb[kHistHead + layer * kTopK + k];
     return n;
 }
 
