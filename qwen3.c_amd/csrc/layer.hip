@@ -1800,6 +1800,8 @@ struct StreamState {
     int hist_hi = 0;              // 1 + the highest layer with recorded ids
     int *h_rb = nullptr;          // pinned: stream_end's read-back, laid out as the device history
     size_t hrb_cap = 0;
+    unsigned long long *h_am = nullptr;   // pinned: stream_norm_argmax's read-back (keys, error words)
+    size_t ham_cap = 0;
     uint64_t chk_moe = ~0ull, chk_layer = ~0ull;   // launch counts at the last clean check
     float *h_nrm = nullptr;       // host copy of the last non-fused route's nrm
     size_t hnrm_cap = 0;
@@ -2361,9 +2363,9 @@ COLI_API int coli_vk_stream_end(float *x, int D) {
     int *dh = hist_dev();
     if (!dh || !host_scratch((void **)&g_str.h_rb, &g_str.hrb_cap, hist_ints() * 4)) return 0;
     if (chk && !err_gather_launch((unsigned long long *)dh)) return 0;
-    if (!sync_stream("stream end")) return 0;
     const size_t nb = g_str.pending ? (kHistHead + (size_t)g_str.hist_hi * kTopK) * 4 : chk ? 24 : 0;
-    if (nb && hipMemcpy(g_str.h_rb, dh, nb, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+    if (nb && hipMemcpyAsync(g_str.h_rb, dh, nb, hipMemcpyDeviceToHost, stream()) != hipSuccess) return 0;
+    if (!sync_stream("stream end")) return 0;   // the drain and the read-back
     if (chk && !stream_err_ok("stream end", (const unsigned long long *)g_str.h_rb)) {
         g_str.live = 0;
         g_str.pending = 0;
@@ -2423,9 +2425,10 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
         if (!gemv_argmax(*tensor, g_str.d_resid, nullptr, stream(), &ep, &sl, g_str.d_fnw, eps)) return 0;
         const bool chk = !err_clean();
         if (chk && !err_gather_launch(sl + kArgSlots)) return 0;
-        unsigned long long hb[kArgSlots + 3];
-        if (!sync_stream("stream_norm_argmax") ||
-            hipMemcpy(hb, sl, (kArgSlots + (chk ? 3 : 0)) * 8, hipMemcpyDeviceToHost) != hipSuccess)
+        if (!host_scratch((void **)&g_str.h_am, &g_str.ham_cap, (kArgSlots + 3) * 8)) return 0;
+        unsigned long long *hb = g_str.h_am;
+        if (hipMemcpyAsync(hb, sl, (kArgSlots + (chk ? 3 : 0)) * 8, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+            !sync_stream("stream_norm_argmax"))
             return 0;
         if (chk && !stream_err_ok("stream_norm_argmax", hb + kArgSlots)) return 0;
         int i;
