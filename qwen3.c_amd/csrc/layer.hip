@@ -1202,6 +1202,74 @@ __global__ __launch_bounds__(kMT) void attn_merge(AttnArgs a) {
     }
 }
 
+// The merge with a head's dims split over blocks (ns <= kMT chunks, hd % 64 == 0): block
+// (h, q) takes dims 64 q .. 64 q + 63, so a head's partials are read by hd / 64 blocks
+// (one block per head read ~130 KB at configs[3]).  Lane l holds dims 64 q + 4 (l % 16) ..
+// + 3 of chunks (u kMW + wave) 4 + l / 16; those rows, each chunk's (m, l) (thread t: chunk
+// t) and the gate go out in one round trip.  The chunk sums meet in LDS and are added in
+// chunk order.
+constexpr int kMDPre = kMT / (kMW * 4);   // chunk rows per lane
+__global__ __launch_bounds__(kMT) void attn_merge_d(AttnArgs a) {
+    __shared__ float s_w[kMT];
+    __shared__ float s_red[kMW];
+    __shared__ __attribute__((aligned(16))) float s_acc[kMT / 16][64];   // [chunk % 32][dim]
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hd = a.hd, nq = hd / 64, h = blockIdx.x / nq, q = blockIdx.x % nq;
+    const int G = a.H / a.KH, kh = h / G, gg = h % G;
+    const int ns = (a.pos + 1 + kAttT - 1) / kAttT;
+    const float *pb = a.part + ((size_t)kh * a.nsplit) * G * (hd + 2) + (size_t)gg * (hd + 2);
+    const size_t stride = (size_t)G * (hd + 2);
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(pb, (uint32_t)(((size_t)(ns - 1) * stride + hd + 2) * 4));
+    auto ldp = [&](size_t i, bool on) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, on ? (int)(i * 4) : (int)kOOB, 0, 0));
+    };
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.q + (size_t)h * 2 * hd + hd, (uint32_t)hd * 4u);
+    const float gv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, tid < 64 ? (64 * q + tid) * 4 : (int)kOOB, 0, 0));
+    const float mv = ldp((size_t)tid * stride + hd, tid < ns);
+    const float lv = ldp((size_t)tid * stride + hd + 1, tid < ns);
+    const int dq = lane & 15, cs = lane >> 4, d0 = 64 * q + 4 * dq;
+    float4 pre[kMDPre];
+#pragma unroll
+    for (int u = 0; u < kMDPre; u++) {
+        const int sc = (u * kMW + wave) * 4 + cs;
+        const uint32_t o = sc < ns ? (uint32_t)(((size_t)sc * stride + d0) * 4) : kOOB;
+        const coli_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)o, 0, 0);
+        pre[u] = make_float4(__int_as_float(v.x), __int_as_float(v.y), __int_as_float(v.z), __int_as_float(v.w));
+    }
+    float m = tid < ns ? mv : -INFINITY;
+    m = wave_max_f(m);
+    if (lane == 0) s_red[wave] = m;
+    lds_barrier();
+    m = s_red[0];
+    for (int w = 1; w < kMW; w++) m = fmaxf(m, s_red[w]);
+    const float wgt = tid < ns ? expf(mv - m) : 0.f;
+    s_w[tid] = wgt;
+    float l = wave_sum_f(tid < ns ? lv * wgt : 0.f);
+    lds_barrier();
+    if (lane == 0) s_red[wave] = l;
+    lds_barrier();
+    l = 0.f;
+    for (int w = 0; w < kMW; w++) l += s_red[w];
+    const float inv = 1.f / l;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < kMDPre; u++) {
+        const int sc = (u * kMW + wave) * 4 + cs;
+        const float w = sc < ns ? s_w[sc] : 0.f;
+        acc.x = fmaf(pre[u].x, w, acc.x);
+        acc.y = fmaf(pre[u].y, w, acc.y);
+        acc.z = fmaf(pre[u].z, w, acc.z);
+        acc.w = fmaf(pre[u].w, w, acc.w);
+    }
+    *(float4 *)&s_acc[wave * 4 + cs][4 * dq] = acc;
+    lds_barrier();
+    if (tid < 64) {
+        float t = 0.f;
+        for (int r = 0; r < kMT / 16; r++) t += s_acc[r][tid];
+        a.ctx[(size_t)h * hd + 64 * q + tid] = t * inv * (1.f / (1.f + expf(-gv)));
+    }
+}
+
 // ---------------------------------------------------------------- small kernels
 __global__ void rms_rows(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ y, int D,
                          float eps) {
@@ -1562,7 +1630,10 @@ static bool gqa_block(int kvi, const float *src, const float *ln, ColiVkTensor *
     case 32: hipLaunchKernelGGL((attn_part<32, kAttW>), dim3(KH * nsplit), dim3(64 * kAttW), 0, st, a); break;
     default: return refuse("head dim not in {64, 128, 256, 512}");
     }
-    hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kMT), 0, st, a);
+    if ((pos + kAttT) / kAttT <= kMT && hd % 64 == 0)   // ns chunks: one per thread
+        hipLaunchKernelGGL(attn_merge_d, dim3(H * (hd / 64)), dim3(kMT), 0, st, a);
+    else
+        hipLaunchKernelGGL(attn_merge, dim3(H), dim3(kMT), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail("attention launch", e);
     const SegIn o[1] = {{to, dst}};
