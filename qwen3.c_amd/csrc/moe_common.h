@@ -259,23 +259,16 @@ __device__ __forceinline__ int cert_check(const RouteLds &R, int K, int nc, floa
 __device__ __forceinline__ int key_expert(unsigned long long k) { return (int)(0xFFFFFFu - (uint32_t)(k & 0xFFFFFFu)); }
 __device__ __forceinline__ float key_value(unsigned long long k) { return __uint_as_float((uint32_t)(k >> 24)); }
 
-// Rank of key `me` among keys[0, n8) (n8 a multiple of 8, zero padded; keys unique), and
-// the largest key below it (0 when none).
-__device__ __forceinline__ int key_rank(const unsigned long long *keys, int n8, unsigned long long me,
-                                        unsigned long long *succ) {
+// Rank of key `me` among keys[0, n8) (n8 a multiple of 8, zero padded; keys unique).
+__device__ __forceinline__ int key_rank(const unsigned long long *keys, int n8, unsigned long long me) {
     int rank = 0;
-    unsigned long long sc = 0ull;
     for (int o0 = 0; o0 < n8; o0 += 8) {   // 8 broadcast reads in flight, no conditions
         unsigned long long o8[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) o8[u] = keys[o0 + u];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            rank += o8[u] > me ? 1 : 0;
-            sc = o8[u] < me && o8[u] > sc ? o8[u] : sc;
-        }
+        for (int u = 0; u < 8; u++) rank += o8[u] > me ? 1 : 0;
     }
-    *succ = sc;
     return rank;
 }
 
@@ -361,27 +354,32 @@ __device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const fl
     const int nc8 = (nc + 7) & ~7;
     if (nc + lane < nc8) R.cand[nc + lane] = 0ull;   // pad to a multiple of 8 (zero is below every key)
     wave_lds_order();
-    // rank by counting; the first K go to R.top.  A candidate whose successor is distinct
-    // but within 2^-21 may share its p: then the exact path decides.
-    bool tie = false;
+    // rank by counting; the first K go to R.top, every candidate's expert to R.cid by rank
     for (int c = lane; c < nc; c += 64) {
         const unsigned long long me = R.cand[c];
-        unsigned long long succ;
-        const int rank = key_rank(R.cand, nc8, me, &succ);
+        const int rank = key_rank(R.cand, nc8, me);
         if (rank < K) R.top[rank] = me;
-        const float a = key_value(me), b = key_value(succ);
-        tie |= succ && b < a && b >= a * (1.f - 0x1p-21f);
-        if (bd) {
-            const int e = key_expert(me);
-            R.cid[rank] = e;
-            R.clo[rank] = lg[e] - bd[e];
-            R.chi[rank] = lg[e] + bd[e];
-        }
+        R.cid[rank] = key_expert(me);
     }
     wave_lds_order();
     if (pv.w)   // nc >= 8 >= K: R.top[0, K) is filled
         for (int q = lane; q < pv.reps * K; q += 64)
             tag_put(pv.w + (size_t)(q / K) * pv.stride + q % K, pv.epoch, __int_as_float(key_expert(R.top[q % K])));
+    // Two candidates of consecutive ranks that are distinct but within 2^-21 may share their
+    // p: then the exact path decides.  Their logit intervals by rank for the certification.
+    bool tie = false;
+    for (int r = lane; r < nc; r += 64) {
+        const int e = R.cid[r];
+        if (r + 1 < nc) {
+            const float a = R.p[e], b = R.p[R.cid[r + 1]];
+            tie |= b < a && b >= a * (1.f - 0x1p-21f);
+        }
+        if (bd) {
+            R.clo[r] = lg[e] - bd[e];
+            R.chi[r] = lg[e] + bd[e];
+        }
+    }
+    wave_lds_order();
     int amb = 0;
     float thr = -INFINITY;
     if (bd) amb = cert_check(R, K, nc, &thr);
@@ -398,8 +396,7 @@ __device__ __forceinline__ void route_wave_n(RouteLds &R, int E, int K, const fl
         wave_lds_order();
         for (int c = lane; c < nc; c += 64) {
             const unsigned long long me = R.cand[c];
-            unsigned long long succ;
-            const int rank = key_rank(R.cand, nc8, me, &succ);
+            const int rank = key_rank(R.cand, nc8, me);
             if (rank < K) R.top[rank] = me;
         }
         wave_lds_order();
