@@ -1446,11 +1446,12 @@ static bool launch_proj_u(ProjArgs &a, hipStream_t st) {
     auto kern = proj_gemv<LPR, CU, U, XF>;
     long nb = ((long)a.ngroups + kWaves * U - 1) / (kWaves * U);
     if (nb > (long)kProjBPC * n_cu()) nb = (long)kProjBPC * n_cu();
-    // A few blocks past a whole number per CU would each share a CU with the others and end
-    // last (measured: the GatedDeltaNet in-projection's 4 blocks past 768 ended ~1 us after
-    // the rest); without them, some waves take one more row step, whose loads are prefetched.
+    // Blocks past a whole number per CU (up to a quarter of the CUs) share a CU with the
+    // others and end last (measured: the GatedDeltaNet in-projection's 4 blocks past 768
+    // ended ~1 us after the rest); without them, some waves take one more row step, whose
+    // loads are prefetched.
     const long ncu = n_cu();
-    if (nb > ncu && nb % ncu <= ncu / 16) nb -= nb % ncu;
+    if (nb > ncu && nb % ncu <= ncu / 4) nb -= nb % ncu;
     if (nb < 1) nb = 1;
     hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(kThreads), 0, st, a);
     const hipError_t e = hipGetLastError();
