@@ -1930,6 +1930,9 @@ void layer_shutdown() {
     scratch_free((void **)&g_str.d_xn, &g_str.xn_cap);
     host_scratch_free((void **)&g_str.h_y, &g_str.hy_cap);
     host_scratch_free((void **)&g_str.h_nrm, &g_str.hnrm_cap);
+    host_scratch_free((void **)&g_str.h_x, &g_str.hx_cap);
+    host_scratch_free((void **)&g_str.h_rb, &g_str.hrb_cap);
+    host_scratch_free((void **)&g_str.h_am, &g_str.ham_cap);
     g_str = StreamState();
 }
 
