@@ -286,6 +286,11 @@ int   coli_hip_layer_fuse(int on);
  * Both give the reference's picks.  A test hook with no counterpart in the reference (it
  * computes only the sequential logits). */
 int   coli_hip_moe_cert_all(int on);
+/* Host-routed expert groups (coli_vk_expert_group*) with more than one row per expert run
+ * as grouped GEMMs on MFMA (0, the default) or, with force_gemv = 1, one GEMV item per
+ * (expert, row) as for single rows; returns the previous setting.  A test and bench hook
+ * with no counterpart in the reference (its multi-row switch is automatic). */
+int   coli_hip_eg_force_gemv(int force_gemv);
 
 /* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
  * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32

@@ -73,6 +73,7 @@ _SIGS = {
     "coli_hip_gdn_state_read": (_I, [_I, _P, _P]),
     "coli_hip_layer_fuse": (_I, [_I]),
     "coli_hip_moe_cert_all": (_I, [_I]),
+    "coli_hip_eg_force_gemv": (_I, [_I]),
     "coli_hip_st_open": (_P, [C.c_char_p]),
     "coli_hip_st_close": (None, [_P]),
     "coli_hip_st_count": (_I, [_P]),
@@ -406,6 +407,11 @@ class Lib:
     def layer_fuse(self, on):
         """Fused layer launches on/off (test hook); returns the previous setting."""
         return bool(self.L.coli_hip_layer_fuse(1 if on else 0))
+
+    def eg_force_gemv(self, on):
+        """Host-routed expert groups with rows > 1 on GEMV items (True) or MFMA (False);
+        returns the previous setting."""
+        return bool(self.L.coli_hip_eg_force_gemv(1 if on else 0))
 
     def moe_cert_all(self, on):
         """Certify every decode route on/off (test hook); returns the previous setting."""

@@ -1001,28 +1001,87 @@ struct EgGroup {
     void *d_xs = nullptr;     // bound prefill rows (coli_vk_eg_xs_bind)
     size_t d_xs_cap = 0;
     int xs_S = 0, xs_D = 0;
+    uint64_t xs_key = 0;      // changes with every bind (names the bound rows' contents)
     hipEvent_t done = nullptr;
 };
 static EgGroup g_grp;
 
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Rows > 1 (the engine's prefill: c/qwen.c:1099-1125, the shared expert over all rows
+// :1149-1161) go to the grouped MFMA GEMMs, as the reference switches to its multi-row
+// kernels there (c/backend_vulkan.c:1462-1466,1575-1585): each expert's weights stream once
+// per unit of up to 32 rows instead of once per row.  Pinned staging holds
+// units | xrow | x | y.
+static bool eg_submit_mfma(ColiVkTensor *const *gates, ColiVkTensor *const *ups, ColiVkTensor *const *downs,
+                           const int *rows, int count, int total, const MoeGeom &m, const float *x,
+                           const int *tok_ids) {
+    const int ur = eg_unit_rows(count, rows, m);
+    int nunits = 0;
+    for (int c = 0; c < count; c++) nunits += (rows[c] + ur - 1) / ur;
+    const size_t un_b = al256((size_t)nunits * sizeof(PfUnit)), xrow_b = al256((size_t)total * 4);
+    const size_t x_b = tok_ids ? 0 : al256((size_t)total * m.D * 4), y_b = (size_t)total * m.D * 4;
+    if (!scratch(&g_grp.d_buf, &g_grp.d_cap, un_b + xrow_b + x_b + al256(y_b))) return false;
+    if (!host_scratch(&g_grp.h_buf, &g_grp.h_cap, un_b + xrow_b + x_b + y_b)) return false;
+    uint8_t *hb = (uint8_t *)g_grp.h_buf;
+    PfUnit *hu = (PfUnit *)hb;
+    int *hrow = (int *)(hb + un_b);
+    for (int c = 0, p = 0, k = 0; c < count; c++) {
+        const ExpertRec rec = {gates[c]->w, ups[c]->w, downs[c]->w, gates[c]->sz, ups[c]->sz, downs[c]->sz};
+        for (int r = 0; r < rows[c]; r += ur, k++) {
+            memset(&hu[k], 0, sizeof(PfUnit));
+            hu[k].rec = rec;
+            hu[k].pos0 = p + r;
+            hu[k].n = rows[c] - r < ur ? rows[c] - r : ur;
+        }
+        for (int r = 0; r < rows[c]; r++, p++) {
+            hrow[p] = tok_ids ? tok_ids[p] : p;
+            if (hrow[p] < 0 || (tok_ids && hrow[p] >= g_grp.xs_S)) return false;
+        }
+    }
+    if (!tok_ids) memcpy(hb + un_b + xrow_b, x, (size_t)total * m.D * 4);
+    uint8_t *db = (uint8_t *)g_grp.d_buf;
+    float *d_y = (float *)(db + un_b + xrow_b + x_b);
+    hipError_t e = hipMemcpyAsync(db, hb, un_b + xrow_b + x_b, hipMemcpyHostToDevice, stream());
+    if (e != hipSuccess) return fail("expert group upload", e);
+    const float *src = tok_ids ? (const float *)g_grp.d_xs : (const float *)(db + un_b + xrow_b);
+    if (!eg_mfma((const PfUnit *)db, nunits, (const int *)(db + un_b), total, m, src, tok_ids ? g_grp.xs_S : total,
+                 tok_ids ? g_grp.xs_key : 0, d_y, stream()))
+        return false;
+    g_grp.y_off = un_b + xrow_b + x_b;
+    g_grp.y_bytes = y_b;
+    e = hipMemcpyAsync(hb + g_grp.y_off, d_y, y_b, hipMemcpyDeviceToHost, stream());
+    if (e == hipSuccess && !g_grp.done) e = hipEventCreateWithFlags(&g_grp.done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(g_grp.done, stream());
+    if (e != hipSuccess) return fail("expert group issue", e);
+    g_grp.inflight = 1;
+    return true;
+}
+
 // Validate a group (c/backend_vulkan.c:1418-1440) and issue it.  tok_ids != NULL: rows
-// come from the bound xs; otherwise x is packed [sum(rows), D].
+// come from the bound xs; otherwise x is packed [sum(rows), D].  Groups of one row per
+// expert run the GEMV kernels (batch-1 decode arithmetic); any expert with more rows sends
+// the whole group to the MFMA path (eg_submit_mfma), unless coli_hip_eg_path forced GEMV.
+static int g_eg_force_gemv = 0;
 static bool eg_submit(ColiVkTensor *const *gates, ColiVkTensor *const *ups, ColiVkTensor *const *downs,
                       const int *rows, int count, const float *x, const int *tok_ids) {
     if (!ok() || count < 1 || count > 64 || !gates || !ups || !downs || !rows) return false;
     MoeGeom m;
-    if (!geom_of(gates[0], downs[0], m) || !geom_supported(m)) return false;
-    int total = 0;
+    if (!geom_of(gates[0], downs[0], m)) return false;
+    int total = 0, max_rows = 0;
     for (int c = 0; c < count; c++) {
         MoeGeom mc, mu;
         if (rows[c] < 1 || !geom_of(gates[c], downs[c], mc) || !same_geom(mc, m) || !ups[c] ||
             !geom_of(ups[c], downs[c], mu) || !same_geom(mu, m))
             return false;
+        if (rows[c] > (1 << 24) - total) return false;
         total += rows[c];
+        max_rows = rows[c] > max_rows ? rows[c] : max_rows;
     }
     if (tok_ids && (!g_grp.d_xs || g_grp.xs_D != m.D)) return false;
+    if (max_rows > 1 && !g_eg_force_gemv && eg_mfma_ok(m))
+        return eg_submit_mfma(gates, ups, downs, rows, count, total, m, x, tok_ids);
+    if (!geom_supported(m)) return false;
     const size_t rec_b = al256((size_t)total * sizeof(ExpertRec)), xrow_b = al256((size_t)total * 4);
     const size_t x_b = tok_ids ? 0 : al256((size_t)total * m.D * 4);
     const size_t h_b = al256((size_t)total * m.I * 4), y_b = (size_t)total * m.D * 4;
@@ -1115,6 +1174,12 @@ COLI_API int coli_vk_expert_group_issue(ColiVkTensor *const *gates, ColiVkTensor
 
 COLI_API int coli_vk_expert_group_take(float *y) { return y && eg_take(y) ? 1 : 0; }
 
+COLI_API int coli_hip_eg_force_gemv(int force_gemv) {
+    const int prev = g_eg_force_gemv;
+    g_eg_force_gemv = force_gemv ? 1 : 0;
+    return prev;
+}
+
 COLI_API int coli_vk_expert_group(ColiVkTensor *const *gates, ColiVkTensor *const *ups, ColiVkTensor *const *downs,
                                   const int *rows, int count, float *y, const float *x) {
     if (g_grp.inflight || !x || !y) return 0;
@@ -1133,6 +1198,8 @@ COLI_API int coli_vk_eg_xs_bind(const float *xs, int S, int D) {
     if (e != hipSuccess) return fail("xs bind", e) ? 1 : 0;
     g_grp.xs_S = S;
     g_grp.xs_D = D;
+    static uint64_t binds = 0;
+    g_grp.xs_key = ++binds;
     return 1;
 }
 

@@ -11,6 +11,13 @@ struct ExpertRec {
     const float *sg, *su, *sd;
 };
 
+// A unit of the host-routed expert group on MFMA: <= 32 consecutive positions (rows of h
+// and y) of one expert.
+struct PfUnit {
+    ExpertRec rec;
+    int pos0, n, pad[2];
+};
+
 // geometry shared by every expert of a table (fmt 6, lanes layout)
 struct MoeGeom {
     int D, I, gs;
@@ -18,6 +25,16 @@ struct MoeGeom {
     int nlG, nlD;   // lanes with data per gate/up row and per down row
     int rbG, rbD;   // device row bytes of gate/up and of down
 };
+
+// The host-routed expert group (coli_vk_expert_group_issue{,_id} with rows > 1) on the
+// prefill MFMA kernels (prefill.hip): nunits units over P positions, position p taking x
+// row xrow[p] of d_x [Sx][D]; y [P][D].  key != 0 names the contents of d_x: the digit
+// planes of the last call with the same (d_x, Sx, key) are reused.  eg_unit_rows: the
+// positions per unit (32, or 16 when 32-row units would leave the CUs short of blocks).
+bool eg_mfma_ok(const MoeGeom &m);
+int eg_unit_rows(int count, const int *rows, const MoeGeom &m);
+bool eg_mfma(const PfUnit *d_units, int nunits, const int *d_xrow, int P, const MoeGeom &m, const float *d_x, int Sx,
+             uint64_t key, float *d_y, hipStream_t st);
 
 constexpr int kMaxE = 1024;
 constexpr int kMaxSlots = kTopK + 1;      // fused kernel: K <= 8 routed + the shared expert

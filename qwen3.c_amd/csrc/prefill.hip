@@ -250,7 +250,10 @@ struct PfArgs {
     const ExpertRec *rec;   // [E + 1], the shared expert last
     const int *off;         // [E + 1] first position per expert (routed)
     const int *plist;       // position -> pair (token = pair / K)
+    const PfUnit *units;    // host-routed form: [nunits] units (rec, off and the shared expert unused)
+    int nunits;
     int E, S, K, D, I;
+    int P;                  // positions (rows of h and y)
     int nlG, rbG, nlD, rbD;   // lanes layout: lanes per row, row bytes (gate/up, down)
     int nsp;                  // shared-expert passes: ceil(S / kPR)
     const int8_t *xd;         // x digit planes [3][S][D]
@@ -269,8 +272,22 @@ struct PfArgs {
 // e's passes, placed so that the nu units of one expert run on one XCD (workgroups are
 // dealt to the 8 XCDs round-robin by index) and share its rows of x in that L2.
 // False for an idle block (or a routed expert without rows).
+// Host-routed form: block b -> unit 8 (b / 8 / nu) + b % 8, u = (b / 8) % nu, one pass.
 __device__ __forceinline__ bool pf_unit(const PfArgs &a, int nu, int &e, int &u, int &p0, int &p1, int &pos0,
                                         int &n, ExpertRec &rec) {
+    if (a.units) {
+        const int b = blockIdx.x, rest = b >> 3, ui = 8 * (rest / nu) + (b & 7);
+        u = rest % nu;
+        if (ui >= a.nunits) return false;
+        const PfUnit &un = a.units[ui];
+        rec = un.rec;
+        pos0 = un.pos0;
+        n = un.n;
+        e = 0;
+        p0 = 0;
+        p1 = 1;
+        return n > 0;
+    }
     const int b = blockIdx.x, nsu = nu * a.nsp, nsu8 = (nsu + 7) & ~7;
     if (b < nsu) {
         e = a.E;
@@ -443,7 +460,7 @@ __device__ __forceinline__ void gu_body(const PfArgs &a, const GemmArgs &g) {
         const int xi = r0 + min(sr, nr - 1);
         int xrow;
         if constexpr (kDense) xrow = xi;
-        else xrow = e == a.E ? xi : a.plist[pos0 + xi] / a.K;
+        else xrow = a.units ? a.plist[pos0 + xi] : e == a.E ? xi : a.plist[pos0 + xi] / a.K;
         uint4 W[2][4];
         w_load(0, W);
         float2 sv[kSV][2];
@@ -656,7 +673,7 @@ __global__ __launch_bounds__(kPT, 2) void pf_down(PfArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15, kq = ((q & 1) << 1) | (q >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const __amdgpu_buffer_rsrc_t wr = buf_rsrc(rec.wd, (uint32_t)a.D * a.rbD);
-    const int P = a.S * a.K + a.S;
+    const int P = a.P;
     const __amdgpu_buffer_rsrc_t hr = buf_rsrc(a.hd, (uint32_t)(3u * P * a.I));
     const int rbase = u * kDR + wave * 64;   // first row of the wave
     constexpr int kHS = 3 * kPR * kDG * kGS / 16 / kPT;   // 16-byte staging chunks per thread (12)
@@ -894,6 +911,7 @@ bool moe_prefill(int layer, const ColiVkTensor *router, int K, const float *d_xs
     a.rbG = m.rbG;
     a.nlD = m.nlD;
     a.rbD = m.rbD;
+    a.P = P;
     a.nsp = (S + kPR - 1) / kPR;
     a.xd = (const int8_t *)(b + o_xd);
     a.xe = (const int *)(b + o_xe);
@@ -970,9 +988,91 @@ bool gemm6(const ColiVkTensor *const *t, float *const *d_y, int nt, const float 
     return true;
 }
 
+// ---------------------------------------------------------------- host-routed expert group
+// x digit planes of the group's source rows, kept while (rows, key) stay the same: the rows
+// bound once per prefill layer (coli_vk_eg_xs_bind) serve every chunk of that layer.
+static PfScratch g_egx, g_egh;
+static const float *g_egx_src = nullptr;
+static int g_egx_rows = 0, g_egx_n = 0;
+static uint64_t g_egx_key = 0;
+
+bool eg_mfma_ok(const MoeGeom &m) {
+    return m.gs == kGS && m.D % kGS == 0 && m.I % kGS == 0 && m.D >= kGS && m.I >= kGS && m.D <= kGemmMaxI &&
+           m.I <= kGemmMaxI;
+}
+
+int eg_unit_rows(int count, const int *rows, const MoeGeom &m) {
+    long units32 = 0;
+    for (int c = 0; c < count; c++) units32 += (rows[c] + kPR - 1) / kPR;
+    const long blocks = units32 * (m.I / kGU);   // gate/up blocks with 32-row units
+    return blocks >= 2L * n_cu() ? kPR : kPR / 2;
+}
+
+bool eg_mfma(const PfUnit *d_units, int nunits, const int *d_xrow, int P, const MoeGeom &m, const float *d_x,
+             int Sx, uint64_t key, float *d_y, hipStream_t st) {
+    if (!eg_mfma_ok(m) || nunits < 1 || P < 1 || Sx < 1 || !d_units || !d_xrow || !d_x || !d_y) return false;
+    const int D = m.D, I = m.I, ngD = D / kGS, ngI = I / kGS;
+    if ((size_t)3 * Sx * D >= (1u << 31) || (size_t)3 * P * I >= (1u << 31) || (size_t)P * D >= (1u << 31))
+        return false;
+    const size_t ox_e = al256((size_t)3 * Sx * D), ox_s = ox_e + al256((size_t)Sx * ngD * 4),
+                 ox_end = ox_s + al256((size_t)Sx * ngD * 4);
+    void *old = g_egx.buf;
+    if (!scratch(&g_egx.buf, &g_egx.cap, ox_end)) return false;
+    uint8_t *xb = (uint8_t *)g_egx.buf;
+    if (key == 0 || key != g_egx_key || d_x != g_egx_src || Sx != g_egx_rows || D != g_egx_n || old != g_egx.buf) {
+        hipLaunchKernelGGL(pf_digits_t<false>, dim3((unsigned)(((size_t)Sx * (D / 8) + 255) / 256)), dim3(256), 0, st,
+                           d_x, Sx, D, (int8_t *)xb, (int *)(xb + ox_e), (float *)(xb + ox_s), nullptr, nullptr, 0, 0,
+                           0.f);
+        g_egx_key = key;
+        g_egx_src = d_x;
+        g_egx_rows = Sx;
+        g_egx_n = D;
+    }
+    const size_t oh_d = al256((size_t)P * I * 4), oh_e = oh_d + al256((size_t)3 * P * I),
+                 oh_s = oh_e + al256((size_t)P * ngI * 4), oh_end = oh_s + al256((size_t)P * ngI * 4);
+    if (!scratch(&g_egh.buf, &g_egh.cap, oh_end)) return false;
+    uint8_t *hb = (uint8_t *)g_egh.buf;
+    PfArgs a;
+    memset(&a, 0, sizeof(a));
+    a.units = d_units;
+    a.nunits = nunits;
+    a.plist = d_xrow;
+    a.S = Sx;
+    a.K = 1;
+    a.D = D;
+    a.I = I;
+    a.P = P;
+    a.nlG = m.nlG;
+    a.rbG = m.rbG;
+    a.nlD = m.nlD;
+    a.rbD = m.rbD;
+    a.xd = (const int8_t *)xb;
+    a.xe = (const int *)(xb + ox_e);
+    a.xsum = (const float *)(xb + ox_s);
+    a.h = (float *)hb;
+    a.hd = (const int8_t *)(hb + oh_d);
+    a.he = (const int *)(hb + oh_e);
+    a.hsum = (const float *)(hb + oh_s);
+    a.y = d_y;
+    const int n8 = 8 * ((nunits + 7) / 8), nh = I / kGU, nq = (D + kDR - 1) / kDR;
+    hipLaunchKernelGGL(pf_gateup, dim3(n8 * nh), dim3(kPT), (size_t)ngD * 2 * kGU * sizeof(float2), st, a);
+    hipLaunchKernelGGL(pf_digits_t<false>, dim3((unsigned)(((size_t)P * (I / 8) + 255) / 256)), dim3(256), 0, st, a.h,
+                       P, I, (int8_t *)(hb + oh_d), (int *)(hb + oh_e), (float *)(hb + oh_s), nullptr, nullptr, 0, 0,
+                       0.f);
+    hipLaunchKernelGGL(pf_down, dim3(n8 * nq), dim3(kPT), 0, st, a);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail("expert group mfma launch", err);
+    return true;
+}
+
 void prefill_shutdown() {
     scratch_free(&g_pf.buf, &g_pf.cap);
     scratch_free(&g_gm.buf, &g_gm.cap);
+    scratch_free(&g_egx.buf, &g_egx.cap);
+    scratch_free(&g_egh.buf, &g_egh.cap);
+    g_egx_src = nullptr;
+    g_egx_rows = g_egx_n = 0;
+    g_egx_key = 0;
 }
 
 }  // namespace coli

@@ -1,0 +1,84 @@
+"""The reference engine's prefill MoE call sequence over the ABI, restated in Python for the
+GPU tests and the bench (the engine itself, c/qwen.c, is C and calls the same entry points).
+
+engine_moe_batch follows moe_batch_from_logits (c/qwen.c:1050-1183) from the routing on:
+the (token, slot) pairs are bucketed by expert (:1076-1083), the routed experts go out in
+ascending id in chunks of at most MOEB_MAXE experts and MOEB_MAXROWS rows, an expert with
+more rows than fit being split and resumed in the next chunk (:1099-1112); each chunk is
+one coli_vk_expert_group_issue_id over the bound rows (:1094,1120) and one take, whose rows
+are added as out[tok] += w * y (:1024-1027,1133); the shared expert then runs over all S
+rows as one coli_vk_expert_group_issue of packed rows and is added with its sigmoid gate
+(:1149-1161).  The float32 adds happen in the engine's order, so the result can be compared
+with the oracle's restatement of the whole block.
+"""
+import numpy as np
+
+MOEB_MAXE = 64       # c/qwen.c:1044
+MOEB_MAXROWS = 1024  # c/qwen.c:1045
+
+
+def group_by_expert(tidx, E):
+    """(ecnt [E + 1] offsets, epair [S K] pair indices by expert) as c/qwen.c:1076-1083."""
+    flat = np.asarray(tidx, np.int64).reshape(-1)
+    cnt = np.bincount(flat, minlength=E)
+    ecnt = np.zeros(E + 1, np.int64)
+    ecnt[1:] = np.cumsum(cnt)
+    epair = np.argsort(flat, kind="stable")   # pairs of one expert in pair order
+    return ecnt, epair
+
+
+def chunks(ecnt, E):
+    """The engine's chunks: lists of (expert, first row, rows), c/qwen.c:1099-1112."""
+    gpu = [e for e in range(E) if ecnt[e + 1] > ecnt[e]]
+    out, gi, roff = [], 0, 0
+    while gi < len(gpu):
+        ch, total = [], 0
+        while gi < len(gpu) and len(ch) < MOEB_MAXE and total < MOEB_MAXROWS:
+            e = gpu[gi]
+            have = int(ecnt[e + 1] - ecnt[e]) - roff
+            nr = min(have, MOEB_MAXROWS - total)
+            ch.append((e, roff, nr))
+            total += nr
+            roff += nr
+            if roff == ecnt[e + 1] - ecnt[e]:
+                gi += 1
+                roff = 0
+        out.append(ch)
+    return out
+
+
+def engine_moe_batch(lib, tensors, xs, S, D, K, tidx, tval, sh_gate, shared_x=True):
+    """out [S, D] of the routed experts and the shared expert (tensors[e] = (g, u, d) for
+    e < E, tensors[E] the shared expert), through the ABI as the engine calls it."""
+    E = len(tensors) - 1
+    xs = np.ascontiguousarray(xs, np.float32).reshape(S, D)
+    tval = np.asarray(tval, np.float32).reshape(-1)
+    ecnt, epair = group_by_expert(tidx, E)
+    out = np.zeros((S, D), np.float32)
+    lib.eg_xs_bind(xs, S, D)
+    for ch in chunks(ecnt, E):
+        rtok, rw = [], []
+        for e, r0, nr in ch:
+            pairs = epair[ecnt[e] + r0:ecnt[e] + r0 + nr]
+            rtok.extend((pairs // K).tolist())
+            rw.extend(tval[pairs].tolist())
+        es = [c[0] for c in ch]
+        if not lib.expert_group_issue_id([tensors[e][0] for e in es], [tensors[e][1] for e in es],
+                                         [tensors[e][2] for e in es], [c[2] for c in ch], rtok):
+            raise RuntimeError("coli_vk_expert_group_issue_id refused a chunk")
+        y = lib.expert_group_take(len(rtok), D).reshape(-1, D)
+        w = np.asarray(rw, np.float32)
+        for r, t in enumerate(rtok):
+            out[t] += w[r] * y[r]
+    if shared_x:
+        g, u, d = tensors[E]
+        if not lib.expert_group_issue([g], [u], [d], [S], xs):
+            raise RuntimeError("coli_vk_expert_group_issue refused the shared expert")
+        y = lib.expert_group_take(S, D).reshape(S, D)
+        sg = np.asarray(sh_gate, np.float32)
+        for s in range(S):
+            # c/qwen.c:1158: gt += sh_gate[d] * x[d] in index order (accumulate is sequential)
+            gt = np.add.accumulate((sg * xs[s]).astype(np.float32), dtype=np.float32)[-1]
+            sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-gt, dtype=np.float32))   # sigmoidf_, c/qwen.c:172
+            out[s] += sig * y[s]
+    return out

@@ -89,3 +89,76 @@ def test_prefill_cfg4_router_int8(lib, orc_omp, gen, torch_dev, cfg4):
     rt, rf = L.int8_router(lib, gen, 0xC0F6)
     xs = gen.normal(S * L.D, 0xC0F7)
     check(orc_omp, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S, router=rt), router=rf)
+
+
+# ---------------------------------------------------------------- the engine's prefill calls
+# The unchanged engine runs prefill MoE through the host-routed expert group
+# (c/qwen.c:1094-1161): chunks of <= 64 experts and <= 1024 rows over the bound rows, then
+# the shared expert over all S rows.  Groups with more than one row per expert run as the
+# grouped MFMA GEMMs (the reference's multi-row kernels, c/backend_vulkan.c:1462-1466).
+
+def _rows_check(orc, L, eids, rows, xrows, y):
+    p, worst = 0, 0.0
+    for e, r in zip(eids, rows):
+        for _ in range(r):
+            ref = np.empty(L.D, np.float32)
+            orc.orc_expert_mlp_fmt6(_util.eptr(L.ex, e), _util.P(xrows[p].copy()), L.D, L.I, L.gs, _util.P(ref))
+            worst = max(worst, _util.maxrel_scaled(y[p * L.D:(p + 1) * L.D], ref))
+            p += 1
+    return worst
+
+
+def test_expert_group_rows_mfma(lib, orc_omp, gen, cfg4):
+    """Packed rows, 1 to 40 per expert (units of 32 and 16 rows, a single-row expert in the
+    group): MFMA path against the oracle per row, and the GEMV items (forced) likewise."""
+    L = cfg4[0]
+    eids, rows = [3, 256, 100, 7, 200, 255], [2, 40, 17, 1, 33, 16]
+    n = sum(rows)
+    x = gen.normal(n * L.D, 0xE900)
+    xr = x.reshape(n, L.D)
+    g, u, d = ([L.t[e][i] for e in eids] for i in range(3))
+    y = lib.expert_group(g, u, d, rows, x)
+    w_mfma = _rows_check(orc_omp, L, eids, rows, xr, y)
+    prev = lib.eg_force_gemv(True)
+    try:
+        y2 = lib.expert_group(g, u, d, rows, x)
+    finally:
+        lib.eg_force_gemv(prev)
+    w_gemv = _rows_check(orc_omp, L, eids, rows, xr, y2)
+    print(f"  rows {rows}: worst maxrel_scaled mfma {w_mfma:.2e}, gemv {w_gemv:.2e}", flush=True)
+    assert w_mfma <= TOL and w_gemv <= TOL
+
+
+@pytest.mark.parametrize("S", [64, 512])
+def test_engine_moe_batch_cfg4(lib, orc_omp, gen, cfg4, S):
+    """configs[4]'s layer through the engine's own call sequence (_engine.engine_moe_batch):
+    per token within 1e-3 of the oracle's moe_batch_from_logits.  At S = 512 the 4096 pairs
+    need several chunks and at least one expert is split across two chunks (c/qwen.c:1104)."""
+    import _engine
+    L, K = cfg4[0], 8
+    xs = gen.normal(S * L.D, 0xE910 + S)
+    out, tidx, tval = L.oracle_prefill(orc_omp, xs, S, K)
+    ecnt, _ = _engine.group_by_expert(tidx, L.E)
+    chs = _engine.chunks(ecnt, L.E)
+    got = _engine.engine_moe_batch(lib, L.t, xs, S, L.D, K, tidx, tval, L.mw.sh_gate)
+    ref = out.reshape(S, L.D)
+    worst = max(_util.maxrel_scaled(got[t], ref[t]) for t in range(S))
+    split = sum(1 for a, b in zip(chs, chs[1:]) if a[-1][0] == b[0][0])
+    print(f"  S={S}: {len(chs)} chunks, {split} split experts, worst per-token maxrel_scaled {worst:.2e}", flush=True)
+    assert worst <= TOL
+    if S == 512:
+        assert len(chs) >= 4 and split >= 1
+
+
+def test_engine_moe_batch_rebind(lib, orc_omp, gen, cfg4):
+    """Two prefill layers' worth of calls in a row on rows of the same shape: the second
+    bind's rows are the ones used (the digit planes of the bound rows are not stale)."""
+    import _engine
+    L, K, S = cfg4[0], 8, 96
+    for seed in (0xE920, 0xE921):
+        xs = gen.normal(S * L.D, seed)
+        out, tidx, tval = L.oracle_prefill(orc_omp, xs, S, K)
+        got = _engine.engine_moe_batch(lib, L.t, xs, S, L.D, K, tidx, tval, L.mw.sh_gate)
+        ref = out.reshape(S, L.D)
+        worst = max(_util.maxrel_scaled(got[t], ref[t]) for t in range(S))
+        assert worst <= TOL, (seed, worst)
