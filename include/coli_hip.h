@@ -291,6 +291,11 @@ int   coli_hip_moe_cert_all(int on);
  * (expert, row) as for single rows; returns the previous setting.  A test and bench hook
  * with no counterpart in the reference (its multi-row switch is automatic). */
 int   coli_hip_eg_force_gemv(int force_gemv);
+/* coli_vk_gqa_full with S >= 4 rows runs them in one batched pass (1, the default: q/k/v
+ * and o-projection GEMMs on MFMA, causal attention over all rows) or token by token through
+ * the decode block (0); returns the previous setting.  A test and bench hook with no
+ * counterpart in the reference. */
+int   coli_hip_gqa_seq(int on);
 
 /* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
  * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32

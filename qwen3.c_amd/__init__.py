@@ -74,6 +74,7 @@ _SIGS = {
     "coli_hip_layer_fuse": (_I, [_I]),
     "coli_hip_moe_cert_all": (_I, [_I]),
     "coli_hip_eg_force_gemv": (_I, [_I]),
+    "coli_hip_gqa_seq": (_I, [_I]),
     "coli_hip_st_open": (_P, [C.c_char_p]),
     "coli_hip_st_close": (None, [_P]),
     "coli_hip_st_count": (_I, [_P]),
@@ -412,6 +413,11 @@ class Lib:
         """Host-routed expert groups with rows > 1 on GEMV items (True) or MFMA (False);
         returns the previous setting."""
         return bool(self.L.coli_hip_eg_force_gemv(1 if on else 0))
+
+    def gqa_seq(self, on):
+        """coli_vk_gqa_full over S >= 4 rows batched (True) or token by token (False);
+        returns the previous setting."""
+        return bool(self.L.coli_hip_gqa_seq(1 if on else 0))
 
     def moe_cert_all(self, on):
         """Certify every decode route on/off (test hook); returns the previous setting."""

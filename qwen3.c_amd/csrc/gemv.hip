@@ -746,6 +746,7 @@ bool gemv(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_
         return launch_lanes_mode<2>(t, d_x, d_y, st, ta) != 0;
     }
     if (S >= kGemmMinS && gemm6_ok(t)) return gemm6(&t, &d_y, 1, d_x, S, st);   // c/backend_vulkan.c:282-299
+    if (S >= 2 && !want_k && gemm_f01_ok(t, d_x)) return gemm_f01(t, d_x, d_y, S, st);
     for (int s = 0; s < S; s++)
         if (!launch_one(t, d_x + (size_t)s * t->I, d_y + (size_t)s * t->O, st)) return false;
     return want_k ? topk(d_y, t->O, tk->k, tk->idx, tk->val, st) : true;
@@ -890,7 +891,8 @@ int gemv_error_take() {
     if (!g_keys) return 0;
     int *w = (int *)((unsigned long long *)g_keys + kFusedGrid * kTopK + 1);
     int e = 0;
-    if (hipStreamSynchronize(stream()) != hipSuccess || hipMemcpy(&e, w, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    // the device, not the library stream: a fused top-k may have run on a caller's stream
+    if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(&e, w, 4, hipMemcpyDeviceToHost) != hipSuccess)
         return -1;
     if (e) {
         const int z = 0;

@@ -100,6 +100,10 @@ struct GatedX {
     float eps;
 };
 bool gemm6_ok(const ColiVkTensor *t);
+// fmt 0 / fmt 1 rows over S >= 2 rows of x in one launch, the reference's sequential fp32
+// sums bit for bit (d_x 16-byte aligned)
+bool gemm_f01_ok(const ColiVkTensor *t, const float *d_x);
+bool gemm_f01(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_t st);
 bool gemm6(const ColiVkTensor *const *t, float *const *d_y, int nt, const float *d_x, int S, hipStream_t st,
            const GatedX *gx = nullptr);
 

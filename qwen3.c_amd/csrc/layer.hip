@@ -1270,6 +1270,205 @@ __global__ __launch_bounds__(kMT) void attn_merge_d(AttnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- GQA over S query rows
+// The block over S > 1 rows at positions pos_base .. pos_base + S - 1, causal (the prompt, or
+// a continuation chunk; c/qwen.c:581-667 restated, batched as c/backend_vulkan.c:2280-2340):
+// projections as GEMMs, qk_rows for the norms, RoPE and KV writes of all rows, attn_rows for
+// the attention and its output gate, then the o-projection GEMM.
+
+// q/k norm + partial RoPE of one head row of token s (c/qwen.c:598-614, the arithmetic of
+// row_finish), block (s, j) of one wave: j < H is q head j into qn [S][H][hd]; j >= H is k
+// head j - H into the cache row pos_base + s, with its v row.  rope [S][rot / 2] holds the
+// (cos, sin) of each position, computed on the host as for the decode block.
+__global__ __launch_bounds__(64) void qk_rows(const float *__restrict__ qraw, const float *__restrict__ kraw,
+                                              const float *__restrict__ vraw, const float *__restrict__ qnw,
+                                              const float *__restrict__ knw, const float2 *__restrict__ rope,
+                                              float *__restrict__ qn, float *__restrict__ Kc, float *__restrict__ Vc,
+                                              int H, int KH, int hd, int rot, int pos_base, int max_t, float eps) {
+    __shared__ float s_row[kAttMaxHD];
+    const int s = blockIdx.x, j = blockIdx.y, lane = threadIdx.x, hr = rot / 2;
+    const bool isq = j < H;
+    const int kh = j - H;
+    const float *src = isq ? qraw + ((size_t)s * H + j) * 2 * hd : kraw + ((size_t)s * KH + kh) * hd;
+    const float *w = isq ? qnw : knw;
+    float *dst = isq ? qn + ((size_t)s * H + j) * hd : Kc + ((size_t)kh * max_t + pos_base + s) * hd;
+    constexpr int kPer = kAttMaxHD / 64;
+    float v[kPer];
+    double ss = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int d = lane + 64 * q;
+        v[q] = d < hd ? src[d] : 0.f;
+        ss += (double)v[q] * v[q];
+    }
+    ss = wave_sum_d(ss);
+    const float r = 1.f / sqrtf((float)(ss / hd) + eps);
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        const int d = lane + 64 * q;
+        if (d < hd) s_row[d] = v[q] * r * (1.f + w[d]);
+    }
+    __syncthreads();
+    const float2 *cs = rope + (size_t)s * hr;
+    for (int d = lane; d < hd; d += 64) {
+        float o = s_row[d];
+        if (d < hr) {
+            const float2 c = cs[d];
+            o = s_row[d] * c.x - s_row[d + hr] * c.y;
+        } else if (d < rot) {
+            const float2 c = cs[d - hr];
+            o = s_row[d] * c.x + s_row[d - hr] * c.y;
+        }
+        dst[d] = o;
+    }
+    if (!isq) {
+        const float *vs = vraw + ((size_t)s * KH + kh) * hd;
+        float *vd = Vc + ((size_t)kh * max_t + pos_base + s) * hd;
+        for (int d = lane; d < hd; d += 64) vd[d] = vs[d];
+    }
+}
+
+// Causal attention of 16 query rows of one head on fp32 MFMA (v_mfma_f32_16x16x4_f32), one
+// block of 4 waves per (head, 16-row query tile); wave w takes the key tiles w, w + 4, ...
+// of 16 positions and keeps its own running max, sum and context; the block merges the
+// four in wave order and applies the output gate (c/qwen.c:641-660).
+//   scores^T = K Q^T: A = 16 keys x 4 dims, B = 4 dims x 16 queries; lane l, register r of
+//     the product is (key 4 (l / 16) + r, query l % 16).  The K dimension is permuted: step
+//     kk of lane group g = l / 16 is dim (hd / 4) g + kk, so each lane holds a contiguous
+//     quarter of its query row (registers) and reads a contiguous quarter of its key row.
+//   ctx^T += V^T P^T: A = 16 dims x 4 keys (V tile from LDS), B = the lane's own 4 scores
+//     (step kk of group g is key 4 g + kk); lane l, register r of dim tile t is
+//     (dim 16 t + 4 (l / 16) + r, query l % 16).  Every per-query value (max, sum, rescale)
+//     stays in the lanes of its query.
+typedef float coli_v4f __attribute__((ext_vector_type(4)));
+constexpr int kPQ = 16, kPKey = 16;
+struct AttnRowsArgs {
+    const float *qraw;    // [S][H][2 hd]: q | gate per head
+    const float *qn;      // [S][H][hd] normed, rotated
+    const float *Kc, *Vc; // [KH][max_t][hd]
+    float *ctx;           // [S][H hd] gated context
+    int S, H, KH, pos_base, max_t, nqt;
+    float scale;
+};
+template <int HD>
+__global__ __launch_bounds__(256) void attn_rows(AttnRowsArgs a) {
+    constexpr int NK = HD / 4, NDT = HD / 16, kVP = HD + 4;   // LDS pitch of a V row
+    __shared__ __attribute__((aligned(16))) float s_v[4][kPKey][kVP];
+    __shared__ float s_m[4][kPQ], s_l[4][kPQ];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = blockIdx.x % a.H, qt = a.nqt - 1 - blockIdx.x / a.H;   // the longest tiles first
+    const int G = a.H / a.KH, kh = h / G, qi = lane & 15, grp = lane >> 4;
+    const int s0 = qt * kPQ, sq = min(s0 + qi, a.S - 1), qpos = a.pos_base + sq;
+    const int last = a.pos_base + min(s0 + kPQ, a.S) - 1, nkt = last / kPKey + 1;
+    float qf[NK];
+    {
+        const float4 *qp = (const float4 *)(a.qn + ((size_t)sq * a.H + h) * HD + NK * grp);
+#pragma unroll
+        for (int i = 0; i < NK / 4; i++) {
+            const float4 v = qp[i];
+            qf[4 * i] = v.x, qf[4 * i + 1] = v.y, qf[4 * i + 2] = v.z, qf[4 * i + 3] = v.w;
+        }
+    }
+    coli_v4f acc[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; t++) acc[t] = coli_v4f{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    const float *Kh = a.Kc + (size_t)kh * a.max_t * HD, *Vh = a.Vc + (size_t)kh * a.max_t * HD;
+    constexpr int kV4 = kPKey * HD / 4 / 64;   // float4 of the V tile per lane
+    for (int kt = wave; kt < nkt; kt += 4) {
+        const int t0 = kt * kPKey;
+        // key rows past the tile's last query position are masked; their loads stay inside
+        // the rows written so far (K clamped, V read as zeros: 0 * stale data is not 0)
+        float kf[NK];
+        const float4 *kp = (const float4 *)(Kh + (size_t)min(t0 + qi, last) * HD + NK * grp);
+#pragma unroll
+        for (int i = 0; i < NK / 4; i++) {
+            const float4 v = kp[i];
+            kf[4 * i] = v.x, kf[4 * i + 1] = v.y, kf[4 * i + 2] = v.z, kf[4 * i + 3] = v.w;
+        }
+        float4 vt[kV4];
+#pragma unroll
+        for (int i = 0; i < kV4; i++) {
+            const int f = lane + 64 * i, key = f / (HD / 4), c4 = f % (HD / 4);
+            vt[i] = t0 + key <= last ? *(const float4 *)(Vh + (size_t)(t0 + key) * HD + 4 * c4)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        coli_v4f sc = coli_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NK; kk++) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kk], qf[kk], sc, 0, 0, 0);
+        wave_lds_order();   // the previous tile's P.V reads of s_v come before these writes
+#pragma unroll
+        for (int i = 0; i < kV4; i++) {
+            const int f = lane + 64 * i, key = f / (HD / 4), c4 = f % (HD / 4);
+            *(float4 *)&s_v[wave][key][4 * c4] = vt[i];
+        }
+        // scale, causal mask, online softmax of the lane's query over the tile's 16 keys
+        float p[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int kpos = t0 + 4 * grp + r;
+            p[r] = kpos <= qpos ? sc[r] * a.scale : -INFINITY;
+            mx = fmaxf(mx, p[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const bool live = mn != -INFINITY;   // some key of the query seen so far
+        const float al = live && m != -INFINITY ? expf(m - mn) : (live ? 0.f : 1.f);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = live && p[r] != -INFINITY ? expf(p[r] - mn) : 0.f;
+            ps += p[r];
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * al + ps;
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < NDT; t++) acc[t] *= al;
+        wave_lds_order();   // the V tile is in LDS before the P.V reads (one wave: in order)
+#pragma unroll
+        for (int t = 0; t < NDT; t++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_v[wave][4 * grp + kk][16 * t + qi], p[kk], acc[t], 0,
+                                                              0, 0);
+    }
+    // merge the four waves (wave order), gate, store
+    if (grp == 0) {
+        s_m[wave][qi] = m;
+        s_l[wave][qi] = l;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) M = fmaxf(M, s_m[w][qi]);
+    const float fw = m == -INFINITY ? 0.f : expf(m - M);
+    float (*s_c)[kPQ][HD] = (float (*)[kPQ][HD])&s_v[0][0][0];   // [4][16][HD] over the V tiles
+    static_assert(sizeof(s_v) >= 4 * kPQ * HD * 4, "context staging fits the V tiles");
+    __syncthreads();   // every wave is done with its V tile
+#pragma unroll
+    for (int t = 0; t < NDT; t++)
+        *(float4 *)&s_c[wave][qi][16 * t + 4 * grp] =
+            make_float4(acc[t][0] * fw, acc[t][1] * fw, acc[t][2] * fw, acc[t][3] * fw);
+    __syncthreads();
+    for (int o = tid; o < kPQ * HD; o += 256) {
+        const int q = o / HD, d = o % HD, s = s0 + q;
+        if (s >= a.S) continue;
+        float L = 0.f, Mq = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) Mq = fmaxf(Mq, s_m[w][q]);
+#pragma unroll
+        for (int w = 0; w < 4; w++) L += s_m[w][q] == -INFINITY ? 0.f : s_l[w][q] * expf(s_m[w][q] - Mq);
+        float c = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) c += s_c[w][q][d];
+        const float gate = a.qraw[((size_t)s * a.H + h) * 2 * HD + HD + d];
+        a.ctx[(size_t)s * a.H * HD + (size_t)h * HD + d] = c / L * (1.f / (1.f + expf(-gate)));
+    }
+}
+
 // ---------------------------------------------------------------- small kernels
 __global__ void rms_rows(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ y, int D,
                          float eps) {
@@ -1411,7 +1610,7 @@ static bool put_vec(float **d, int *have, const float *h, int n, const char *who
 // ---------------------------------------------------------------- work buffers
 enum {
     W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_AB, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
-    W_HIST, W_BND, W_SQKV, W_SZ, W_SY, W_COUNT
+    W_HIST, W_BND, W_SQKV, W_SZ, W_SY, W_ROPE, W_COUNT
 };
 struct WorkBuf {
     void *p = nullptr;
@@ -2036,12 +2235,92 @@ static int gqa_rows(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTe
     return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
 }
 
+// S >= kGemmMinS rows in one pass (c/backend_vulkan.c:2280-2340): q/k/v as one digit
+// decomposition and three GEMMs, qk_rows, attn_rows, the o-projection GEMM.  0 with no
+// device work done when a shape is outside these kernels (the caller then takes gqa_rows).
+enum { kSeqNo = -1 };
+static int g_gqa_seq = 1;   // 0: every S takes the token loop (coli_hip_gqa_seq)
+static int gqa_seq(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTensor *tk, ColiVkTensor *tv,
+                   ColiVkTensor *to, float *out, int S, const GqaDims &d, int pos_base, int Dout) {
+    const int H = d.H, KH = d.KH, hd = d.hd, hr = d.rot / 2;
+    if (layer < 0 || layer >= kMaxLayers || S < kGemmMinS || (hd != 64 && hd != 128 && hd != 256)) return kSeqNo;
+    const KvState &kv = g_kv[layer];
+    const QkNorm &qk = g_qk[layer];
+    if (!kv.K || kv.kd != hd || kv.vd != hd || (long)KH * d.max_t > kv.rows || !qk.qn || qk.hd != hd) return kSeqNo;
+    if (H < 1 || KH < 1 || H % KH || d.rot < 2 || d.rot > hd || d.rot % 2 || pos_base < 0 ||
+        (long)pos_base + S > d.max_t)
+        return kSeqNo;
+    if (!gemm6_ok(tq) || !gemm6_ok(tk) || !gemm6_ok(tv) || !gemm6_ok(to) || tq->I != D || tk->I != D ||
+        tv->I != D || tq->O != 2 * H * hd || tk->O != KH * hd || tv->O != KH * hd || to->I != H * hd ||
+        to->O != Dout)
+        return kSeqNo;
+    float *dx = wbuf(W_IO_X, (size_t)S * D), *dout = wbuf(W_IO_O, (size_t)S * Dout);
+    float *qraw = wbuf(W_SQKV, (size_t)S * 2 * H * hd), *kr = wbuf(W_SZ, (size_t)S * 2 * KH * hd);
+    float *qn = wbuf(W_SY, (size_t)S * H * hd), *ctx = wbuf(W_CTX, (size_t)S * H * hd);
+    float *rope = wbuf(W_ROPE, (size_t)S * hr * 2);
+    if (!dx || !dout || !qraw || !kr || !qn || !ctx || !rope) return 0;
+    float *vr = kr + (size_t)S * KH * hd;
+    float *tab = (float *)malloc((size_t)S * hr * 2 * 4);
+    if (!tab) return 0;
+    for (int s = 0; s < S; s++)   // c/qwen.c:570-579 as the decode block: in double, rounded to float
+        for (int j = 0; j < hr; j++) {
+            const float inv = (float)pow((double)d.theta, (double)(-2.0f * j / d.rot));
+            const float ang = (float)(pos_base + s) * inv;
+            tab[((size_t)s * hr + j) * 2] = (float)cos((double)ang);
+            tab[((size_t)s * hr + j) * 2 + 1] = (float)sin((double)ang);
+        }
+    const bool up = h2d(dx, x, (size_t)S * D * 4, "gqa seq x") && h2d(rope, tab, (size_t)S * hr * 8, "gqa seq rope");
+    free(tab);
+    if (!up) return 0;
+    const ColiVkTensor *tp[3] = {tq, tk, tv};
+    float *const yp[3] = {qraw, kr, vr};
+    if (!gemm6(tp, yp, 3, dx, S, stream())) return 0;
+    hipLaunchKernelGGL(qk_rows, dim3(S, H + KH), dim3(64), 0, stream(), qraw, kr, vr, qk.qn, qk.kn,
+                       (const float2 *)rope, qn, kv.K, kv.V, H, KH, hd, d.rot, pos_base, d.max_t, d.eps);
+    AttnRowsArgs a;
+    a.qraw = qraw;
+    a.qn = qn;
+    a.Kc = kv.K;
+    a.Vc = kv.V;
+    a.ctx = ctx;
+    a.S = S;
+    a.H = H;
+    a.KH = KH;
+    a.pos_base = pos_base;
+    a.max_t = d.max_t;
+    a.nqt = (S + kPQ - 1) / kPQ;
+    a.scale = 1.f / sqrtf((float)hd);
+    const dim3 ga((unsigned)(H * a.nqt));
+    if (hd == 64) hipLaunchKernelGGL(attn_rows<64>, ga, dim3(256), 0, stream(), a);
+    else if (hd == 128) hipLaunchKernelGGL(attn_rows<128>, ga, dim3(256), 0, stream(), a);
+    else hipLaunchKernelGGL(attn_rows<256>, ga, dim3(256), 0, stream(), a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail("attention rows launch", e) ? 1 : 0;
+    const ColiVkTensor *op[1] = {to};
+    float *const oy[1] = {dout};
+    if (!gemm6(op, oy, 1, ctx, S, stream()) || !sync_stream("gqa seq")) return 0;
+    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+}
+
 // c/backend_vulkan.h:171-178: x is the normed input [S, D]; out [S, Dout] = block output
 COLI_API int coli_vk_gqa_full(int layer, const float *x, int D, ColiVkTensor *gq_t, ColiVkTensor *gk_t,
                               ColiVkTensor *gv_t, ColiVkTensor *out_t, float *out, int S, int H, int KH, int hd,
                               int rot, int pos_base, int max_t, float eps, float theta, int Dout) {
     const GqaDims d = {H, KH, hd, rot, max_t, eps, theta};
+    if (!ok() || !x || !out || S < 1 || D < 1) return 0;
+    if (g_gqa_seq) {
+        const int r = gqa_seq(layer, x, D, gq_t, gk_t, gv_t, out_t, out, S, d, pos_base, Dout);
+        if (r != kSeqNo) return r;
+    }
     return gqa_rows(layer, x, D, gq_t, gk_t, gv_t, out_t, out, S, d, pos_base, Dout);
+}
+
+// Test and bench hook: S > 1 rows of coli_vk_gqa_full in one batched pass (1, the default) or
+// as the token loop (0); returns the previous setting.
+COLI_API int coli_hip_gqa_seq(int on) {
+    const int prev = g_gqa_seq;
+    g_gqa_seq = on ? 1 : 0;
+    return prev;
 }
 
 // The staged forms take host-computed q (already normed and rotated) and the host KV

@@ -988,6 +988,25 @@ bool gemm6(const ColiVkTensor *const *t, float *const *d_y, int nt, const float 
     return true;
 }
 
+// ---------------------------------------------------------------- fmt 0 / fmt 1 over S rows
+// The engine's router (c/qwen.c:1189) and GatedDeltaNet a/b (:1359) over S prefill rows are
+// fmt 1 (int8 rows, c/qwen.c:1876-1878) or fmt 0: one pf_logits launch for all rows, the
+// reference's sequential fp32 sums (c/qwen.c:178-189, 230-238) bit for bit.
+bool gemm_f01_ok(const ColiVkTensor *t, const float *d_x) {
+    return tensor_live(t) && (t->fmt == 0 || t->fmt == 1) && t->layout == kLayoutRows && t->I % 4 == 0 &&
+           t->row_bytes % (t->fmt == 0 ? 16 : 4) == 0 && ((uintptr_t)d_x & 15) == 0 &&
+           (t->O + kLE - 1) / kLE <= 65535;
+}
+
+bool gemm_f01(const ColiVkTensor *t, const float *d_x, float *d_y, int S, hipStream_t st) {
+    if (!gemm_f01_ok(t, d_x) || S < 1 || !d_y) return false;
+    hipLaunchKernelGGL(pf_logits, dim3((S + kLT - 1) / kLT, (t->O + kLE - 1) / kLE), dim3(256), 0, st, d_x, S, t->I,
+                       t->w, t->sz, t->fmt, t->row_bytes, t->O, d_y);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail("fmt 0/1 rows launch", err);
+    return true;
+}
+
 // ---------------------------------------------------------------- host-routed expert group
 // x digit planes of the group's source rows, kept while (rows, key) stay the same: the rows
 // bound once per prefill layer (coli_vk_eg_xs_bind) serve every chunk of that layer.

@@ -120,6 +120,54 @@ def test_fmt0_router(lib, orc, gen):
     assert normrel(y, yo) <= TOL_NORM
 
 
+def _int8_rows(orc, gen, O, I, seed):
+    W = gen.normal(O * I, seed, 0.02)
+    q = np.empty(O * I, np.uint8)
+    s = np.empty(O, np.float32)
+    orc.orc_quant_rows(P(W), I, O, 1, 0, P(q), P(s))
+    return q, s
+
+
+@pytest.mark.parametrize("fmt,O,I,S", [(1, 256, 2048, 512), (1, 32, 2048, 37), (0, 256, 2048, 5), (0, 100, 132, 2),
+                                       (1, 17, 260, 3)])
+def test_rows_f01(lib, orc, gen, fmt, O, I, S):
+    """fmt 1 / fmt 0 rows over S >= 2 rows of x (the engine's router and GDN a/b over the
+    prefill rows, c/qwen.c:1189,1359): one launch, the reference's sequential fp32 sums
+    (c/qwen.c:178-189, 230-238) bit for bit."""
+    x = gen.normal(S * I, 0x3100 + S)
+    if fmt == 1:
+        q, s = _int8_rows(orc, gen, O, I, 0x3101)
+        t = lib.tensor(q, s, 1, I, O, 0)
+    else:
+        W = gen.normal(O * I, 0x3102, 0.02)
+        t = lib.tensor(W, None, 0, I, O, 0)
+    y = lib.matmul(t, x, S).reshape(S, O)
+    for r in range(S):
+        yo = np.empty(O, np.float32)
+        xr = np.ascontiguousarray(x[r * I:(r + 1) * I])
+        if fmt == 1:
+            orc.orc_matmul_q8(P(yo), P(xr), P(q), P(s), I, O)
+        else:
+            orc.orc_matmul_f32(P(yo), P(xr), P(W), 1, I, O)
+        assert np.array_equal(y[r], yo), (r, maxrel(y[r], yo))
+
+
+def test_rows_f01_pair(lib, orc, gen):
+    """GatedDeltaNet b and a over S rows as one coli_vk_matmul_pair (c/qwen.c:1359), fmt 1."""
+    S, I, VH = 37, 2048, 32
+    qb, sb = _int8_rows(orc, gen, VH, I, 0x3201)
+    qa, sa = _int8_rows(orc, gen, VH, I, 0x3202)
+    tb, ta = lib.tensor(qb, sb, 1, I, VH, 0), lib.tensor(qa, sa, 1, I, VH, 0)
+    x = gen.normal(S * I, 0x3203)
+    yb, ya = lib.matmul_pair(tb, ta, x, S)
+    for r in range(S):
+        xr = np.ascontiguousarray(x[r * I:(r + 1) * I])
+        for y, q, s in ((yb, qb, sb), (ya, qa, sa)):
+            yo = np.empty(VH, np.float32)
+            orc.orc_matmul_q8(P(yo), P(xr), P(q), P(s), I, VH)
+            assert np.array_equal(y.reshape(S, VH)[r], yo), r
+
+
 def test_matmul_pair(lib, orc, gen):
     I, gs = 2048, 128
     q1, s1 = gen.fmt6(512, I, gs, 21)

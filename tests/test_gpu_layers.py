@@ -90,6 +90,53 @@ def test_gqa_long_cache(lib, lorc, gen):
         assert err <= TOL, (pos, err)
 
 
+@pytest.fixture(scope="module")
+def lorc_omp(orc_omp):
+    _layers.bind(orc_omp)
+    return orc_omp
+
+
+GQA_ROWS = {   # D, H, KH, hd, rot, gs, max_t, layer, S, pos_base, S2 (a continuation call)
+    "cfg3": (2048, 16, 2, 256, 64, 128, 4096, 20, 512, 0, 64),
+    "hd128": (512, 32, 2, 128, 32, 128, 200, 21, 37, 3, 9),
+    "hd64": (256, 4, 2, 64, 16, 128, 100, 22, 20, 30, 5),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(GQA_ROWS))
+def test_gqa_full_rows(lib, lorc_omp, gen, shape):
+    """coli_vk_gqa_full with S >= 4 rows: one batched pass (q/k/v and o-projection GEMMs on
+    MFMA, the norms, RoPE and KV writes of all rows, causal attention on fp32 MFMA) against
+    the oracle's token loop (c/qwen.c:581-667), then a continuation call of S2 rows; cache
+    rows before pos_base are seeded, partial 16-row query tiles occur; the KV rows the passes
+    write against the oracle's cache."""
+    D, H, KH, hd, rot, gs, max_t, layer, S, pos_base, S2 = GQA_ROWS[shape]
+    W = _layers.GqaWeights(gen, gen.stream(0x9E00, layer), D, H, KH, hd, rot, gs)
+    tq, tk, tv, to = (m.upload(lib) for m in (W.q, W.k, W.v, W.o))
+    lib.kv_ensure(layer, KH * max_t, hd, hd)
+    lib.gqa_norm_weight(layer, W.qn, W.kn)
+    Kc = gen.normal(KH * max_t * hd, 0x9E10 + layer, 1.0)
+    Vc = gen.normal(KH * max_t * hd, 0x9E11 + layer, 1.0)
+    lib.kv_load(layer, 0, Kc.reshape(-1, hd), Vc.reshape(-1, hd))
+    cache = (Kc.copy(), Vc.copy())
+    pos = pos_base
+    for n, seed in ((S, 0x9E20), (S2, 0x9E21)):
+        xs = gen.normal(n * D, seed + layer)
+        y = lib.gqa_full(layer, xs, tq, tk, tv, to, n, H, KH, hd, rot, pos, max_t, W.eps, W.theta)
+        worst = 0.0
+        for t in range(n):
+            ref = W.oracle(lorc_omp, cache, max_t, pos + t, xs[t * D:(t + 1) * D])
+            worst = max(worst, _util.maxrel_scaled(y[t * D:(t + 1) * D], ref))
+        print(f"gqa rows {shape}: S={n} at pos {pos}: worst maxrel_scaled {worst:.2e}", flush=True)
+        assert worst <= TOL, (n, pos, worst)
+        pos += n
+    for h in range(KH):
+        Kd, Vd = lib.kv_read(layer, h * max_t + pos_base, pos - pos_base, hd, hd)
+        Kr = cache[0].reshape(KH, max_t, hd)[h, pos_base:pos]
+        Vr = cache[1].reshape(KH, max_t, hd)[h, pos_base:pos]
+        assert rel_to_max(Kd, Kr) < 1e-4 and rel_to_max(Vd, Vr) < 1e-5
+
+
 # ---------------------------------------------------------------- GDN block
 host_params = _layers.gdn_host_params
 
