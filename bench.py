@@ -309,6 +309,86 @@ def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
             "mfma_util_counters": {"pf_gateup": profile_mfma("pf_gateup"), "pf_down": profile_mfma("pf_down")}}
 
 
+def _route_host(lg, K):
+    """softmax, top-K (ties to the lower id) and renormalisation per row (c/qwen.c:1057-1072)."""
+    import numpy as np
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    idx = np.argsort(-p, axis=1, kind="stable")[:, :K].astype(np.int32)
+    val = np.take_along_axis(p, idx, axis=1)
+    return idx, (val / val.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def engine_prefill_cfg4(lib, torch, dev, layer, reps=3):
+    """The unchanged engine's prefill calls over S = 512 tokens (host buffers in and out, as
+    the engine passes them): one MoE layer of configs[4] (router logits by coli_vk_matmul over
+    the S rows, c/qwen.c:1189; the routed experts in chunks of <= 64 experts and <= 1024 rows
+    by coli_vk_eg_xs_bind + coli_vk_expert_group_issue_id / take, :1094-1125; the shared
+    expert over all rows by coli_vk_expert_group_issue / take, :1149-1152) and one gated GQA
+    layer of configs[3] (coli_vk_gqa_full with S = 512 at pos 0, c/qwen.c:589).  Timed: the
+    library calls only (the engine's host softmax, grouping and weighted adds excluded).
+    Each is also timed on the per-row paths it replaces (GEMV items per (expert, row); the
+    decode block once per token)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _engine
+    router, keep, _ = layer
+    S, D, E, K = 512, K_HID, 256, 8
+    rng = np.random.default_rng(0xE4)
+    xs = rng.normal(0.0, 1.0, (S, D)).astype(np.float32)
+    lib.matmul(router, xs, S)   # warm-up
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        lg = lib.matmul(router, xs, S).reshape(S, E)
+    router_ms = (time.perf_counter() - t0) / reps * 1e3
+    tidx, tval = _route_host(lg.astype(np.float64), K)
+    chs = _engine.plan(tidx, tval, K, E)
+
+    def moe_ms(n):
+        _engine.issue_chunks(lib, keep, xs, S, D, chs)
+        t = time.perf_counter()
+        for _ in range(n):
+            _engine.issue_chunks(lib, keep, xs, S, D, chs)
+        return (time.perf_counter() - t) / n * 1e3
+
+    mfma_ms = moe_ms(reps)
+    prev = lib.eg_force_gemv(True)
+    try:
+        gemv_ms = moe_ms(1)
+    finally:
+        lib.eg_force_gemv(prev)
+    # GQA layer at configs[3] geometry
+    H, KH, hd, rot, max_t, gl = 16, 2, 256, 64, 4096, 151
+    tq = lib.tensor_synth(6, D, 2 * H * hd, GS, 0xE40, 0.02)
+    tk = lib.tensor_synth(6, D, KH * hd, GS, 0xE41, 0.02)
+    tv = lib.tensor_synth(6, D, KH * hd, GS, 0xE42, 0.02)
+    to = lib.tensor_synth(6, H * hd, D, GS, 0xE43, 0.02)
+    lib.kv_ensure(gl, KH * max_t, hd, hd)
+    lib.gqa_norm_weight(gl, rng.normal(0, 0.1, hd).astype(np.float32), rng.normal(0, 0.1, hd).astype(np.float32))
+
+    def gqa_ms(n):
+        lib.gqa_full(gl, xs, tq, tk, tv, to, S, H, KH, hd, rot, 0, max_t, 1e-6, 1e7)
+        t = time.perf_counter()
+        for _ in range(n):
+            lib.gqa_full(gl, xs, tq, tk, tv, to, S, H, KH, hd, rot, 0, max_t, 1e-6, 1e7)
+        return (time.perf_counter() - t) / n * 1e3
+
+    gqa_batched = gqa_ms(reps)
+    prev = lib.gqa_seq(False)
+    try:
+        gqa_loop = gqa_ms(1)
+    finally:
+        lib.gqa_seq(prev)
+    rows = [len(c[2]) for c in chs]
+    return {"workload": "engine prefill calls, S=512: cfg4 MoE layer (router matmul, expert-group chunks, shared "
+                        "expert) + cfg3 gated GQA layer (gqa_full at pos 0), host buffers",
+            "router_matmul_ms": round(router_ms, 3), "moe_chunks": len(chs), "moe_rows_per_chunk_max": max(rows),
+            "moe_calls_ms": round(mfma_ms, 3), "moe_calls_ms_gemv_items": round(gemv_ms, 3),
+            "gqa_full_ms": round(gqa_batched, 3), "gqa_full_ms_token_loop": round(gqa_loop, 3),
+            "layer_pair_ms": round(router_ms + mfma_ms + gqa_batched, 3),
+            "tokens_per_s_moe_layer": round(S / ((router_ms + mfma_ms) * 1e-3), 1)}
+
+
 def gemm_prefill(lib, torch, dev, steps, warmup):
     """Dense fmt6 GEMM over S = 512 rows of x on MFMA (the prefill projections that
     coli_vk_matmul runs for S >= 4, c/backend_vulkan.c:282-299): O = 8192, I = 2048 (the
@@ -621,6 +701,7 @@ def main():
     if not args.no_moe:
         layer, out["moe_cfg2"] = moe_cfg2(lib, torch, dev, args.steps, args.warmup)
         out["moe_prefill_cfg4"] = moe_prefill_cfg4(lib, torch, dev, layer, max(args.steps // 10, 5), 2)
+        out["engine_prefill_cfg4"] = engine_prefill_cfg4(lib, torch, dev, layer)
     out["gemm_prefill"] = gemm_prefill(lib, torch, dev, max(args.steps // 10, 5), 2)
     out["gdn_prefill_cfg3"] = gdn_prefill_cfg3(lib)
     if not args.no_decode:

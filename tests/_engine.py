@@ -47,38 +47,57 @@ def chunks(ecnt, E):
     return out
 
 
-def engine_moe_batch(lib, tensors, xs, S, D, K, tidx, tval, sh_gate, shared_x=True):
-    """out [S, D] of the routed experts and the shared expert (tensors[e] = (g, u, d) for
-    e < E, tensors[E] the shared expert), through the ABI as the engine calls it."""
-    E = len(tensors) - 1
-    xs = np.ascontiguousarray(xs, np.float32).reshape(S, D)
+def plan(tidx, tval, K, E):
+    """The engine's chunks as ABI arguments: per chunk (experts, rows, token ids, weights)."""
     tval = np.asarray(tval, np.float32).reshape(-1)
     ecnt, epair = group_by_expert(tidx, E)
-    out = np.zeros((S, D), np.float32)
-    lib.eg_xs_bind(xs, S, D)
+    out = []
     for ch in chunks(ecnt, E):
         rtok, rw = [], []
         for e, r0, nr in ch:
             pairs = epair[ecnt[e] + r0:ecnt[e] + r0 + nr]
             rtok.extend((pairs // K).tolist())
             rw.extend(tval[pairs].tolist())
-        es = [c[0] for c in ch]
+        out.append(([c[0] for c in ch], [c[2] for c in ch], np.asarray(rtok, np.int32), np.asarray(rw, np.float32)))
+    return out
+
+
+def issue_chunks(lib, tensors, xs, S, D, chs, shared=True):
+    """The ABI calls alone (c/qwen.c:1094,1120-1121,1149-1152): bind, one issue_id + take per
+    chunk, then the shared expert over all S rows.  Returns the y blocks (the last one the
+    shared expert's)."""
+    E = len(tensors) - 1
+    lib.eg_xs_bind(xs, S, D)
+    ys = []
+    for es, rows, rtok, _ in chs:
         if not lib.expert_group_issue_id([tensors[e][0] for e in es], [tensors[e][1] for e in es],
-                                         [tensors[e][2] for e in es], [c[2] for c in ch], rtok):
+                                         [tensors[e][2] for e in es], rows, rtok):
             raise RuntimeError("coli_vk_expert_group_issue_id refused a chunk")
-        y = lib.expert_group_take(len(rtok), D).reshape(-1, D)
-        w = np.asarray(rw, np.float32)
-        for r, t in enumerate(rtok):
-            out[t] += w[r] * y[r]
-    if shared_x:
+        ys.append(lib.expert_group_take(len(rtok), D).reshape(-1, D))
+    if shared:
         g, u, d = tensors[E]
         if not lib.expert_group_issue([g], [u], [d], [S], xs):
             raise RuntimeError("coli_vk_expert_group_issue refused the shared expert")
-        y = lib.expert_group_take(S, D).reshape(S, D)
-        sg = np.asarray(sh_gate, np.float32)
-        for s in range(S):
-            # c/qwen.c:1158: gt += sh_gate[d] * x[d] in index order (accumulate is sequential)
-            gt = np.add.accumulate((sg * xs[s]).astype(np.float32), dtype=np.float32)[-1]
-            sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-gt, dtype=np.float32))   # sigmoidf_, c/qwen.c:172
-            out[s] += sig * y[s]
+        ys.append(lib.expert_group_take(S, D).reshape(S, D))
+    return ys
+
+
+def engine_moe_batch(lib, tensors, xs, S, D, K, tidx, tval, sh_gate):
+    """out [S, D] of the routed experts and the shared expert (tensors[e] = (g, u, d) for
+    e < E, tensors[E] the shared expert), through the ABI as the engine calls it."""
+    E = len(tensors) - 1
+    xs = np.ascontiguousarray(xs, np.float32).reshape(S, D)
+    chs = plan(tidx, tval, K, E)
+    ys = issue_chunks(lib, tensors, xs, S, D, chs)
+    out = np.zeros((S, D), np.float32)
+    for (_, _, rtok, rw), y in zip(chs, ys):
+        for r, t in enumerate(rtok):   # c/qwen.c:1024-1027,1133: rows in chunk order
+            out[t] += rw[r] * y[r]
+    y = ys[-1]
+    sg = np.asarray(sh_gate, np.float32)
+    for s in range(S):
+        # c/qwen.c:1158: gt += sh_gate[d] * x[d] in index order (accumulate is sequential)
+        gt = np.add.accumulate((sg * xs[s]).astype(np.float32), dtype=np.float32)[-1]
+        sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-gt, dtype=np.float32))   # sigmoidf_, c/qwen.c:172
+        out[s] += sig * y[s]
     return out
