@@ -217,6 +217,12 @@ class Lib:
             raise RuntimeError("coli_vk_init failed (no gfx950 device?)")
         return self
 
+    def mem_info(self):
+        """(device bytes held by live tensors, live tensor count), coli_vk_mem_info."""
+        b, n = C.c_size_t(), C.c_size_t()
+        self.L.coli_vk_mem_info(C.byref(b), C.byref(n))
+        return b.value, n.value
+
     def available(self):
         return bool(self.L.coli_vk_available())
 

@@ -1281,13 +1281,33 @@ COLI_API int coli_vk_eg_table_init(int n_layers, int E, int D, int I, int gs) {
     return 1;
 }
 
+namespace coli {
+// Would slot (layer, eid) of the current table take these tensors (eid == E: the shared
+// expert)?  The table's dimensions, the fmt 6 lanes layout and the geometry of the slots
+// already set must match.
+bool eg_table_check(int layer, int eid, const ColiVkTensor *g, const ColiVkTensor *u, const ColiVkTensor *d,
+                    MoeGeom *out) {
+    const EgTable &T = g_eg;
+    if (!ok() || !T.d_rec || layer < 0 || layer >= T.n_layers || eid < 0 || eid > T.E || !g || !u || !d) return false;
+    MoeGeom m, mu;
+    if (!geom_of(g, d, m) || !geom_of(u, d, mu) || !same_geom(m, mu) || !geom_supported(m)) return false;
+    if (m.D != T.D || m.I != T.I || m.gs != T.gs) return false;
+    if (T.geom_set && !same_geom(m, T.geom)) return false;
+    if (out) *out = m;
+    return true;
+}
+
+bool eg_table_dims(int layer, int E, int D, int I, int gs) {
+    const EgTable &T = g_eg;
+    return ok() && T.d_rec && layer >= 0 && layer < T.n_layers && E >= 1 && E <= T.E && D == T.D && I == T.I &&
+           gs == T.gs;
+}
+}  // namespace coli
+
 static int eg_table_put(int layer, int eid, ColiVkTensor *g, ColiVkTensor *u, ColiVkTensor *d) {
     EgTable &T = g_eg;
-    if (!ok() || !T.d_rec || layer < 0 || layer >= T.n_layers || eid < 0 || eid > T.E || !g || !u || !d) return 0;
-    MoeGeom m, mu;
-    if (!geom_of(g, d, m) || !geom_of(u, d, mu) || !same_geom(m, mu) || !geom_supported(m)) return 0;
-    if (m.D != T.D || m.I != T.I || m.gs != T.gs) return 0;
-    if (T.geom_set && !same_geom(m, T.geom)) return 0;
+    MoeGeom m;
+    if (!eg_table_check(layer, eid, g, u, d, &m)) return 0;
     T.geom = m;
     T.geom_set = 1;
     const size_t i = (size_t)layer * (T.E + 1) + eid;

@@ -36,6 +36,12 @@ int eg_unit_rows(int count, const int *rows, const MoeGeom &m);
 bool eg_mfma(const PfUnit *d_units, int nunits, const int *d_xrow, int P, const MoeGeom &m, const float *d_x, int Sx,
              uint64_t key, float *d_y, hipStream_t st);
 
+// The resident expert table (moe.hip): would slot (layer, eid) take these tensors (no
+// change made; *out their geometry), and are (layer, E, D, I, gs) within the table's shape.
+bool eg_table_check(int layer, int eid, const ColiVkTensor *g, const ColiVkTensor *u, const ColiVkTensor *d,
+                    MoeGeom *out);
+bool eg_table_dims(int layer, int E, int D, int I, int gs);
+
 constexpr int kMaxE = 1024;
 constexpr int kMaxSlots = kTopK + 1;      // fused kernel: K <= 8 routed + the shared expert
 constexpr int kMoeMaxI = 512;             // expert intermediate size (h staged in LDS)

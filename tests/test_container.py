@@ -14,6 +14,7 @@ safetensors package and by hand.
 import json
 import os
 import struct
+import subprocess
 
 import numpy as np
 import pytest
@@ -156,16 +157,16 @@ def test_truncated_and_empty(lib, tmp_path):
     assert st.find("té") is not None
 
 
-def test_mutated_headers_never_crash(lib, tmp_path):
-    """600 seeded mutations (byte flips, insertions, truncations) of a valid two-tensor
-    header: every open either succeeds or is refused; an accepted index still answers
-    find and bounded reads."""
+_MUT_DATA = bytes(range(40))
+
+
+def _mutations(n=600):
+    """n seeded mutations (byte flips, insertions, truncations) of a valid two-tensor header."""
     hdr = json.dumps({"__metadata__": {"a": "b"}, "w": {"dtype": "U8", "shape": [4, 2], "data_offsets": [0, 8]},
                       "w.qs": {"dtype": "F32", "shape": [4, 2], "data_offsets": [8, 40]}}).encode()
-    data = bytes(range(40))
     rng = np.random.default_rng(0xC0FFEE)
     alphabet = b'{}[]":,0123456789-.eE\\u tnrfalsedtype' + bytes([0, 0x7F, 0xC3, 0xFF])
-    for i in range(600):
+    for _ in range(n):
         h = bytearray(hdr)
         for _ in range(int(rng.integers(1, 4))):
             op, at = int(rng.integers(0, 3)), int(rng.integers(0, len(h)))
@@ -175,7 +176,14 @@ def test_mutated_headers_never_crash(lib, tmp_path):
                 h.insert(at, alphabet[int(rng.integers(0, len(alphabet)))])
             else:
                 del h[at:at + int(rng.integers(1, 8))]
-        _raw_file(tmp_path / "m.safetensors", bytes(h), data)
+        yield bytes(h)
+
+
+def test_mutated_headers_never_crash(lib, tmp_path):
+    """600 seeded mutations of a valid two-tensor header: every open either succeeds or is
+    refused; an accepted index still answers find and bounded reads."""
+    for h in _mutations():
+        _raw_file(tmp_path / "m.safetensors", h, _MUT_DATA)
         try:
             st = ql.Container(lib, str(tmp_path))
         except ValueError:
@@ -185,3 +193,60 @@ def test_mutated_headers_never_crash(lib, tmp_path):
             if r is not None and r[2] <= 64:
                 st.read_raw(name, 64)
         st.close()
+
+
+def test_reader_under_address_sanitizer(lib, tmp_path):
+    """The reader's host side (csrc/st_host.cpp) built alone with -fsanitize=address,undefined
+    (tests/st_asan.cpp drives it): the hostile headers, the 600 mutations, truncated shards,
+    the BF16 / F16 file and the safetensors package's file are opened and every indexed tensor
+    read.  No sanitizer report, and each directory gets the same verdict (open or refused) as
+    from the product library."""
+    exe = tmp_path / "st_asan"
+    src = os.path.join(_util.ROOT, "qwen3.c_amd", "csrc", "st_host.cpp")
+    drv = os.path.join(_util.ROOT, "tests", "st_asan.cpp")
+    r = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+                        "-fno-sanitize-recover=undefined", drv, src, "-o", str(exe)], capture_output=True, text=True)
+    if r.returncode != 0 and "asan" in (r.stderr or "").lower():
+        pytest.skip("no AddressSanitizer runtime for the host compiler")
+    assert r.returncode == 0, r.stderr
+    dirs = []
+
+    def new_dir():
+        d = tmp_path / f"d{len(dirs)}"
+        d.mkdir()
+        dirs.append(d)
+        return d
+
+    for case in sorted(HOSTILE):
+        spec = HOSTILE[case]
+        _raw_file(new_dir() / "x.safetensors", spec.get("header", _ok_hdr()), b"\0" * 8, spec.get("hlen"))
+    for h in _mutations():
+        _raw_file(new_dir() / "m.safetensors", h, _MUT_DATA)
+    for cut in (1, 3, 8, 20):   # a valid file cut short, inside the length word, header and data
+        d = new_dir()
+        _raw_file(d / "t.safetensors", _ok_hdr(), np.ones(2, np.float32).tobytes())
+        b = (d / "t.safetensors").read_bytes()
+        (d / "t.safetensors").write_bytes(b[:min(cut, len(b) - 1)] if cut < 8 else b[:-cut // 4])
+    bits = np.arange(65536, dtype=np.uint16)
+    _st(new_dir() / "a.safetensors", {"b": ("BF16", [65536], bits.tobytes()), "h": ("F16", [256, 256], bits.tobytes())})
+    rng = np.random.default_rng(2)
+    save_file({"u": rng.integers(0, 256, (64, 128), dtype=np.uint8), "f": rng.normal(size=(3, 5)).astype(np.float32),
+               "e": np.zeros((0, 4), np.float32)}, str(new_dir() / "p.safetensors"))
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0", UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([str(exe)] + [str(d) for d in dirs], capture_output=True, text=True, errors="replace", env=env,
+                       timeout=300)
+    assert "AddressSanitizer" not in r.stderr and "runtime error" not in r.stderr, r.stderr[-4000:]
+    assert r.returncode == 0, r.stderr[-4000:]
+    verdict = {}
+    for line in r.stdout.splitlines():
+        word, path = line.split()[:2]
+        verdict[path] = word
+    assert len(verdict) == len(dirs)
+    for d in dirs:
+        try:
+            ql.Container(lib, str(d)).close()
+            want = "open"
+        except ValueError:
+            want = "refused"
+        assert verdict[str(d)] == want, d
+    assert sum(v == "open" for v in verdict.values()) >= 3

@@ -153,3 +153,50 @@ def test_st_experts_refuses_wrong_container(lib, gen, tmp_path):
     with pytest.raises(RuntimeError):
         st.experts(layer, E, D, I, gs)
     assert lib.available()
+
+
+def test_st_experts_failure_releases_uploads(lib, gen, tmp_path):
+    """A shard cut short after it was indexed, under the last expert of a layer whose reads
+    need two batches (64 configs[2] experts, ~113 MB): the first batch is already on the
+    device when the read fails.  The call returns 0 and the library's tensor count and bytes
+    are back where they were; a table of the wrong shape is refused before any upload; the
+    device stays usable and the intact layer then loads."""
+    mod = _util.load_product()
+    D, I, E, gs, layer = 2048, 512, 64, 128, 5
+    mw = _util.MoeWeights(gen, 0x5F00, D, I, E, gs)
+    _write_experts(tmp_path, mw, layer, shards=2)
+    st = mod.Container(lib, str(tmp_path))
+    _moe._active[0] = None
+    lib.eg_table_init(layer + 1, E, D, 2 * I, gs)   # wrong I: refused up front
+    before = lib.mem_info()
+    with pytest.raises(RuntimeError):
+        st.experts(layer, E, D, I, gs)
+    assert lib.mem_info() == before
+    lib.eg_table_init(layer + 1, E, D, I, gs)
+    shard = tmp_path / f"out-layer-{layer:02d}-1.safetensors"
+    full = shard.read_bytes()
+    shard.write_bytes(full[:len(full) - 4096])   # the index was built from the whole file
+    with pytest.raises(RuntimeError):
+        st.experts(layer, E, D, I, gs)
+    assert lib.mem_info() == before
+    assert lib.available()
+    shard.write_bytes(full)
+    st.experts(layer, E, D, I, gs)
+    assert lib.mem_info()[1] == before[1] + 3 * E
+    _moe._active[0] = None
+
+
+def test_st_tensor_half_scales(lib, orc, gen, tmp_path):
+    """A .qs tensor stored as F16 (c/qwen.c:528-534 reads it through st_read_f32, which
+    converts): the same device tensor as the upload of the converted f32 scales."""
+    mod = _util.load_product()
+    O, I, gs = 512, 2048, 128
+    q, sz = gen.fmt6(O, I, gs, 0x5F10)
+    sz16 = sz.astype(np.float16)
+    wq, ws = _arrays(q, sz16.astype(np.float32), I, O, gs)
+    save_file({"h.weight": wq, "h.weight.qs": ws.astype(np.float16)}, str(tmp_path / "h.safetensors"))
+    st = mod.Container(lib, str(tmp_path))
+    t_st = st.tensor("h.weight", 6, I, O, gs)
+    t_up = lib.tensor(q, sz16.astype(np.float32), 6, I, O, gs)
+    a, b = _device_bytes(lib, t_st), _device_bytes(lib, t_up)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
