@@ -14,7 +14,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libcoli_hip.so")
+# COLI_HIP_LIB names another build of the library (a variant with other launch constants,
+# for side-by-side timing); the default is the in-tree build.
+LIB_PATH = os.environ.get("COLI_HIP_LIB") or os.path.join(HERE, "libcoli_hip.so")
 
 _P = C.c_void_p
 _I = C.c_int

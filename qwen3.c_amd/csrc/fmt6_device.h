@@ -323,7 +323,7 @@ __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr,
     lds_barrier();
     double t = 0;
     for (int w = 0; w < NT / 64; w++) t += s_red[w];
-    const float r = 1.f / sqrtf((float)(t / I) + eps);
+    const float r = 1.f / sqrtf((float)((I & (I - 1)) ? t / I : t * (1.0 / I)) + eps);   // 1 / I exact for I = 2^k
 #pragma unroll
     for (int k = 0; k < XRegsT<NT>::kWords; k++) {
         const int w = threadIdx.x + k * NT;
@@ -331,6 +331,26 @@ __device__ __forceinline__ void norm_apply(XRegsT<NT> &xr, const XRegsT<NT> &wr,
         for (int c = 0; c < 8; c++)
             if (w < ncols / 8 && w * 8 + c < I) xr.v[k][c] = xr.v[k][c] * r * (1.f + wr.v[k][c]);
     }
+}
+
+// 22 - e for a group maximum m: e = ilogb(m) + 1 (m < 2^e), the exponent frexp gives for
+// finite m > 0 (denormals included); 0 for an all-zero group.
+__device__ __forceinline__ int exp22_of(float m) { return 22 - (m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0); }
+
+// The balanced digits of one 8-column word at scale 2^k (k = 22 - e, |v 2^k| < 2^22):
+// u[c] = rint(v[c] 2^k) + 0x888888 (digit l + 8 in nibble l), and the sum of the
+// rint(v[c] 2^k).  rint comes from adding 1.5 2^23 (round to nearest even, |v 2^k| < 2^22):
+// the sum's bits are 0x4B400000 + rint(v 2^k).
+__device__ __forceinline__ int word_digits(const float (&v)[8], int k, uint32_t (&u)[8]) {
+    int qs = 0;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const float t = ldexpf(v[c], k) + 12582912.f;
+        const int q = (int)(__float_as_uint(t) - 0x4B400000u);
+        qs += q;
+        u[c] = (uint32_t)(q + 0x888888);
+    }
+    return qs;
 }
 
 template <int NT = kThreads>
@@ -341,6 +361,7 @@ __device__ __forceinline__ void prep_x(const XRegsT<NT> &xr, int gs, int ncols, 
     // aligned run of lanes: its maximum comes by DPP, and a chunk's q sum (4 words) by a
     // quad sum, with no LDS round trip.  Other group sizes use LDS atomics.
     const bool runs = wpg <= 16 && (wpg & (wpg - 1)) == 0;
+    const int gsh = runs ? __builtin_ctz((unsigned)wpg) : 0;   // word -> group shift (runs)
     const auto &xv = xr.v;
     if (!runs) {
         for (int g = tid; g < ngrp; g += NT) P.gmax[g] = 0u;
@@ -365,15 +386,8 @@ __device__ __forceinline__ void prep_x(const XRegsT<NT> &xr, int gs, int ncols, 
         const int w = tid + k * NT;
         const bool on = w < nwords;
         const float m = runs ? __uint_as_float(mb[k]) : on ? __uint_as_float(P.gmax[(w * 8) / gs]) : 0.f;
-        const int e = m > 0.f ? ilogbf(m) + 1 : 0;    // m < 2^e
         uint32_t u[8];
-        int qs = 0;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int q = (int)rintf(ldexpf(xv[k][c], 22 - e));
-            qs += q;
-            u[c] = (uint32_t)(q + 0x888888);   // balanced digits d -> unsigned nibbles d + 8
-        }
+        int qs = word_digits(xv[k], exp22_of(m), u);
         if (on) {
             uint32_t lw[kLimbs];
             digit_planes(u, lw);
@@ -382,14 +396,14 @@ __device__ __forceinline__ void prep_x(const XRegsT<NT> &xr, int gs, int ncols, 
         }
         qs = quad_sum(qs);
         if (on && (w & 3) == 0) P.qsum[w >> 2] = qs;
-        if (runs && on && (w & (wpg - 1)) == 0) P.gmax[(w * 8) / gs] = mb[k];
+        if (runs && on && (w & (wpg - 1)) == 0) P.gmax[w >> gsh] = mb[k];
     }
     lds_barrier();
 }
 
 __device__ __forceinline__ int group_exp22(const XPrep &P, int g) {
     const float m = __uint_as_float(P.gmax[g]);
-    return (m > 0.f ? ilogbf(m) + 1 : 0) - 22;
+    return -exp22_of(m);
 }
 
 // ---------------------------------------------------------------- per-lane state

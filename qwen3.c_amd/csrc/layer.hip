@@ -128,7 +128,7 @@ __device__ __forceinline__ void xf_apply(XRegs &xr, const XRegs &ar, const XRegs
 #pragma unroll
             for (int c = 0; c < 8; c++) ss += (double)xr.v[k][c] * xr.v[k][c];
             ss = seg_sum_d(ss, wph);
-            const float r = 1.f / sqrtf((float)(ss / a.VD) + a.eps);
+            const float r = 1.f / sqrtf((float)(ss * (1.0 / a.VD)) + a.eps);   // VD = 8 wph, a power of two: exact
 #pragma unroll
             for (int c = 0; c < 8; c++) {
                 const int i = w * 8 + c;

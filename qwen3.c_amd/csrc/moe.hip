@@ -128,15 +128,8 @@ __device__ __forceinline__ void prep_h(const float (&v)[kHWords][8], int I, int 
         const int q = tid + k * kThreads;
         const bool on = q < nw;
         const float m = runs ? __uint_as_float(mb[k]) : on ? __uint_as_float(H.gmax[(q * 8) / gs]) : 0.f;
-        const int e = m > 0.f ? ilogbf(m) + 1 : 0;
         uint32_t u[8];
-        int qs = 0;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int qv = (int)rintf(ldexpf(v[k][c], 22 - e));
-            qs += qv;
-            u[c] = (uint32_t)(qv + 0x888888);
-        }
+        int qs = word_digits(v[k], exp22_of(m), u);
         if (on) {
             uint32_t lw[kLimbs];
             digit_planes(u, lw);
@@ -189,7 +182,7 @@ __device__ __forceinline__ float down_chunk(const HPrep &H, int gs, const DownTh
     const int hi = t[3] + 16 * t[4] + 256 * t[5];
     const float T = fmaf((float)hi, 4096.f, (float)lo);
     const float m = __uint_as_float(H.gmax[(d.h * 32) / gs]);
-    const int ue = (m > 0.f ? ilogbf(m) + 1 : 0) - 22;
+    const int ue = -exp22_of(m);
     const float ucs = ldexpf((float)H.qsum[d.h], ue);
     return sz.x * fmaf(-(sz.y - 8.f), ucs, ldexpf(T, ue));
 }
