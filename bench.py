@@ -345,7 +345,9 @@ def engine_prefill_cfg4(lib, torch, dev, layer, reps=3):
     by coli_vk_eg_xs_bind + coli_vk_expert_group_issue_id / take, :1094-1125; the shared
     expert over all rows by coli_vk_expert_group_issue / take, :1149-1152) and one gated GQA
     layer of configs[3] (coli_vk_gqa_full with S = 512 at pos 0, c/qwen.c:589).  Timed: the
-    library calls only (the engine's host softmax, grouping and weighted adds excluded).
+    library calls only (the engine's host softmax, grouping and weighted adds excluded); the
+    expert-group rows are taken into one host buffer, as the engine's per-chunk malloc/free
+    of its y block is served warm by the C heap after the first chunk.
     Each is also timed on the per-row paths it replaces (GEMV items per (expert, row); the
     decode block once per token)."""
     import numpy as np
@@ -363,11 +365,13 @@ def engine_prefill_cfg4(lib, torch, dev, layer, reps=3):
     tidx, tval = _route_host(lg.astype(np.float64), K)
     chs = _engine.plan(tidx, tval, K, E)
 
+    ybuf = np.zeros(max(max(len(c[2]) for c in chs), S) * D, np.float32)
+
     def moe_ms(n):
-        _engine.issue_chunks(lib, keep, xs, S, D, chs)
+        _engine.issue_chunks_into(lib, keep, xs, S, D, chs, ybuf)
         t = time.perf_counter()
         for _ in range(n):
-            _engine.issue_chunks(lib, keep, xs, S, D, chs)
+            _engine.issue_chunks_into(lib, keep, xs, S, D, chs, ybuf)
         return (time.perf_counter() - t) / n * 1e3
 
     mfma_ms = moe_ms(reps)

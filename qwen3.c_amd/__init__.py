@@ -330,6 +330,14 @@ class Lib:
             raise RuntimeError("coli_vk_expert_group_take failed")
         return y
 
+    def expert_group_take_into(self, y):
+        """take into a caller's float32 buffer (reused across calls, as the engine's heap
+        block is); y must hold the issued rows."""
+        assert y.dtype == np.float32 and y.flags.c_contiguous
+        if not self.L.coli_vk_expert_group_take(_ptr(y)):
+            raise RuntimeError("coli_vk_expert_group_take failed")
+        return y
+
     def eg_xs_bind(self, xs, S, D):
         xs = np.ascontiguousarray(xs, dtype=np.float32)
         if not self.L.coli_vk_eg_xs_bind(_ptr(xs), S, D):

@@ -788,12 +788,7 @@ static bool stage_x(const float *x, size_t xb) {
 }
 
 static bool fetch(void *dst, const void *dsrc, size_t bytes, const char *who) {
-    if (!host_scratch(&g_st.hy, &g_st.hyc, bytes)) return false;
-    hipError_t e = hipMemcpyAsync(g_st.hy, dsrc, bytes, hipMemcpyDeviceToHost, stream());
-    if (e == hipSuccess) e = hipStreamSynchronize(stream());
-    if (e != hipSuccess) return fail(who, e);
-    memcpy(dst, g_st.hy, bytes);
-    return true;
+    return read_back(dst, dsrc, bytes, stream(), who);
 }
 
 }  // namespace coli

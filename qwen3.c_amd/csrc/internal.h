@@ -54,6 +54,22 @@ bool scratch(void **p, size_t *cap, size_t need);   // grow-only device scratch
 bool host_scratch(void **p, size_t *cap, size_t need);  // grow-only pinned host scratch
 bool sync_stream(const char *who);
 
+// device -> pageable host read-back through pinned staging, copied out piece by piece as
+// the pieces arrive (runtime.hip); read_back synchronises with every piece on `st`.
+bool read_back(void *dst, const void *dsrc, size_t n, hipStream_t st, const char *who);
+// The pieces of a read-back already issued into pinned memory: record one event per piece
+// after issuing it, then copy_out waits for each in turn and copies it out.
+struct PieceEvents {
+    static constexpr int kMax = 8;
+    hipEvent_t ev[kMax] = {};
+    size_t piece = 0, n = 0;
+    int count = 0;
+};
+bool issue_pieces(PieceEvents &pe, void *hdst, const void *dsrc, size_t n, hipStream_t st);
+bool copy_out(PieceEvents &pe, void *dst, const void *hsrc, const char *who);
+void piece_events_free(PieceEvents &pe);
+void read_back_shutdown();
+
 // tensors
 bool tensor_live(const ColiVkTensor *t);  // non-NULL and allocated since the last shutdown
 constexpr int kLaneMaxI = 4096;          // fmt 6 lanes layout / fast GEMV path: nl <= 64

@@ -2231,8 +2231,7 @@ static int gqa_rows(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTe
         if (!gqa_block(layer, dx + (size_t)s * D, nullptr, tq, tk, tv, to, dout + (size_t)s * Dout, false, d,
                        pos_base + s, stream()))
             return 0;
-    if (!sync_stream("gqa rows")) return 0;
-    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+    return read_back(out, dout, (size_t)S * Dout * 4, stream(), "gqa rows") ? 1 : 0;
 }
 
 // S >= kGemmMinS rows in one pass (c/backend_vulkan.c:2280-2340): q/k/v as one digit
@@ -2298,8 +2297,8 @@ static int gqa_seq(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTen
     if (e != hipSuccess) return fail("attention rows launch", e) ? 1 : 0;
     const ColiVkTensor *op[1] = {to};
     float *const oy[1] = {dout};
-    if (!gemm6(op, oy, 1, ctx, S, stream()) || !sync_stream("gqa seq")) return 0;
-    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+    if (!gemm6(op, oy, 1, ctx, S, stream())) return 0;
+    return read_back(out, dout, (size_t)S * Dout * 4, stream(), "gqa seq") ? 1 : 0;
 }
 
 // c/backend_vulkan.h:171-178: x is the normed input [S, D]; out [S, Dout] = block output
@@ -2492,8 +2491,7 @@ static int gdn_rows(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_
         if (!gdn_block(layer, dx + (size_t)s * D, nullptr, dp + (size_t)s * prs, gqkv_t, gz_t, nullptr, nullptr,
                        out_t, dout + (size_t)s * Dout, false, d, stream()))
             return 0;
-    if (!sync_stream("gdn rows")) return 0;
-    return hipMemcpy(out, dout, (size_t)S * Dout * 4, hipMemcpyDeviceToHost) == hipSuccess ? 1 : 0;
+    return read_back(out, dout, (size_t)S * Dout * 4, stream(), "gdn rows") ? 1 : 0;
 }
 
 // c/backend_vulkan.h:268-271: one token, x normed, params [decay | beta | gnorm]
@@ -2565,9 +2563,9 @@ static bool full_route_out(const float *dres, const float *dnrm, const float *dl
                            float *resid_out, float *nrm_out, float *pr_out) {
     if (!sync_stream("route read-back")) return false;
     bool r = true;
-    if (resid_out) r &= hipMemcpy(resid_out, dres, (size_t)S * D * 4, hipMemcpyDeviceToHost) == hipSuccess;
-    if (nrm_out) r &= hipMemcpy(nrm_out, dnrm, (size_t)S * D * 4, hipMemcpyDeviceToHost) == hipSuccess;
-    if (pr_out) r &= hipMemcpy(pr_out, dlog, (size_t)S * E * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    if (resid_out) r &= read_back(resid_out, dres, (size_t)S * D * 4, stream(), "route read-back");
+    if (nrm_out) r &= read_back(nrm_out, dnrm, (size_t)S * D * 4, stream(), "route read-back");
+    if (pr_out) r &= read_back(pr_out, dlog, (size_t)S * E * 4, stream(), "route read-back");
     return r;
 }
 

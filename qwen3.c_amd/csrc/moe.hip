@@ -986,7 +986,8 @@ struct LaunchEg {
 // One group in flight (c/backend_vulkan.c:1648).  Pinned staging holds rec | xrow | x | y.
 struct EgGroup {
     int inflight = 0;
-    size_t y_off = 0, y_bytes = 0;
+    size_t y_off = 0;
+    PieceEvents y;            // the rows' read-back, in pieces
     void *d_buf = nullptr;
     size_t d_cap = 0;
     void *h_buf = nullptr;
@@ -995,7 +996,6 @@ struct EgGroup {
     size_t d_xs_cap = 0;
     int xs_S = 0, xs_D = 0;
     uint64_t xs_key = 0;      // changes with every bind (names the bound rows' contents)
-    hipEvent_t done = nullptr;
 };
 static EgGroup g_grp;
 
@@ -1042,11 +1042,7 @@ static bool eg_submit_mfma(ColiVkTensor *const *gates, ColiVkTensor *const *ups,
                  tok_ids ? g_grp.xs_key : 0, d_y, stream()))
         return false;
     g_grp.y_off = un_b + xrow_b + x_b;
-    g_grp.y_bytes = y_b;
-    e = hipMemcpyAsync(hb + g_grp.y_off, d_y, y_b, hipMemcpyDeviceToHost, stream());
-    if (e == hipSuccess && !g_grp.done) e = hipEventCreateWithFlags(&g_grp.done, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventRecord(g_grp.done, stream());
-    if (e != hipSuccess) return fail("expert group issue", e);
+    if (!issue_pieces(g_grp.y, hb + g_grp.y_off, d_y, y_b, stream())) return false;
     g_grp.inflight = 1;
     return true;
 }
@@ -1104,22 +1100,17 @@ static bool eg_submit(ColiVkTensor *const *gates, ColiVkTensor *const *ups, Coli
     if (e != hipSuccess) return fail("expert group upload", e);
     if (!dispatch_shape<LaunchEg>(m, it, stream())) return false;
     g_grp.y_off = rec_b + xrow_b + x_b;
-    g_grp.y_bytes = y_b;
-    e = hipMemcpyAsync(hb + g_grp.y_off, it.y, y_b, hipMemcpyDeviceToHost, stream());
-    if (e == hipSuccess && !g_grp.done) e = hipEventCreateWithFlags(&g_grp.done, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventRecord(g_grp.done, stream());
-    if (e != hipSuccess) return fail("expert group issue", e);
+    if (!issue_pieces(g_grp.y, hb + g_grp.y_off, it.y, y_b, stream())) return false;
     g_grp.inflight = 1;
     return true;
 }
 
+// The rows come back in pieces (issue_pieces at issue time); each is copied out as soon as
+// it has arrived.
 static bool eg_take(float *y) {
     if (!g_grp.inflight) return false;
     g_grp.inflight = 0;
-    const hipError_t e = hipEventSynchronize(g_grp.done);
-    if (e != hipSuccess) return fail("expert group take", e);
-    memcpy(y, (uint8_t *)g_grp.h_buf + g_grp.y_off, g_grp.y_bytes);
-    return true;
+    return copy_out(g_grp.y, y, (uint8_t *)g_grp.h_buf + g_grp.y_off, "expert group take");
 }
 
 __global__ void silu_mul_kernel(const float *g, const float *u, float *h, size_t n) {
@@ -1143,7 +1134,7 @@ void moe_shutdown() {
     scratch_free(&g_grp.d_buf, &g_grp.d_cap);
     host_scratch_free(&g_grp.h_buf, &g_grp.h_cap);
     scratch_free(&g_grp.d_xs, &g_grp.d_xs_cap);
-    if (g_grp.done) (void)hipEventDestroy(g_grp.done);
+    piece_events_free(g_grp.y);
     g_grp = EgGroup();
     scratch_free(&g_gu_d, &g_gu_dc);
     host_scratch_free(&g_gu_h, &g_gu_hc);

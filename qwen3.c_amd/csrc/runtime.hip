@@ -132,6 +132,63 @@ bool sync_stream(const char *who) {
     return true;
 }
 
+// ---------------------------------------------------------------- read-backs
+// A read-back into a caller's (pageable) buffer goes through pinned staging: the device
+// copies in up to 8 pieces, each with its event, and each piece is copied out on the host
+// as soon as it has arrived, so the host copy of one piece overlaps the transfer of the
+// next.  (Several host threads do not copy faster here: one thread already reaches the
+// host memory bandwidth the process gets, ~30 GB/s for 8 MiB blocks on the MI355X boxes.)
+namespace {
+void *g_rb = nullptr;   // pinned staging of read_back
+size_t g_rb_cap = 0;
+PieceEvents g_rb_pe;
+}  // namespace
+
+void read_back_shutdown() {
+    host_scratch_free(&g_rb, &g_rb_cap);
+    piece_events_free(g_rb_pe);
+}
+
+// Up to PieceEvents::kMax pieces of at least 1 MiB each.
+bool issue_pieces(PieceEvents &pe, void *hdst, const void *dsrc, size_t n, hipStream_t st) {
+    size_t piece = (size_t)1 << 20;
+    if (n > piece * PieceEvents::kMax) piece = (n + PieceEvents::kMax - 1) / PieceEvents::kMax;
+    piece = (piece + 4095) & ~(size_t)4095;
+    pe.piece = piece;
+    pe.n = n;
+    pe.count = n ? (int)((n + piece - 1) / piece) : 0;
+    for (int i = 0; i < pe.count; i++) {
+        const size_t o = (size_t)i * piece, len = n - o < piece ? n - o : piece;
+        hipError_t e = hipMemcpyAsync((uint8_t *)hdst + o, (const uint8_t *)dsrc + o, len, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess && !pe.ev[i]) e = hipEventCreateWithFlags(&pe.ev[i], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventRecord(pe.ev[i], st);
+        if (e != hipSuccess) return fail("read-back issue", e);
+    }
+    return true;
+}
+
+bool copy_out(PieceEvents &pe, void *dst, const void *hsrc, const char *who) {
+    for (int i = 0; i < pe.count; i++) {
+        const hipError_t e = hipEventSynchronize(pe.ev[i]);
+        if (e != hipSuccess) return fail(who, e);
+        const size_t o = (size_t)i * pe.piece, len = pe.n - o < pe.piece ? pe.n - o : pe.piece;
+        memcpy((uint8_t *)dst + o, (const uint8_t *)hsrc + o, len);
+    }
+    return true;
+}
+
+void piece_events_free(PieceEvents &pe) {
+    for (int i = 0; i < PieceEvents::kMax; i++)
+        if (pe.ev[i]) (void)hipEventDestroy(pe.ev[i]);
+    pe = PieceEvents();
+}
+
+bool read_back(void *dst, const void *dsrc, size_t n, hipStream_t st, const char *who) {
+    if (!n) return true;
+    if (!host_scratch(&g_rb, &g_rb_cap, n)) return false;
+    return issue_pieces(g_rb_pe, g_rb, dsrc, n, st) && copy_out(g_rb_pe, dst, g_rb, who);
+}
+
 // Device layout of a tensor (see ColiVkTensor) and its arena slice.
 ColiVkTensor *tensor_alloc(int fmt, int I, int O, int gs) {
     if (I < 1 || O < 1) return nullptr;
@@ -309,6 +366,7 @@ COLI_API void coli_vk_shutdown(void) {
     prefill_shutdown();
     layer_shutdown();
     container_shutdown();
+    read_back_shutdown();
     scratch_free(&g_stage, &g_stage_cap);
     for (int i = 0; i < G.nblocks; i++) (void)hipFree(G.blocks[i].base);
     G.nblocks = 0;

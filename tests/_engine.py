@@ -82,6 +82,23 @@ def issue_chunks(lib, tensors, xs, S, D, chs, shared=True):
     return ys
 
 
+def issue_chunks_into(lib, tensors, xs, S, D, chs, ybuf):
+    """issue_chunks with every take into one host buffer ybuf (at least max rows x D floats):
+    the engine allocates and frees its y block per chunk (c/qwen.c:1115,1141,1155), which
+    the C heap hands back warm after the first chunk."""
+    E = len(tensors) - 1
+    lib.eg_xs_bind(xs, S, D)
+    for es, rows, rtok, _ in chs:
+        if not lib.expert_group_issue_id([tensors[e][0] for e in es], [tensors[e][1] for e in es],
+                                         [tensors[e][2] for e in es], rows, rtok):
+            raise RuntimeError("coli_vk_expert_group_issue_id refused a chunk")
+        lib.expert_group_take_into(ybuf[:len(rtok) * D])
+    g, u, d = tensors[E]
+    if not lib.expert_group_issue([g], [u], [d], [S], xs):
+        raise RuntimeError("coli_vk_expert_group_issue refused the shared expert")
+    lib.expert_group_take_into(ybuf[:S * D])
+
+
 def engine_moe_batch(lib, tensors, xs, S, D, K, tidx, tval, sh_gate):
     """out [S, D] of the routed experts and the shared expert (tensors[e] = (g, u, d) for
     e < E, tensors[E] the shared expert), through the ABI as the engine calls it."""
