@@ -84,36 +84,30 @@ __device__ __forceinline__ void key_decode(unsigned long long key, int *row, flo
     *val = __uint_as_float(u);
 }
 
-// out[r] = the key of rank r (r < kTopK) among keys[0, n) in LDS (src[r] = its index
-// when src != NULL), by counting for each key the keys above it.  keys must be 16-byte
-// aligned and hold zeros from n up to the next multiple of 8 (zero is below every key),
-// so the counting loop reads without conditions.  Real keys are unique (the row is part
-// of the key); equal padding keys share a rank, so out is filled with the padding key
-// (and src with -1) first.  All threads of the block call; ends with __syncthreads().
-__device__ __forceinline__ void rank_keys(const unsigned long long *keys, int n, unsigned long long pad,
-                                          unsigned long long *out, int *src = nullptr) {
-    if (threadIdx.x < kTopK) {
-        out[threadIdx.x] = pad;
-        if (src) src[threadIdx.x] = -1;
-    }
-    __syncthreads();
+// One wave ranks keys[0, n) in LDS (n <= 64; 16-byte aligned, zeros from n up to the next
+// multiple of 8: zero is below every key, so the counting loop reads without conditions)
+// by counting for each key the keys above it; out (LDS) gets the key of rank r < kTopK.
+// Real keys are unique (the row is part of the key); equal padding keys share a rank, so
+// out is filled with the padding key first.  The keys were written by the block before a
+// barrier the caller has passed; only the calling wave's LDS operations touch out, and
+// they complete in issue order, so no block barrier is needed.
+__device__ __forceinline__ void rank_keys_wave(const unsigned long long *keys, int n, unsigned long long pad,
+                                               unsigned long long *out) {
+    const int lane = threadIdx.x & 63;
+    if (lane < kTopK) out[lane] = pad;
+    asm volatile("" ::: "memory");
     const ulonglong2 *k2 = (const ulonglong2 *)keys;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-        const unsigned long long me = keys[c];
-        int r = 0;
-        for (int o = 0; o < (n + 7) / 8 * 4; o += 4) {   // 4 x 16-byte broadcast reads in flight
-            ulonglong2 q[4];
+    const unsigned long long me = lane < n ? keys[lane] : 0ull;
+    int r = 0;
+    for (int o = 0; o < (n + 7) / 8 * 4; o += 4) {
+        ulonglong2 q[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) q[u] = k2[o + u];
+        for (int u = 0; u < 4; u++) q[u] = k2[o + u];
 #pragma unroll
-            for (int u = 0; u < 4; u++) r += (q[u].x > me ? 1 : 0) + (q[u].y > me ? 1 : 0);
-        }
-        if (r < kTopK) {
-            out[r] = me;
-            if (src && me != pad) src[r] = c;
-        }
+        for (int u = 0; u < 4; u++) r += (q[u].x > me ? 1 : 0) + (q[u].y > me ? 1 : 0);
     }
-    __syncthreads();
+    if (lane < n && r < kTopK) out[r] = me;
+    asm volatile("" ::: "memory");
 }
 
 // Arrival counter of a fused top-k launch: two, used by launch-tag parity, after the keys.
@@ -227,15 +221,16 @@ __device__ __forceinline__ void topk_final_block(const TopkArgs &tk, int nblk) {
     const unsigned long long wl = wave_rounds<kTopK>(L, pad);   // lane r: the wave's key of rank r
     if (lane < kTopK) s_wl[wave * kTopK + lane] = wl;
     bad = __syncthreads_or(bad);
-    rank_keys(s_wl, kWaves * kTopK, pad, s_top);
-    if (tid < tk.k) {
+    if (wave != 0) return;   // wave 0 ranks the 4 wave lists and writes the result
+    rank_keys_wave(s_wl, kWaves * kTopK, pad, s_top);
+    if (lane < tk.k) {
         int row;
         float v;
-        key_decode(s_top[tid], &row, &v);
-        tk.out_i[tid] = bad ? -1 : row;
-        tk.out_v[tid] = v;
+        key_decode(s_top[lane], &row, &v);
+        tk.out_i[lane] = bad ? -1 : row;
+        tk.out_v[lane] = v;
     }
-    if (bad && tid == 0) __hip_atomic_store(tk.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (bad && lane == 0) __hip_atomic_store(tk.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The k best of nblk sorted partial lists (k entries each).  The global top k can only
@@ -461,13 +456,16 @@ __global__ __launch_bounds__(kThreads) void gemv6_lanes(const uint8_t *__restric
         __shared__ unsigned long long s_bl[kTopK];
         __shared__ int s_merge;
         if (lane < kTopK) s_wl[wave * kTopK + lane] = tl;
-        rank_keys(s_wl, kWaves * kTopK, pad, s_bl);
-        if (threadIdx.x < kTopK)
-            __hip_atomic_store(tk.slots + (size_t)blockIdx.x * kTopK + threadIdx.x, s_bl[threadIdx.x],
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0)   // arrival count of this launch: the first block merges
-            s_merge = __hip_atomic_fetch_add(topk_counter(tk, tk.epoch), 1u, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) == 0;
+        __syncthreads();
+        if (wave == 0) {   // one wave ranks the block's list and stores it
+            rank_keys_wave(s_wl, kWaves * kTopK, pad, s_bl);
+            if (lane < kTopK)
+                __hip_atomic_store(tk.slots + (size_t)blockIdx.x * kTopK + lane, s_bl[lane], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0)   // arrival count of this launch: the first block merges
+                s_merge = __hip_atomic_fetch_add(topk_counter(tk, tk.epoch), 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) == 0;
+        }
         __syncthreads();
         if (s_merge) topk_final_block(tk, gridDim.x);
     }
