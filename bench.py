@@ -57,10 +57,19 @@ def profile_traffic(name):
 
 
 def profile_mfma(kernel):
-    """MFMA utilisation of a prefill kernel from the committed rocprofv3 counter summary."""
+    """MFMA utilisation of a prefill kernel from the committed rocprofv3 counter summary
+    (not measured by this run; the summary names the commit it was taken at)."""
     try:
         with open(os.path.join(ROOT, "profiles", "pf_mfma_cfg4.json")) as f:
             return json.load(f)["kernels"][kernel]["mfma_util"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def profile_mfma_source():
+    try:
+        with open(os.path.join(ROOT, "profiles", "pf_mfma_cfg4.json")) as f:
+            return "profiles/pf_mfma_cfg4.json, rocprofv3 counters taken at commit " + json.load(f)["source_commit"]
     except (OSError, ValueError, KeyError):
         return None
 
@@ -325,7 +334,8 @@ def moe_prefill_cfg4(lib, torch, dev, layer, steps, warmup):
             "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
             "useful_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
             "frac_bf16_dense_peak": round(flops / (ms * 1e-3) / 2.5e15, 4),
-            "mfma_util_counters": {"pf_gateup": profile_mfma("pf_gateup"), "pf_down": profile_mfma("pf_down")}}
+            "mfma_util_counters": {"pf_gateup": profile_mfma("pf_gateup"), "pf_down": profile_mfma("pf_down"),
+                                   "from": profile_mfma_source()}}
 
 
 def _route_host(lg, K):
