@@ -296,6 +296,10 @@ int   coli_hip_eg_force_gemv(int force_gemv);
  * the decode block (0); returns the previous setting.  A test and bench hook with no
  * counterpart in the reference. */
 int   coli_hip_gqa_seq(int on);
+/* coli_vk_gdn_full_seq's recurrence in closed form per 64-token chunk (1, the default) or
+ * token by token (0); returns the previous setting.  A test and bench hook with no
+ * counterpart in the reference. */
+int   coli_hip_gdn_chunked(int on);
 
 /* ---- fmt=6 container reader (c/st.h:120-456, c/qwen.c:509-536) ----
  * The safetensors shards c/tools/convert_qwen35_moe.py writes (U8 int4 nibbles plus an F32

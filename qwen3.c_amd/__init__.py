@@ -77,6 +77,7 @@ _SIGS = {
     "coli_hip_moe_cert_all": (_I, [_I]),
     "coli_hip_eg_force_gemv": (_I, [_I]),
     "coli_hip_gqa_seq": (_I, [_I]),
+    "coli_hip_gdn_chunked": (_I, [_I]),
     "coli_hip_st_open": (_P, [C.c_char_p]),
     "coli_hip_st_close": (None, [_P]),
     "coli_hip_st_count": (_I, [_P]),
@@ -434,6 +435,11 @@ class Lib:
         """coli_vk_gqa_full over S >= 4 rows batched (True) or token by token (False);
         returns the previous setting."""
         return bool(self.L.coli_hip_gqa_seq(1 if on else 0))
+
+    def gdn_chunked(self, on):
+        """coli_vk_gdn_full_seq's recurrence per 64-token chunk (True) or token by token;
+        returns the previous setting."""
+        return bool(self.L.coli_hip_gdn_chunked(1 if on else 0))
 
     def moe_cert_all(self, on):
         """Certify every decode route on/off (test hook); returns the previous setting."""

@@ -807,6 +807,389 @@ __global__ void gdn_ring_push(const float *__restrict__ qkv, int n, float *__res
     }
 }
 
+// ---------------------------------------------------------------- chunked GatedDeltaNet recurrence
+// The delta rule of c/qwen.c:749-767 (per value column: s = decay s; kv = s . k;
+// delta = (v - kv) beta; s += k delta; y = s . q) over a chunk of kGc tokens from the state
+// s_0, in closed form.  With G_t = sum over j <= t of log decay_j:
+//   s_t = e^{G_t} s_0 + sum_{i <= t} e^{G_t - G_i} k_i delta_i
+//   (I + L) delta = r,  L[t][i] = beta_t e^{G_t - G_i} (k_t . k_i) for i < t,
+//                       r_t = beta_t (v_t - e^{G_t} (k_t . s_0))
+//   y_t = e^{G_t} (q_t . s_0) + sum_{i <= t} e^{G_t - G_i} (q_t . k_i) delta_i
+//   s_end = e^{G_end} s_0 + sum_i e^{G_end - G_i} k_i delta_i
+// Each value column is independent, so a scan block takes kGcCols columns of one v-head
+// through the chunks in order.  T = (I + L)^-1 and M[t][i] = e^{G_t - G_i} (q_t . k_i)
+// (i <= t) depend only on the head and the chunk: gdn_chunk_mats forms them for all chunks
+// at once.  The result equals gdn_seq's token-by-token recurrence up to fp32 rounding (the
+// decays enter as exponentials of summed logs instead of repeated products).  Tokens past
+// the end of the last chunk are padding: k = q = v = 0, beta = 0, decay = 1, so they change
+// nothing and their outputs are not stored.
+static int g_gdn_chunked = 1;  // prefill recurrence in closed form per chunk (0: gdn_seq)
+typedef float coli_v4f __attribute__((ext_vector_type(4)));
+constexpr int kGc = 64;        // tokens per chunk
+constexpr int kGcCols = 16;    // value columns per scan block
+constexpr int kGcConvT = 16;   // tokens per conv block
+constexpr int kGcMaxKD = 128;  // key head dims of the chunked path
+constexpr int kGcMat = 2 * kGc * kGc + 2 * kGc + 4;   // floats per (head, chunk): T, M, e^G, w, e^G_end
+constexpr float kGcMinLog = -87.f;   // log decay clamp: e^-87 is still a normal float
+
+struct GdnChunkArgs {
+    const float *qkv;      // [n][CD] projected inputs of the call's tokens
+    const float *ring;     // [K][CD] previous inputs (see GdnSeqArgs)
+    int head, n;
+    const float *convw;    // [CD][K]
+    const float *params;   // [n][prs]: decay(VH) | beta(VH) | gnorm
+    int prs;
+    float eps;
+    int KH, KD, VH, VD, K, CD, nchunk;
+    float *qn, *kn;        // [n][KH][KD] normed q (times 1/sqrt(KD)) and k
+    float *vv;             // [n][CD] conv + SiLU of every channel (q | k | v)
+    float *mats;           // [VH][nchunk][kGcMat]
+    float *S;              // [VH][VD][KD] state, updated in place
+    float *y;              // [n][VH][VD]
+};
+
+// Conv1d + SiLU of every channel (c/qwen.c:697-707; the window's older inputs first, this
+// token last, as gdn_seq): one thread per channel walks kGcConvT tokens with its K - 1 previous
+// inputs in registers; the loads of a token row are one coalesced pass.
+__global__ __launch_bounds__(kThreads) void gdn_chunk_conv(GdnChunkArgs g) {
+    const int ch = blockIdx.x * kThreads + threadIdx.x, t0 = blockIdx.y * kGcConvT, K = g.K;
+    if (ch >= g.CD) return;
+    float cw[kGdnMaxK], win[kGdnMaxK - 1];
+#pragma unroll
+    for (int q = 0; q < kGdnMaxK; q++) cw[q] = q < K ? g.convw[(size_t)ch * K + q] : 0.f;
+#pragma unroll
+    for (int q = 0; q + 1 < kGdnMaxK; q++) {   // inputs t0 - (K - 1) + q: this call's rows or the ring
+        const int tp = t0 - (K - 1) + q;
+        win[q] = q + 1 >= K ? 0.f
+                 : tp >= 0  ? g.qkv[(size_t)tp * g.CD + ch]
+                            : g.ring[(size_t)((g.head + K + tp) % K) * g.CD + ch];
+    }
+    const int nt = min(kGcConvT, g.n - t0);
+    constexpr int kU = 8;   // token rows loaded ahead
+    for (int j0 = 0; j0 < nt; j0 += kU) {
+        float xin[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) xin[u] = j0 + u < nt ? g.qkv[(size_t)(t0 + j0 + u) * g.CD + ch] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            if (j0 + u >= nt) break;
+            float acc = 0.f;
+#pragma unroll
+            for (int q = 0; q + 1 < kGdnMaxK; q++)
+                if (q + 1 < K) acc += cw[q] * win[q];
+            acc += cw[K - 1] * xin[u];
+#pragma unroll
+            for (int q = 0; q + 1 < kGdnMaxK; q++) {
+                if (q + 2 < K) win[q] = win[q + 1];
+                else if (q + 2 == K) win[q] = xin[u];
+            }
+            g.vv[(size_t)(t0 + j0 + u) * g.CD + ch] = silu_f(acc);
+        }
+    }
+}
+
+// l2 norms of q and k (c/qwen.c:713-721): one wave per (token, head), each lane's columns
+// summed in order and the wave's sum by DPP, as gdn_seq does it.
+__global__ __launch_bounds__(kThreads) void gdn_chunk_norm(GdnChunkArgs g) {
+    const int w = blockIdx.x * kWaves + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int tok = w / (2 * g.KH), hh = w % (2 * g.KH);
+    if (tok >= g.n) return;   // wave uniform
+    const float *v = g.vv + (size_t)tok * g.CD + (size_t)hh * g.KD;
+    float x[kGcMaxKD / 64];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGcMaxKD / 64; i++) {
+        const int d = lane + 64 * i;
+        x[i] = d < g.KD ? v[d] : 0.f;
+        if (d < g.KD) ss += x[i] * x[i];
+    }
+    ss = wave_sum_f(ss);
+    const bool isq = hh < g.KH;
+    const float r = isq ? 1.f / sqrtf(ss + g.eps) / sqrtf((float)g.KD) : 1.f / sqrtf(ss + g.eps);
+    float *dst = isq ? g.qn + ((size_t)tok * g.KH + hh) * g.KD : g.kn + ((size_t)tok * g.KH + hh - g.KH) * g.KD;
+#pragma unroll
+    for (int i = 0; i < kGcMaxKD / 64; i++) {
+        const int d = lane + 64 * i;
+        if (d < g.KD) dst[d] = x[i] * r;
+    }
+}
+
+// Rows [t0, t0 + kGc) of a [n][KH][KD] array for k-head src into s[kGc][ld] (zeros past n),
+// 16-byte loads, all of a thread's loads issued before its stores.
+template <int LD>
+__device__ __forceinline__ void gc_rows(const float *a, int t0, int n, int KH, int src, int KD, float (*s)[LD]) {
+    constexpr int kPer = kGc * kGcMaxKD / 4 / kThreads;   // float4 per thread at KD = kGcMaxKD (8)
+    const int q4 = KD / 4;
+    float4 v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int f = threadIdx.x + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
+        v[i] = t < kGc && t0 + t < n ? *(const float4 *)(a + ((size_t)(t0 + t) * KH + src) * KD + e)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int f = threadIdx.x + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
+        if (t < kGc) *(float4 *)&s[t][e] = v[i];
+    }
+}
+
+// One block per (v-head, chunk): G, the Gram products, T = (I + L)^-1 and M, the products on
+// fp32 MFMA in the lane layout of gdn_chunk_scan.  T by block forward substitution over its
+// 16 x 16 blocks: wave w inverts diagonal block w by rows, one lane per column, then block
+// (r, c) = -T[r][r] sum_{c <= m < r} L[r][m] T[m][c], one block distance at a time.
+__global__ __launch_bounds__(kThreads) void gdn_chunk_mats(GdnChunkArgs g) {
+    constexpr int LDK = kGcMaxKD + 4, LDT = kGc + 4, NB = kGc / 16;
+    static_assert(NB == kWaves, "one diagonal block per wave");
+    __shared__ __attribute__((aligned(16))) float sK[kGc][LDK], sQ[kGc][LDK];
+    __shared__ __attribute__((aligned(16))) float sL[kGc][LDT], sT[kGc][LDT];
+    __shared__ float sG[kGc], sBe[kGc];
+    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, KD = g.KD;
+    const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const int src = h / (g.VH / g.KH), t0 = c * kGc, nt = min(kGc, g.n - t0);
+    gc_rows<LDK>(g.kn, t0, g.n, g.KH, src, KD, sK);
+    gc_rows<LDK>(g.qn, t0, g.n, g.KH, src, KD, sQ);
+    for (int i = tid; i < kGc * LDT; i += kThreads) (&sT[0][0])[i] = 0.f;
+    if (wave == 0) {   // G_t: the logs up to t, an inclusive scan across the wave (kGc = 64)
+        const bool on = lane < nt;
+        float a = on ? fmaxf(logf(g.params[(size_t)(t0 + lane) * g.prs + h]), kGcMinLog) : 0.f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float u = __shfl_up(a, o);
+            if (lane >= o) a += u;
+        }
+        sG[lane] = a;
+        sBe[lane] = on ? g.params[(size_t)(t0 + lane) * g.prs + g.VH + h] : 0.f;
+    }
+    __syncthreads();
+    auto mfma = [](float a, float b, coli_v4f c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); };
+    float *mat = g.mats + ((size_t)h * g.nchunk + c) * kGcMat;   // T [kGc][kGc] | M | e^G | w | e^G_end
+    // Gram tiles (ti, tj <= ti): ten of K K^T (into L), then ten of Q K^T (into M)
+    for (int u = wave; u < NB * (NB + 1); u += kWaves) {
+        const bool isq = u >= NB * (NB + 1) / 2;
+        const int v = isq ? u - NB * (NB + 1) / 2 : u;
+        int ti = 0;
+        while ((ti + 1) * (ti + 2) / 2 <= v) ti++;
+        const int tj = v - ti * (ti + 1) / 2;
+        const float(*A)[LDK] = isq ? sQ : sK;
+        coli_v4f acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb < KD; kb += 16) {
+            const float4 a4 = *(const float4 *)&A[16 * ti + li][kb + 4 * lg];
+            const float4 b4 = *(const float4 *)&sK[16 * tj + li][kb + 4 * lg];
+            acc = mfma(a4.x, b4.x, acc);
+            acc = mfma(a4.y, b4.y, acc);
+            acc = mfma(a4.z, b4.z, acc);
+            acc = mfma(a4.w, b4.w, acc);
+        }
+        const int i = 16 * tj + li;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int t = 16 * ti + 4 * lg + r;
+            const float dec = expf(sG[t] - sG[min(i, t)]);
+            if (!isq) sL[t][i] = i < t ? sBe[t] * dec * acc[r] : 0.f;
+            else mat[kGc * kGc + t * kGc + i] = i <= t ? dec * acc[r] : 0.f;
+        }
+    }
+    for (int idx = tid; idx < kGc * kGc; idx += kThreads) {   // M right of the diagonal blocks
+        const int t = idx / kGc, i = idx % kGc;
+        if (i / 16 > t / 16) mat[kGc * kGc + idx] = 0.f;
+    }
+    __syncthreads();
+    {   // diagonal block wave: T[t][j] = [t == j] - sum_{i < t} L[t][i] T[i][j], column j = li
+        const int o = 16 * wave;
+        float col[16];
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            float acc = t == li ? 1.f : 0.f;
+#pragma unroll
+            for (int i = 0; i < t; i++) acc = fmaf(-sL[o + t][o + i], col[i], acc);
+            col[t] = acc;
+        }
+        if (lg == 0) {
+#pragma unroll
+            for (int t = 0; t < 16; t++) sT[o + t][o + li] = col[t];
+        }
+    }
+    __syncthreads();
+    for (int dist = 1; dist < NB; dist++) {
+        const int cb = wave, rb = wave + dist;
+        if (rb < NB) {   // wave uniform
+            coli_v4f x = {0.f, 0.f, 0.f, 0.f};
+            for (int mb = cb; mb < rb; mb++) {   // X = sum_mb L[rb][mb] T[mb][cb]
+                const float4 l4 = *(const float4 *)&sL[16 * rb + li][16 * mb + 4 * lg];
+                x = mfma(l4.x, sT[16 * mb + 4 * lg][16 * cb + li], x);
+                x = mfma(l4.y, sT[16 * mb + 4 * lg + 1][16 * cb + li], x);
+                x = mfma(l4.z, sT[16 * mb + 4 * lg + 2][16 * cb + li], x);
+                x = mfma(l4.w, sT[16 * mb + 4 * lg + 3][16 * cb + li], x);
+            }
+            // T[rb][cb] = -T[rb][rb] X, X as B in its D layout (register s holds k = 4 lg + s)
+            const float4 d4 = *(const float4 *)&sT[16 * rb + li][16 * rb + 4 * lg];
+            coli_v4f y = {0.f, 0.f, 0.f, 0.f};
+            y = mfma(d4.x, x[0], y);
+            y = mfma(d4.y, x[1], y);
+            y = mfma(d4.z, x[2], y);
+            y = mfma(d4.w, x[3], y);
+#pragma unroll
+            for (int r = 0; r < 4; r++) sT[16 * rb + 4 * lg + r][16 * cb + li] = -y[r];
+        }
+        __syncthreads();
+    }
+    for (int i = tid; i < kGc * kGc / 4; i += kThreads)
+        ((float4 *)mat)[i] = *(const float4 *)&sT[4 * i / kGc][4 * i % kGc];
+    if (tid < kGc) {
+        mat[2 * kGc * kGc + tid] = expf(sG[tid]);
+        mat[2 * kGc * kGc + kGc + tid] = expf(sG[kGc - 1] - sG[tid]);
+    }
+    if (tid == 0) mat[2 * kGc * kGc + 2 * kGc] = expf(sG[kGc - 1]);
+}
+
+// One block per (v-head, kGcCols value columns): the chunks in order, the columns' state
+// slice in LDS, every product on fp32 MFMA (v_mfma_f32_16x16x4_f32: lane l gives A[l % 16]
+// [l / 16] and B[l / 16][l % 16]; D[4 (l / 16) + r][l % 16] is its register r).  A lane
+// gives the four k = kb + 4 (l / 16) + s of a 16-wide k block over four MFMAs (s = 0..3),
+// so each operand is one 16-byte LDS read, and D's layout is B's for the next product.
+// Wave w forms tokens 16 w .. + 15 of a = K s, b = Q s, r, delta = T r and y = e^G b + M delta
+// (T and M are zero right of the diagonal block) and key tiles w, w + 4, .. of the state.
+// The next chunk's operands are loaded into registers while this one is computed.
+__global__ __launch_bounds__(kThreads) void gdn_chunk_scan(GdnChunkArgs g) {
+    constexpr int LDK = kGcMaxKD + 4, LDT = kGc + 4;
+    __shared__ __attribute__((aligned(16))) float sK[kGc][LDK], sQ[kGc][LDK];
+    __shared__ __attribute__((aligned(16))) float sT[kGc][LDT], sM[kGc][LDT];
+    __shared__ __attribute__((aligned(16))) float sS[kGcCols][LDK];   // state slice, [column][key]
+    __shared__ __attribute__((aligned(16))) float sR[kGcCols][LDT], sD[kGcCols][LDT], sWD[kGcCols][LDT];
+    const int nsl = g.VD / kGcCols, h = blockIdx.x / nsl, c0 = (blockIdx.x % nsl) * kGcCols;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const int KD = g.KD, q4 = KD / 4, src = h / (g.VH / g.KH), key_dim = g.KH * KD;
+    const int row0 = 16 * wave + 4 * lg;   // the tokens of this lane's D registers
+    for (int i = tid; i < KD * kGcCols; i += kThreads) {
+        const int e = i % KD, cc = i / KD;
+        sS[cc][e] = g.S[((size_t)h * g.VD + c0 + cc) * KD + e];
+    }
+    constexpr int kKQ = kGc * kGcMaxKD / 4 / kThreads, kTM = kGc * kGc / 4 / kThreads;
+    coli_v4f pk[kKQ], pq[kKQ], pt[kTM], pm[kTM];
+    float4 pe, pw;
+    float pv[4], pb[4], pend;
+    auto fetch = [&](int c) {
+        const int t0 = c * kGc;
+        const float *mat = g.mats + ((size_t)h * g.nchunk + c) * kGcMat;
+#pragma unroll
+        for (int i = 0; i < kKQ; i++) {
+            const int f = tid + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
+            const bool on = t < kGc && t0 + t < g.n;
+            const size_t o = ((size_t)(t0 + t) * g.KH + src) * KD + e;
+            pk[i] = on ? *(const coli_v4f *)(g.kn + o) : coli_v4f{0.f, 0.f, 0.f, 0.f};
+            pq[i] = on ? *(const coli_v4f *)(g.qn + o) : coli_v4f{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < kTM; i++) {
+            pt[i] = ((const coli_v4f *)mat)[tid + i * kThreads];
+            pm[i] = ((const coli_v4f *)(mat + kGc * kGc))[tid + i * kThreads];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int t = t0 + row0 + r;
+            pv[r] = t < g.n ? g.vv[(size_t)t * g.CD + 2 * key_dim + (size_t)h * g.VD + c0 + li] : 0.f;
+            pb[r] = t < g.n ? g.params[(size_t)t * g.prs + g.VH + h] : 0.f;
+        }
+        pe = *(const float4 *)(mat + 2 * kGc * kGc + row0);
+        pw = *(const float4 *)(mat + 2 * kGc * kGc + kGc + row0);
+        pend = mat[2 * kGc * kGc + 2 * kGc];
+    };
+    auto mfma = [](float a, float b, coli_v4f c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); };
+    fetch(0);
+    for (int c = 0; c < g.nchunk; c++) {
+        const int t0 = c * kGc;
+#pragma unroll
+        for (int i = 0; i < kKQ; i++) {
+            const int f = tid + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
+            if (t < kGc) {
+                *(coli_v4f *)&sK[t][e] = pk[i];
+                *(coli_v4f *)&sQ[t][e] = pq[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kTM; i++) {
+            const int f = 4 * (tid + i * kThreads), t = f / kGc, j = f % kGc;
+            *(coli_v4f *)&sT[t][j] = pt[i];
+            *(coli_v4f *)&sM[t][j] = pm[i];
+        }
+        const float4 eg = pe, wt = pw;
+        const float eend = pend;
+        float v[4], be[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            v[r] = pv[r];
+            be[r] = pb[r];
+        }
+        __syncthreads();   // the chunk's K, Q, T, M and the state slice in LDS
+        if (c + 1 < g.nchunk) fetch(c + 1);
+        // a = K s and b = Q s
+        coli_v4f a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb < KD; kb += 16) {
+            const float4 k4 = *(const float4 *)&sK[16 * wave + li][kb + 4 * lg];
+            const float4 x4 = *(const float4 *)&sQ[16 * wave + li][kb + 4 * lg];
+            const float4 s4 = *(const float4 *)&sS[li][kb + 4 * lg];
+            a = mfma(k4.x, s4.x, a);
+            b = mfma(x4.x, s4.x, b);
+            a = mfma(k4.y, s4.y, a);
+            b = mfma(x4.y, s4.y, b);
+            a = mfma(k4.z, s4.z, a);
+            b = mfma(x4.z, s4.z, b);
+            a = mfma(k4.w, s4.w, a);
+            b = mfma(x4.w, s4.w, b);
+        }
+        // r = beta (v - e^G a)
+        *(float4 *)&sR[li][row0] = make_float4(be[0] * (v[0] - eg.x * a[0]), be[1] * (v[1] - eg.y * a[1]),
+                                               be[2] * (v[2] - eg.z * a[2]), be[3] * (v[3] - eg.w * a[3]));
+        __syncthreads();
+        // delta = T r
+        coli_v4f d = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb <= 16 * wave; kb += 16) {
+            const float4 t4 = *(const float4 *)&sT[16 * wave + li][kb + 4 * lg];
+            const float4 r4 = *(const float4 *)&sR[li][kb + 4 * lg];
+            d = mfma(t4.x, r4.x, d);
+            d = mfma(t4.y, r4.y, d);
+            d = mfma(t4.z, r4.z, d);
+            d = mfma(t4.w, r4.w, d);
+        }
+        *(float4 *)&sD[li][row0] = make_float4(d[0], d[1], d[2], d[3]);
+        *(float4 *)&sWD[li][row0] = make_float4(wt.x * d[0], wt.y * d[1], wt.z * d[2], wt.w * d[3]);
+        __syncthreads();
+        // y = e^G b + M delta
+        coli_v4f y = {eg.x * b[0], eg.y * b[1], eg.z * b[2], eg.w * b[3]};
+        for (int kb = 0; kb <= 16 * wave; kb += 16) {
+            const float4 m4 = *(const float4 *)&sM[16 * wave + li][kb + 4 * lg];
+            const float4 d4 = *(const float4 *)&sD[li][kb + 4 * lg];
+            y = mfma(m4.x, d4.x, y);
+            y = mfma(m4.y, d4.y, y);
+            y = mfma(m4.z, d4.z, y);
+            y = mfma(m4.w, d4.w, y);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (t0 + row0 + r < g.n) g.y[((size_t)(t0 + row0 + r) * g.VH + h) * g.VD + c0 + li] = y[r];
+        // s = e^G_end s + K^T (w delta), key tile m: A[e][t] = K[t][16 m + e]
+        for (int m = wave; m < KD / 16; m += kWaves) {
+            const float4 s4 = *(const float4 *)&sS[li][16 * m + 4 * lg];
+            coli_v4f acc = {eend * s4.x, eend * s4.y, eend * s4.z, eend * s4.w};
+#pragma unroll 4
+            for (int kb = 0; kb < kGc; kb += 16) {
+                const float4 w4 = *(const float4 *)&sWD[li][kb + 4 * lg];
+                acc = mfma(sK[kb + 4 * lg][16 * m + li], w4.x, acc);
+                acc = mfma(sK[kb + 4 * lg + 1][16 * m + li], w4.y, acc);
+                acc = mfma(sK[kb + 4 * lg + 2][16 * m + li], w4.z, acc);
+                acc = mfma(sK[kb + 4 * lg + 3][16 * m + li], w4.w, acc);
+            }
+            *(float4 *)&sS[li][16 * m + 4 * lg] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        }
+        __syncthreads();   // the chunk's operands are replaced by the next chunk's
+    }
+    for (int i = tid; i < KD * kGcCols; i += kThreads) {
+        const int e = i % KD, cc = i / KD;
+        g.S[((size_t)h * g.VD + c0 + cc) * KD + e] = sS[cc][e];
+    }
+}
+
 // ---------------------------------------------------------------- GQA attention
 constexpr int kAttT = 32;       // positions per chunk (block)
 constexpr int kAttW = 8;        // waves of an attn_part block
@@ -1340,7 +1723,6 @@ __global__ __launch_bounds__(64) void qk_rows(const float *__restrict__ qraw, co
 //     (step kk of group g is key 4 g + kk); lane l, register r of dim tile t is
 //     (dim 16 t + 4 (l / 16) + r, query l % 16).  Every per-query value (max, sum, rescale)
 //     stays in the lanes of its query.
-typedef float coli_v4f __attribute__((ext_vector_type(4)));
 constexpr int kPQ = 16, kPKey = 16;
 struct AttnRowsArgs {
     const float *qraw;    // [S][H][2 hd]: q | gate per head
@@ -1610,7 +1992,7 @@ static bool put_vec(float **d, int *have, const float *h, int n, const char *who
 // ---------------------------------------------------------------- work buffers
 enum {
     W_Q, W_K, W_V, W_CTX, W_PART, W_QKV, W_Z, W_Y, W_AB, W_NRM, W_LOGIT, W_IDX, W_IO_X, W_IO_R, W_IO_P, W_IO_O,
-    W_HIST, W_BND, W_SQKV, W_SZ, W_SY, W_ROPE, W_COUNT
+    W_HIST, W_BND, W_SQKV, W_SZ, W_SY, W_ROPE, W_GQN, W_GKN, W_GVV, W_GMAT, W_COUNT
 };
 struct WorkBuf {
     void *p = nullptr;
@@ -2322,6 +2704,12 @@ COLI_API int coli_hip_gqa_seq(int on) {
     return prev;
 }
 
+COLI_API int coli_hip_gdn_chunked(int on) {
+    const int prev = g_gdn_chunked;
+    g_gdn_chunked = on ? 1 : 0;
+    return prev;
+}
+
 // The staged forms take host-computed q (already normed and rotated) and the host KV
 // mirror rows; the engine only reaches them when the fused block is off.  Not provided:
 // 0 makes the engine attend on the CPU (c/qwen.c:620-636).
@@ -2407,8 +2795,10 @@ COLI_API int coli_vk_gdn_ba_weight(int layer, const float *alog, const float *dt
 
 // GDN prefill over S >= kGemmMinS tokens with host params (c/backend_vulkan.c:2018-2157),
 // per chunk of up to kGdnSeqChunk tokens: qkv and z of all the chunk's rows in one dense
-// GEMM (one digit decomposition of x), the recurrence of the chunk in one gdn_seq launch,
-// the ring push, then the gated norm and out-projection of all rows in one more GEMM.
+// GEMM (one digit decomposition of x), the recurrence of the chunk (gdn_chunk_prep /
+// _mats / _scan over 64-token pieces; gdn_seq token by token for other shapes or when
+// coli_hip_gdn_chunked(0)), the ring push, then the gated norm and out-projection of all
+// rows in one more GEMM.
 // False with nothing launched when the shapes are not the GEMM's or the conv is longer than
 // gdn_seq's register window (the caller then runs the tokens one at a time).
 constexpr int kGdnSeqChunk = 1024;
@@ -2454,12 +2844,44 @@ static bool gdn_chunks(int gi, const float *dx, const float *dp, int S, const Co
         a.VD = d.VD;
         a.K = d.K;
         a.CD = d.CD;
-        const dim3 grid(d.VH * (d.VD / kSeqCols));
-        switch (d.KD / 64) {
-        case 1: hipLaunchKernelGGL(gdn_seq<1>, grid, dim3(kThreads), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(gdn_seq<2>, grid, dim3(kThreads), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(gdn_seq<4>, grid, dim3(kThreads), 0, st, a); break;
-        default: return refuse("GDN key head dim not in {64, 128, 256}");
+        if (g_gdn_chunked && d.KD <= kGcMaxKD && d.KD % 16 == 0 && d.VD % kGcCols == 0) {
+            const int nchunk = (n + kGc - 1) / kGc;
+            GdnChunkArgs c;
+            c.qkv = qkv;
+            c.ring = G.ring;
+            c.head = G.head;
+            c.n = n;
+            c.convw = G.convw;
+            c.params = a.params;
+            c.prs = prs;
+            c.eps = d.eps;
+            c.KH = d.KH;
+            c.KD = d.KD;
+            c.VH = d.VH;
+            c.VD = d.VD;
+            c.K = d.K;
+            c.CD = d.CD;
+            c.nchunk = nchunk;
+            c.qn = wbuf(W_GQN, (size_t)n * d.KH * d.KD);
+            c.kn = wbuf(W_GKN, (size_t)n * d.KH * d.KD);
+            c.vv = wbuf(W_GVV, (size_t)n * d.CD);
+            c.mats = wbuf(W_GMAT, (size_t)d.VH * nchunk * kGcMat);
+            c.S = G.S;
+            c.y = y;
+            if (!c.qn || !c.kn || !c.vv || !c.mats) return false;
+            hipLaunchKernelGGL(gdn_chunk_conv, dim3((d.CD + kThreads - 1) / kThreads, (n + kGcConvT - 1) / kGcConvT),
+                               dim3(kThreads), 0, st, c);
+            hipLaunchKernelGGL(gdn_chunk_norm, dim3((n * 2 * d.KH + kWaves - 1) / kWaves), dim3(kThreads), 0, st, c);
+            hipLaunchKernelGGL(gdn_chunk_mats, dim3(d.VH, nchunk), dim3(kThreads), 0, st, c);
+            hipLaunchKernelGGL(gdn_chunk_scan, dim3(d.VH * (d.VD / kGcCols)), dim3(kThreads), 0, st, c);
+        } else {
+            const dim3 grid(d.VH * (d.VD / kSeqCols));
+            switch (d.KD / 64) {
+            case 1: hipLaunchKernelGGL(gdn_seq<1>, grid, dim3(kThreads), 0, st, a); break;
+            case 2: hipLaunchKernelGGL(gdn_seq<2>, grid, dim3(kThreads), 0, st, a); break;
+            case 4: hipLaunchKernelGGL(gdn_seq<4>, grid, dim3(kThreads), 0, st, a); break;
+            default: return refuse("GDN key head dim not in {64, 128, 256}");
+            }
         }
         const int pushed = min(n, d.K) * d.CD;
         hipLaunchKernelGGL(gdn_ring_push, dim3((pushed + 255) / 256), dim3(256), 0, st, qkv, n, G.ring, G.head, d.K,

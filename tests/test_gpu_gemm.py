@@ -141,7 +141,16 @@ def _rel_to_max(got, ref):
     return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / max(1e-30, float(np.max(np.abs(ref)))))
 
 
-def test_gdn_seq_cfg3(lib, lorc, gen):
+@pytest.fixture(params=["chunked", "token loop"])
+def gdn_path(request, lib):
+    """The prefill recurrence: closed form per 64-token chunk (the default) or the
+    token-by-token loop (the fallback for shapes the chunked kernels do not take)."""
+    prev = lib.gdn_chunked(request.param == "chunked")
+    yield request.param
+    lib.gdn_chunked(prev)
+
+
+def test_gdn_seq_cfg3(lib, lorc, gen, gdn_path):
     """configs[3] GatedDeltaNet geometry (KH 16, KD 128, VH 32, VD 128, conv 4, gs 128):
     40 tokens in one call, 6 in a second, then one decode token (S = 1, the per-token
     kernels) on the ring and state the chunks left."""
@@ -157,9 +166,10 @@ def test_gdn_seq_cfg3(lib, lorc, gen):
     assert _rel_to_max(S, st[1]) < 1e-4
 
 
-def test_gdn_seq_chunks(lib, lorc, gen):
-    """A small layer (D 256, KH 2, KD 64, VH 4, VD 32, gs 128) over 1030 tokens: two chunks
-    (1024 + 6) in one call, the ring carried across the chunk boundary."""
+def test_gdn_seq_chunks(lib, lorc, gen, gdn_path):
+    """A small layer (D 256, KH 2, KD 64, VH 4, VD 32, gs 128) over 1030 tokens: two input
+    pieces (1024 + 6) in one call, the ring carried across the piece boundary; the chunked
+    recurrence takes 16 full 64-token chunks and a 6-token one."""
     D, KH, KD, VH, VD, K, gs, layer = 256, 2, 64, 4, 32, 4, 128, 10
     W = _layers.GdnWeights(gen, gen.stream(0x6F80, layer), D, KH, KD, VH, VD, K, gs)
     ts = tuple(m.upload(lib) for m in (W.qkv, W.z, W.out))
