@@ -453,8 +453,9 @@ def gemm_prefill(lib, torch, dev, steps, warmup):
 def gdn_prefill_cfg3(lib, calls=5):
     """One GatedDeltaNet layer at configs[3] geometry over S = 512 tokens through the ABI
     call the engine makes for prefill (coli_vk_gdn_full_seq, host buffers in and out,
-    c/qwen.c:1370): qkv + z in one GEMM, the chunk's recurrence in one launch, gated norm +
-    out-projection in one GEMM.  Wall clock per call, PCIe included."""
+    c/qwen.c:1370): qkv + z in one GEMM, the recurrence in closed form per 64-token chunk
+    (conv, norms, per-chunk matrices, scan), gated norm + out-projection in one GEMM.  Wall
+    clock per call, PCIe included."""
     import numpy as np
     D, KH, KD, VH, VD, K, S, layer = K_HID, 16, 128, 32, 128, 4, 512, 150
     CD = 2 * KH * KD + VH * VD

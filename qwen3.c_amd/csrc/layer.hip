@@ -1049,69 +1049,97 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_mats(GdnChunkArgs g) {
 // gives the four k = kb + 4 (l / 16) + s of a 16-wide k block over four MFMAs (s = 0..3),
 // so each operand is one 16-byte LDS read, and D's layout is B's for the next product.
 // Wave w forms tokens 16 w .. + 15 of a = K s, b = Q s, r, delta = T r and y = e^G b + M delta
-// (T and M are zero right of the diagonal block) and key tiles w, w + 4, .. of the state.
-// The next chunk's operands are loaded into registers while this one is computed.
+// and key tiles w, w + 4, .. of the state.  T and M are zero right of their diagonal blocks,
+// so every wave takes all four token blocks of T r and M delta (wave 3 needs them all anyway)
+// and issues its LDS reads before its MFMAs.  The next chunk's operands are loaded into
+// registers in three parts between the k blocks of a and b, one load per two MFMAs (the
+// scheduler's group barriers), while the MFMAs run.
+template <int KD>
 __global__ __launch_bounds__(kThreads) void gdn_chunk_scan(GdnChunkArgs g) {
-    constexpr int LDK = kGcMaxKD + 4, LDT = kGc + 4;
+    static_assert(KD % 64 == 0 && KD <= kGcMaxKD, "key tiles per wave");
+    constexpr int LDK = KD + 4, LDT = kGc + 4, NTB = kGc / 16, kTW = KD / 16 / kWaves;
+    constexpr int kKQ = kGc * KD / 4 / kThreads, kTM = kGc * kGc / 4 / kThreads, kSV = kGcCols * KD / 4 / kThreads;
     __shared__ __attribute__((aligned(16))) float sK[kGc][LDK], sQ[kGc][LDK];
     __shared__ __attribute__((aligned(16))) float sT[kGc][LDT], sM[kGc][LDT];
     __shared__ __attribute__((aligned(16))) float sS[kGcCols][LDK];   // state slice, [column][key]
     __shared__ __attribute__((aligned(16))) float sR[kGcCols][LDT], sD[kGcCols][LDT], sWD[kGcCols][LDT];
     const int nsl = g.VD / kGcCols, h = blockIdx.x / nsl, c0 = (blockIdx.x % nsl) * kGcCols;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-    const int KD = g.KD, q4 = KD / 4, src = h / (g.VH / g.KH), key_dim = g.KH * KD;
-    const int row0 = 16 * wave + 4 * lg;   // the tokens of this lane's D registers
-    for (int i = tid; i < KD * kGcCols; i += kThreads) {
-        const int e = i % KD, cc = i / KD;
-        sS[cc][e] = g.S[((size_t)h * g.VD + c0 + cc) * KD + e];
+    const int src = h / (g.VH / g.KH), key_dim = g.KH * KD;
+    const int row0 = 16 * wave + 4 * lg, r16 = 16 * wave + li;   // D rows of this lane; A row
+    // the slice's columns are adjacent in S ([VH][VD][KD]): one contiguous run of kGcCols KD floats
+    coli_v4f *Sg = (coli_v4f *)(g.S + ((size_t)h * g.VD + c0) * KD);
+    {
+        coli_v4f sv[kSV];
+#pragma unroll
+        for (int i = 0; i < kSV; i++) sv[i] = Sg[tid + i * kThreads];
+#pragma unroll
+        for (int i = 0; i < kSV; i++) {
+            const int f = 4 * (tid + i * kThreads);
+            *(coli_v4f *)&sS[f / KD][f % KD] = sv[i];
+        }
     }
-    constexpr int kKQ = kGc * kGcMaxKD / 4 / kThreads, kTM = kGc * kGc / 4 / kThreads;
     coli_v4f pk[kKQ], pq[kKQ], pt[kTM], pm[kTM];
     float4 pe, pw;
     float pv[4], pb[4], pend;
-    auto fetch = [&](int c) {
-        const int t0 = c * kGc;
-        const float *mat = g.mats + ((size_t)h * g.nchunk + c) * kGcMat;
+    // The loads of a chunk go through buffer descriptors bounded by the arrays' sizes, so rows
+    // past n (and a chunk past the last) read as zeros without a branch; a chunk past the last
+    // of head h reads head h + 1's first matrices or zeros, and is never stored.
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(g.kn, (uint32_t)g.n * g.KH * KD * 4u);
+    const __amdgpu_buffer_rsrc_t rq = buf_rsrc(g.qn, (uint32_t)g.n * g.KH * KD * 4u);
+    const __amdgpu_buffer_rsrc_t rm = buf_rsrc(g.mats, (uint32_t)g.VH * g.nchunk * kGcMat * 4u);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(g.vv, (uint32_t)g.n * g.CD * 4u);
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(g.params, (uint32_t)g.n * g.prs * 4u);
+    auto ld4 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return __builtin_bit_cast(coli_v4f, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    };
+    auto ld1 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+    };
+    auto fetch_kq = [&](int c, __amdgpu_buffer_rsrc_t r, coli_v4f *dst) {
+        const uint32_t t0 = (uint32_t)c * kGc;
 #pragma unroll
         for (int i = 0; i < kKQ; i++) {
-            const int f = tid + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
-            const bool on = t < kGc && t0 + t < g.n;
-            const size_t o = ((size_t)(t0 + t) * g.KH + src) * KD + e;
-            pk[i] = on ? *(const coli_v4f *)(g.kn + o) : coli_v4f{0.f, 0.f, 0.f, 0.f};
-            pq[i] = on ? *(const coli_v4f *)(g.qn + o) : coli_v4f{0.f, 0.f, 0.f, 0.f};
+            const int f = tid + i * kThreads, t = f / (KD / 4), e = (f % (KD / 4)) * 4;
+            dst[i] = ld4(r, (((t0 + t) * g.KH + src) * KD + e) * 4u);
         }
+    };
+    auto fetch_rest = [&](int c) {
+        const uint32_t t0 = (uint32_t)c * kGc, mo = ((uint32_t)h * g.nchunk + c) * kGcMat;
 #pragma unroll
         for (int i = 0; i < kTM; i++) {
-            pt[i] = ((const coli_v4f *)mat)[tid + i * kThreads];
-            pm[i] = ((const coli_v4f *)(mat + kGc * kGc))[tid + i * kThreads];
+            pt[i] = ld4(rm, (mo + 4 * (tid + i * kThreads)) * 4u);
+            pm[i] = ld4(rm, (mo + kGc * kGc + 4 * (tid + i * kThreads)) * 4u);
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int t = t0 + row0 + r;
-            pv[r] = t < g.n ? g.vv[(size_t)t * g.CD + 2 * key_dim + (size_t)h * g.VD + c0 + li] : 0.f;
-            pb[r] = t < g.n ? g.params[(size_t)t * g.prs + g.VH + h] : 0.f;
+            const uint32_t t = t0 + row0 + r;
+            pv[r] = ld1(rv, (t * g.CD + 2 * key_dim + h * g.VD + c0 + li) * 4u);
+            pb[r] = ld1(rp, (t * g.prs + g.VH + h) * 4u);
         }
-        pe = *(const float4 *)(mat + 2 * kGc * kGc + row0);
-        pw = *(const float4 *)(mat + 2 * kGc * kGc + kGc + row0);
-        pend = mat[2 * kGc * kGc + 2 * kGc];
+        const coli_v4f e4 = ld4(rm, (mo + 2 * kGc * kGc + row0) * 4u);
+        const coli_v4f w4 = ld4(rm, (mo + 2 * kGc * kGc + kGc + row0) * 4u);
+        pe = make_float4(e4[0], e4[1], e4[2], e4[3]);
+        pw = make_float4(w4[0], w4[1], w4[2], w4[3]);
+        pend = ld1(rm, (mo + 2 * kGc * kGc + 2 * kGc) * 4u);
     };
     auto mfma = [](float a, float b, coli_v4f c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); };
-    fetch(0);
+    fetch_kq(0, rk, pk);
+    fetch_kq(0, rq, pq);
+    fetch_rest(0);
     for (int c = 0; c < g.nchunk; c++) {
         const int t0 = c * kGc;
 #pragma unroll
         for (int i = 0; i < kKQ; i++) {
-            const int f = tid + i * kThreads, t = f / q4, e = (f - t * q4) * 4;
-            if (t < kGc) {
-                *(coli_v4f *)&sK[t][e] = pk[i];
-                *(coli_v4f *)&sQ[t][e] = pq[i];
-            }
+            const int f = tid + i * kThreads, t = f / (KD / 4), e = (f % (KD / 4)) * 4;
+            *(coli_v4f *)&sK[t][e] = pk[i];
+            *(coli_v4f *)&sQ[t][e] = pq[i];
         }
 #pragma unroll
         for (int i = 0; i < kTM; i++) {
-            const int f = 4 * (tid + i * kThreads), t = f / kGc, j = f % kGc;
-            *(coli_v4f *)&sT[t][j] = pt[i];
-            *(coli_v4f *)&sM[t][j] = pm[i];
+            const int f = 4 * (tid + i * kThreads);
+            *(coli_v4f *)&sT[f / kGc][f % kGc] = pt[i];
+            *(coli_v4f *)&sM[f / kGc][f % kGc] = pm[i];
         }
         const float4 eg = pe, wt = pw;
         const float eend = pend;
@@ -1122,71 +1150,86 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_scan(GdnChunkArgs g) {
             be[r] = pb[r];
         }
         __syncthreads();   // the chunk's K, Q, T, M and the state slice in LDS
-        if (c + 1 < g.nchunk) fetch(c + 1);
         // a = K s and b = Q s
         coli_v4f a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
         for (int kb = 0; kb < KD; kb += 16) {
-            const float4 k4 = *(const float4 *)&sK[16 * wave + li][kb + 4 * lg];
-            const float4 x4 = *(const float4 *)&sQ[16 * wave + li][kb + 4 * lg];
-            const float4 s4 = *(const float4 *)&sS[li][kb + 4 * lg];
-            a = mfma(k4.x, s4.x, a);
-            b = mfma(x4.x, s4.x, b);
-            a = mfma(k4.y, s4.y, a);
-            b = mfma(x4.y, s4.y, b);
-            a = mfma(k4.z, s4.z, a);
-            b = mfma(x4.z, s4.z, b);
-            a = mfma(k4.w, s4.w, a);
-            b = mfma(x4.w, s4.w, b);
+            const coli_v4f k4 = *(const coli_v4f *)&sK[r16][kb + 4 * lg];
+            const coli_v4f x4 = *(const coli_v4f *)&sQ[r16][kb + 4 * lg];
+            const coli_v4f s4 = *(const coli_v4f *)&sS[li][kb + 4 * lg];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                a = mfma(k4[s], s4[s], a);
+                b = mfma(x4[s], s4[s], b);
+            }
+            if (kb == 0) fetch_kq(c + 1, rk, pk);   // the next chunk's (zeros past the last)
+            else if (kb == 16) fetch_kq(c + 1, rq, pq);
+            else if (kb == 32) fetch_rest(c + 1);
+            // per k block: its 3 LDS reads, then 2 MFMAs per global load of the next chunk
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
         }
         // r = beta (v - e^G a)
         *(float4 *)&sR[li][row0] = make_float4(be[0] * (v[0] - eg.x * a[0]), be[1] * (v[1] - eg.y * a[1]),
                                                be[2] * (v[2] - eg.z * a[2]), be[3] * (v[3] - eg.w * a[3]));
         __syncthreads();
         // delta = T r
-        coli_v4f d = {0.f, 0.f, 0.f, 0.f};
-        for (int kb = 0; kb <= 16 * wave; kb += 16) {
-            const float4 t4 = *(const float4 *)&sT[16 * wave + li][kb + 4 * lg];
-            const float4 r4 = *(const float4 *)&sR[li][kb + 4 * lg];
-            d = mfma(t4.x, r4.x, d);
-            d = mfma(t4.y, r4.y, d);
-            d = mfma(t4.z, r4.z, d);
-            d = mfma(t4.w, r4.w, d);
+        coli_v4f op[NTB], rv[NTB];
+#pragma unroll
+        for (int j = 0; j < NTB; j++) {
+            op[j] = *(const coli_v4f *)&sT[r16][16 * j + 4 * lg];
+            rv[j] = *(const coli_v4f *)&sR[li][16 * j + 4 * lg];
         }
+        coli_v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NTB; j++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) d = mfma(op[j][s], rv[j][s], d);
         *(float4 *)&sD[li][row0] = make_float4(d[0], d[1], d[2], d[3]);
         *(float4 *)&sWD[li][row0] = make_float4(wt.x * d[0], wt.y * d[1], wt.z * d[2], wt.w * d[3]);
         __syncthreads();
         // y = e^G b + M delta
-        coli_v4f y = {eg.x * b[0], eg.y * b[1], eg.z * b[2], eg.w * b[3]};
-        for (int kb = 0; kb <= 16 * wave; kb += 16) {
-            const float4 m4 = *(const float4 *)&sM[16 * wave + li][kb + 4 * lg];
-            const float4 d4 = *(const float4 *)&sD[li][kb + 4 * lg];
-            y = mfma(m4.x, d4.x, y);
-            y = mfma(m4.y, d4.y, y);
-            y = mfma(m4.z, d4.z, y);
-            y = mfma(m4.w, d4.w, y);
+#pragma unroll
+        for (int j = 0; j < NTB; j++) {
+            op[j] = *(const coli_v4f *)&sM[r16][16 * j + 4 * lg];
+            rv[j] = *(const coli_v4f *)&sD[li][16 * j + 4 * lg];
         }
+        coli_v4f y = {eg.x * b[0], eg.y * b[1], eg.z * b[2], eg.w * b[3]};
+#pragma unroll
+        for (int j = 0; j < NTB; j++)
+#pragma unroll
+            for (int s = 0; s < 4; s++) y = mfma(op[j][s], rv[j][s], y);
 #pragma unroll
         for (int r = 0; r < 4; r++)
             if (t0 + row0 + r < g.n) g.y[((size_t)(t0 + row0 + r) * g.VH + h) * g.VD + c0 + li] = y[r];
-        // s = e^G_end s + K^T (w delta), key tile m: A[e][t] = K[t][16 m + e]
-        for (int m = wave; m < KD / 16; m += kWaves) {
-            const float4 s4 = *(const float4 *)&sS[li][16 * m + 4 * lg];
-            coli_v4f acc = {eend * s4.x, eend * s4.y, eend * s4.z, eend * s4.w};
-#pragma unroll 4
-            for (int kb = 0; kb < kGc; kb += 16) {
-                const float4 w4 = *(const float4 *)&sWD[li][kb + 4 * lg];
-                acc = mfma(sK[kb + 4 * lg][16 * m + li], w4.x, acc);
-                acc = mfma(sK[kb + 4 * lg + 1][16 * m + li], w4.y, acc);
-                acc = mfma(sK[kb + 4 * lg + 2][16 * m + li], w4.z, acc);
-                acc = mfma(sK[kb + 4 * lg + 3][16 * m + li], w4.w, acc);
-            }
-            *(float4 *)&sS[li][16 * m + 4 * lg] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        // s = e^G_end s + K^T (w delta), key tiles m = wave + kWaves j: A[e][t] = K[t][16 m + e]
+        coli_v4f acc[kTW];
+#pragma unroll
+        for (int j = 0; j < kTW; j++) {
+            const coli_v4f s4 = *(const coli_v4f *)&sS[li][16 * (wave + kWaves * j) + 4 * lg];
+            acc[j] = eend * s4;
         }
+#pragma unroll
+        for (int tb = 0; tb < NTB; tb++) {
+            const coli_v4f w4 = *(const coli_v4f *)&sWD[li][16 * tb + 4 * lg];
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int j = 0; j < kTW; j++)
+                    acc[j] = mfma(sK[16 * tb + 4 * lg + s][16 * (wave + kWaves * j) + li], w4[s], acc[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kTW; j++) *(coli_v4f *)&sS[li][16 * (wave + kWaves * j) + 4 * lg] = acc[j];
         __syncthreads();   // the chunk's operands are replaced by the next chunk's
     }
-    for (int i = tid; i < KD * kGcCols; i += kThreads) {
-        const int e = i % KD, cc = i / KD;
-        g.S[((size_t)h * g.VD + c0 + cc) * KD + e] = sS[cc][e];
+#pragma unroll
+    for (int i = 0; i < kSV; i++) {
+        const int f = 4 * (tid + i * kThreads);
+        Sg[tid + i * kThreads] = *(const coli_v4f *)&sS[f / KD][f % KD];
     }
 }
 
@@ -2844,7 +2887,7 @@ static bool gdn_chunks(int gi, const float *dx, const float *dp, int S, const Co
         a.VD = d.VD;
         a.K = d.K;
         a.CD = d.CD;
-        if (g_gdn_chunked && d.KD <= kGcMaxKD && d.KD % 16 == 0 && d.VD % kGcCols == 0) {
+        if (g_gdn_chunked && (d.KD == 64 || d.KD == 128) && d.VD % kGcCols == 0) {
             const int nchunk = (n + kGc - 1) / kGc;
             GdnChunkArgs c;
             c.qkv = qkv;
@@ -2873,7 +2916,10 @@ static bool gdn_chunks(int gi, const float *dx, const float *dp, int S, const Co
                                dim3(kThreads), 0, st, c);
             hipLaunchKernelGGL(gdn_chunk_norm, dim3((n * 2 * d.KH + kWaves - 1) / kWaves), dim3(kThreads), 0, st, c);
             hipLaunchKernelGGL(gdn_chunk_mats, dim3(d.VH, nchunk), dim3(kThreads), 0, st, c);
-            hipLaunchKernelGGL(gdn_chunk_scan, dim3(d.VH * (d.VD / kGcCols)), dim3(kThreads), 0, st, c);
+            if (d.KD == 128)
+                hipLaunchKernelGGL(gdn_chunk_scan<128>, dim3(d.VH * (d.VD / kGcCols)), dim3(kThreads), 0, st, c);
+            else
+                hipLaunchKernelGGL(gdn_chunk_scan<64>, dim3(d.VH * (d.VD / kGcCols)), dim3(kThreads), 0, st, c);
         } else {
             const dim3 grid(d.VH * (d.VD / kSeqCols));
             switch (d.KD / 64) {
