@@ -107,8 +107,10 @@ __device__ __forceinline__ void digit8(const float (&v)[8], bool valid, int col,
 // rows (rfmt 1) convert each weight and multiply acc by the row scale after the sum
 // (c/qwen.c:230-238).  One output per thread, 16 tokens x 16 experts per block of 256
 // threads; x and w tiles of kLC columns staged in LDS (double buffered), read as float4
-// (4 k per read, each lane's k order unchanged).
-constexpr int kLT = 16, kLE = 16, kLC = 64;
+// (4 k per read, each lane's k order unchanged).  A tile's global loads go out when the
+// tile before it starts, so they have its kLC steps of adds to arrive in (64-column tiles
+// waited on their loads at every tile: 34 against 29.5 us at configs[4]).
+constexpr int kLT = 16, kLE = 16, kLC = 256, kLS = kLC / 4 / 16;   // float4 per staged row and thread
 __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, int S, int D,
                                                  const uint8_t *__restrict__ rw, const float *__restrict__ rs,
                                                  int rfmt, int rrb, int E, float *__restrict__ lg) {
@@ -116,24 +118,31 @@ __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, i
     __shared__ __attribute__((aligned(16))) float s_w[2][kLE][kLC + 4];
     const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
     const int t0 = blockIdx.x * kLT, e0 = blockIdx.y * kLE;
-    // staging: thread tid stages float4 (tid & 15) of row tid >> 4 for x and for w
+    // staging: thread tid stages float4 (tid & 15) + 16 j of row tid >> 4 for x and for w
     const int sr = tid >> 4, sc = 4 * (tid & 15);
-    float4 rx, rv;
+    float4 rx[kLS], rv[kLS];
     auto load = [&](int kc) {
-        const int t = t0 + sr, e = e0 + sr, k = kc + sc;
-        rx = (t < S && k < D) ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e >= E || k >= D) {
-            rv = make_float4(0.f, 0.f, 0.f, 0.f);
-        } else if (rfmt == 0) {
-            rv = *(const float4 *)(rw + (size_t)e * rrb + 4 * (size_t)k);
-        } else {
-            const char4 c = *(const char4 *)(rw + (size_t)e * rrb + k);
-            rv = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
+        const int t = t0 + sr, e = e0 + sr;
+#pragma unroll
+        for (int j = 0; j < kLS; j++) {
+            const int k = kc + sc + 64 * j;
+            rx[j] = (t < S && k < D) ? *(const float4 *)(xs + (size_t)t * D + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e >= E || k >= D) {
+                rv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            } else if (rfmt == 0) {
+                rv[j] = *(const float4 *)(rw + (size_t)e * rrb + 4 * (size_t)k);
+            } else {
+                const char4 c = *(const char4 *)(rw + (size_t)e * rrb + k);
+                rv[j] = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
+            }
         }
     };
     auto store = [&](int buf) {
-        *(float4 *)&s_x[buf][sr][sc] = rx;
-        *(float4 *)&s_w[buf][sr][sc] = rv;
+#pragma unroll
+        for (int j = 0; j < kLS; j++) {
+            *(float4 *)&s_x[buf][sr][sc + 64 * j] = rx[j];
+            *(float4 *)&s_w[buf][sr][sc + 64 * j] = rv[j];
+        }
     };
     float acc = 0.f;
     load(0);
@@ -143,7 +152,7 @@ __global__ __launch_bounds__(256) void pf_logits(const float *__restrict__ xs, i
         const bool more = kc + kLC < D;
         if (more) load(kc + kLC);
         const int n = D - kc < kLC ? D - kc : kLC;   // D % 4 == 0
-#pragma unroll 4
+#pragma unroll 8
         for (int k = 0; k < n; k += 4) {
             const float4 a = *(const float4 *)&s_x[buf][ty][k];
             const float4 w = *(const float4 *)&s_w[buf][tx][k];
