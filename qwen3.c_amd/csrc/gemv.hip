@@ -770,19 +770,18 @@ bool rmsnorm_zc(const float *d_x, const float *d_w, float *d_y, int D, float eps
 }
 
 // ----------------------------------------------------------------------------------
-// host-buffer entry points: stage through pinned buffers, one sync per call
+// host-buffer entry points: x up through the pinned upload staging, y back through pinned
+// buffers, one sync per call
 struct Stage {
-    void *hx = nullptr, *hy = nullptr, *dx = nullptr, *dy = nullptr, *dk = nullptr;
-    size_t hxc = 0, hyc = 0, dxc = 0, dyc = 0, dkc = 0;
+    void *hy = nullptr, *dx = nullptr, *dy = nullptr, *dk = nullptr;
+    size_t hyc = 0, dxc = 0, dyc = 0, dkc = 0;
 };
 static Stage g_st;
 
 static bool stage_x(const float *x, size_t xb) {
-    if (!host_scratch(&g_st.hx, &g_st.hxc, xb) || !scratch(&g_st.dx, &g_st.dxc, xb)) return false;
-    memcpy(g_st.hx, x, xb);
-    const hipError_t e = hipMemcpyAsync(g_st.dx, g_st.hx, xb, hipMemcpyHostToDevice, stream());
-    if (e != hipSuccess) return fail("x upload", e);
-    return true;
+    if (!scratch(&g_st.dx, &g_st.dxc, xb)) return false;
+    const Upload u = {g_st.dx, x, xb};
+    return upload(&u, 1, stream(), "x upload");
 }
 
 static bool fetch(void *dst, const void *dsrc, size_t bytes, const char *who) {
@@ -899,7 +898,6 @@ void gemv_shutdown() {
     scratch_free(&g_logits, &g_logits_cap);
     scratch_free(&g_slots, &g_slots_cap);
     scratch_free(&g_keys, &g_keys_cap);
-    host_scratch_free(&g_st.hx, &g_st.hxc);
     host_scratch_free(&g_st.hy, &g_st.hyc);
     scratch_free(&g_st.dx, &g_st.dxc);
     scratch_free(&g_st.dy, &g_st.dyc);

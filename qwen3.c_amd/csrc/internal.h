@@ -57,6 +57,14 @@ bool sync_stream(const char *who);
 // device -> pageable host read-back through pinned staging, copied out piece by piece as
 // the pieces arrive (runtime.hip); read_back synchronises with every piece on `st`.
 bool read_back(void *dst, const void *dsrc, size_t n, hipStream_t st, const char *who);
+// Host buffers to device memory on `st` through pinned staging in pieces (runtime.hip); the
+// host buffers may be reused on return.
+struct Upload {
+    void *d;
+    const void *h;
+    size_t n;
+};
+bool upload(const Upload *u, int nu, hipStream_t st, const char *who);
 // The pieces of a read-back already issued into pinned memory: record one event per piece
 // after issuing it, then copy_out waits for each in turn and copies it out.
 struct PieceEvents {

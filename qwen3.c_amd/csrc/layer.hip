@@ -2693,7 +2693,8 @@ static int gqa_seq(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTen
             tab[((size_t)s * hr + j) * 2] = (float)cos((double)ang);
             tab[((size_t)s * hr + j) * 2 + 1] = (float)sin((double)ang);
         }
-    const bool up = h2d(dx, x, (size_t)S * D * 4, "gqa seq x") && h2d(rope, tab, (size_t)S * hr * 8, "gqa seq rope");
+    const Upload u[2] = {{dx, x, (size_t)S * D * 4}, {rope, tab, (size_t)S * hr * 8}};
+    const bool up = upload(u, 2, stream(), "gqa seq upload");
     free(tab);
     if (!up) return 0;
     const ColiVkTensor *tp[3] = {tq, tk, tv};
@@ -2950,9 +2951,8 @@ static int gdn_rows(int layer, const float *x, int S, int D, ColiVkTensor *gqkv_
     const int prs = 2 * d.VH + d.VD;
     float *dx = wbuf(W_IO_X, (size_t)S * D), *dp = wbuf(W_IO_P, (size_t)S * prs),
           *dout = wbuf(W_IO_O, (size_t)S * Dout);
-    if (!dx || !dp || !dout || !h2d(dx, x, (size_t)S * D * 4, "gdn rows") ||
-        !h2d(dp, params, (size_t)S * prs * 4, "gdn params"))
-        return 0;
+    const Upload u[2] = {{dx, x, (size_t)S * D * 4}, {dp, params, (size_t)S * prs * 4}};
+    if (!dx || !dp || !dout || !upload(u, 2, stream(), "gdn rows upload")) return 0;
     bool ran;
     if (!gdn_chunks(layer, dx, dp, S, gqkv_t, gz_t, out_t, dout, d, stream(), &ran)) return 0;
     for (int s = 0; !ran && s < S; s++)

@@ -1178,8 +1178,8 @@ COLI_API int coli_vk_eg_xs_bind(const float *xs, int S, int D) {
     if (!ok() || !xs || S < 1 || D < 1 || g_grp.inflight) return 0;
     const size_t xb = (size_t)S * D * 4;
     if (!scratch(&g_grp.d_xs, &g_grp.d_xs_cap, xb)) return 0;
-    const hipError_t e = hipMemcpy(g_grp.d_xs, xs, xb, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return fail("xs bind", e) ? 1 : 0;
+    const Upload u = {g_grp.d_xs, xs, xb};
+    if (!upload(&u, 1, stream(), "xs bind")) return 0;
     g_grp.xs_S = S;
     g_grp.xs_D = D;
     static uint64_t binds = 0;

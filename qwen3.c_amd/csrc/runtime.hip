@@ -144,9 +144,65 @@ size_t g_rb_cap = 0;
 PieceEvents g_rb_pe;
 }  // namespace
 
+namespace {
+void *g_up = nullptr;   // write-combined pinned staging of upload
+size_t g_up_cap = 0;
+hipEvent_t g_up_done = nullptr;   // after the last transfer out of g_up
+bool g_up_busy = false;
+}  // namespace
+
 void read_back_shutdown() {
     host_scratch_free(&g_rb, &g_rb_cap);
     piece_events_free(g_rb_pe);
+    if (g_up_busy) (void)hipEventSynchronize(g_up_done);
+    g_up_busy = false;
+    host_scratch_free(&g_up, &g_up_cap);
+    if (g_up_done) (void)hipEventDestroy(g_up_done);
+    g_up_done = nullptr;
+}
+
+// ---------------------------------------------------------------- uploads
+// Caller (pageable) buffers to the device through pinned staging, laid out one after the
+// other: each 1 MiB piece is copied into the staging on the host and its transfer issued at
+// once, so the transfer of one piece overlaps the host copy of the next (a pageable
+// hipMemcpyAsync does them in turn).  The staging is write-combined: the host only writes
+// it and the device only reads it.  The next upload reuses it once the last transfer out of
+// it is done (an event); the caller's buffers are free again on return.
+bool upload(const Upload *u, int nu, hipStream_t st, const char *who) {
+    constexpr size_t kPiece = (size_t)1 << 20;
+    size_t total = 0;
+    for (int i = 0; i < nu; i++) total += (u[i].n + 4095) & ~(size_t)4095;
+    if (!total) return true;
+    if (g_up_busy) {
+        const hipError_t e = hipEventSynchronize(g_up_done);
+        if (e != hipSuccess) return fail(who, e);
+        g_up_busy = false;
+    }
+    if (total > g_up_cap || !g_up) {
+        host_scratch_free(&g_up, &g_up_cap);
+        const hipError_t e = hipHostMalloc(&g_up, total, hipHostMallocWriteCombined);
+        if (e != hipSuccess) {
+            g_up = nullptr;
+            return fail("hipHostMalloc (upload staging)", e);
+        }
+        g_up_cap = total;
+    }
+    size_t off = 0;
+    for (int i = 0; i < nu; i++) {
+        for (size_t o = 0; o < u[i].n; o += kPiece) {
+            const size_t len = u[i].n - o < kPiece ? u[i].n - o : kPiece;
+            uint8_t *s = (uint8_t *)g_up + off + o;
+            memcpy(s, (const uint8_t *)u[i].h + o, len);
+            const hipError_t e = hipMemcpyAsync((uint8_t *)u[i].d + o, s, len, hipMemcpyHostToDevice, st);
+            if (e != hipSuccess) return fail(who, e);
+        }
+        off += (u[i].n + 4095) & ~(size_t)4095;
+    }
+    hipError_t e = g_up_done ? hipSuccess : hipEventCreateWithFlags(&g_up_done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(g_up_done, st);
+    if (e != hipSuccess) return fail(who, e);
+    g_up_busy = true;
+    return true;
 }
 
 // Up to PieceEvents::kMax pieces of at least 1 MiB each.
