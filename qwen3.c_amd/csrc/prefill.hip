@@ -226,7 +226,15 @@ __global__ __launch_bounds__(1024) void pf_group(const int *tidx, int npairs, in
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int e = tid; e < E; e += 1024) s_cnt[e] = 0;
     __syncthreads();
-    for (int i = tid; i < npairs; i += 1024) rank[i] = atomicAdd(&s_cnt[tidx[i]], 1);
+    constexpr int kB = 4;   // pairs per thread and batch, their loads in flight together
+    for (int i0 = tid; i0 < npairs; i0 += 1024 * kB) {
+        int e[kB];
+#pragma unroll
+        for (int k = 0; k < kB; k++) e[k] = i0 + 1024 * k < npairs ? tidx[i0 + 1024 * k] : 0;
+#pragma unroll
+        for (int k = 0; k < kB; k++)
+            if (i0 + 1024 * k < npairs) rank[i0 + 1024 * k] = atomicAdd(&s_cnt[e[k]], 1);
+    }
     __syncthreads();
     // exclusive scan of the counts: inclusive per wave, then the wave totals
     const int c = tid < E ? s_cnt[tid] : 0;
@@ -247,10 +255,22 @@ __global__ __launch_bounds__(1024) void pf_group(const int *tidx, int npairs, in
     }
     if (tid == 1023) off[E] = base + inc;   // the last thread's inclusive sum is the total
     __syncthreads();
-    for (int i = tid; i < npairs; i += 1024) {
-        const int p = s_cnt[tidx[i]] + rank[i];
-        plist[p] = i;
-        ppos[i] = p;
+    for (int i0 = tid; i0 < npairs; i0 += 1024 * kB) {
+        int e[kB], rk[kB];
+#pragma unroll
+        for (int k = 0; k < kB; k++) {
+            const bool on = i0 + 1024 * k < npairs;
+            e[k] = on ? tidx[i0 + 1024 * k] : 0;
+            rk[k] = on ? rank[i0 + 1024 * k] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kB; k++) {
+            const int i = i0 + 1024 * k;
+            if (i >= npairs) continue;
+            const int p = s_cnt[e[k]] + rk[k];
+            plist[p] = i;
+            ppos[i] = p;
+        }
     }
 }
 
@@ -815,48 +835,62 @@ __global__ __launch_bounds__(kPT, 2) void pf_down(PfArgs a) {
 
 // ---------------------------------------------------------------- combine
 // out[t] = sum over t's K experts in ascending expert id of w * y[pos] + shgt * y_sh[t]
-// (c/qwen.c:1144, 1159-1161); float4 columns, all K + 1 rows in flight.
+// (c/qwen.c:1144, 1159-1161).  The token's ids, positions and weights come in one round of
+// loads and are put in expert order in registers (an odd-even transposition network: ids
+// are distinct); then every float4 of the thread's columns and all K + 1 rows are loaded
+// before the sums, which keep the order above.
+constexpr int kCbCols = 2;   // float4 columns per thread and pass of 4 * 256 * kCbCols columns
 __global__ __launch_bounds__(256) void pf_combine(const float *__restrict__ y, const int *tidx, const float *tval,
                                                   const float *tshg, const int *ppos, int S, int K, int D,
                                                   float *__restrict__ out) {
     const int t = blockIdx.x;
-    int ord[kTopK];
-    int nk = 0;
-    for (int k = 0; k < K; k++) {   // slots sorted by expert id (insertion; K <= 8 here)
-        int j = nk++;
-        while (j > 0 && tidx[t * K + ord[j - 1]] > tidx[t * K + k]) {
-            ord[j] = ord[j - 1];
-            j--;
-        }
-        ord[j] = k;
-    }
-    const float *row[kTopK];
+    int id[kTopK], pp[kTopK];
     float w[kTopK];
 #pragma unroll
-    for (int i = 0; i < kTopK; i++) {
-        const int k = i < K ? ord[i] : 0;
-        row[i] = y + (size_t)ppos[t * K + k] * D;
-        w[i] = tval[t * K + k];
+    for (int k = 0; k < kTopK; k++) {
+        id[k] = k < K ? tidx[t * K + k] : 0x7FFFFFFF;   // absent slots sort last
+        pp[k] = k < K ? ppos[t * K + k] : 0;
+        w[k] = k < K ? tval[t * K + k] : 0.f;
     }
     const float shg = tshg[t];
-    const float *ysh = y + (size_t)(S * K + t) * D;
-    for (int c = 4 * threadIdx.x; c < D; c += 4 * 256) {
-        float4 v[kTopK];
 #pragma unroll
-        for (int i = 0; i < kTopK; i++)
-            if (i < K) v[i] = *(const float4 *)(row[i] + c);
-        const float4 s = *(const float4 *)(ysh + c);
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < kTopK; i++)
 #pragma unroll
-        for (int i = 0; i < kTopK; i++)
-            if (i < K) {
-                acc.x = acc.x + w[i] * v[i].x;
-                acc.y = acc.y + w[i] * v[i].y;
-                acc.z = acc.z + w[i] * v[i].z;
-                acc.w = acc.w + w[i] * v[i].w;
+        for (int k = i & 1; k + 1 < kTopK; k += 2)
+            if (id[k] > id[k + 1]) {
+                const int a = id[k], b = pp[k];
+                const float c = w[k];
+                id[k] = id[k + 1], pp[k] = pp[k + 1], w[k] = w[k + 1];
+                id[k + 1] = a, pp[k + 1] = b, w[k + 1] = c;
             }
-        *(float4 *)(out + (size_t)t * D + c) =
-            make_float4(acc.x + shg * s.x, acc.y + shg * s.y, acc.z + shg * s.z, acc.w + shg * s.w);
+    const float *ysh = y + (size_t)(S * K + t) * D;
+    for (int c0 = 0; c0 < D; c0 += 4 * 256 * kCbCols) {
+        float4 v[kCbCols][kTopK], sv[kCbCols];
+#pragma unroll
+        for (int q = 0; q < kCbCols; q++) {
+            const int c = c0 + 4 * threadIdx.x + 4 * 256 * q;
+            const bool on = c < D;
+#pragma unroll
+            for (int i = 0; i < kTopK; i++)
+                v[q][i] = on && i < K ? *(const float4 *)(y + (size_t)pp[i] * D + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            sv[q] = on ? *(const float4 *)(ysh + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int q = 0; q < kCbCols; q++) {
+            const int c = c0 + 4 * threadIdx.x + 4 * 256 * q;
+            if (c >= D) continue;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int i = 0; i < kTopK; i++)
+                if (i < K) {
+                    acc.x = acc.x + w[i] * v[q][i].x;
+                    acc.y = acc.y + w[i] * v[q][i].y;
+                    acc.z = acc.z + w[i] * v[q][i].z;
+                    acc.w = acc.w + w[i] * v[q][i].w;
+                }
+            *(float4 *)(out + (size_t)t * D + c) = make_float4(acc.x + shg * sv[q].x, acc.y + shg * sv[q].y,
+                                                               acc.z + shg * sv[q].z, acc.w + shg * sv[q].w);
+        }
     }
 }
 
