@@ -8,6 +8,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+#include <condition_variable>
+#include <mutex>
+#include <thread>
+
 namespace coli {
 
 struct ArenaBlock {
@@ -132,12 +137,127 @@ bool sync_stream(const char *who) {
     return true;
 }
 
+// ---------------------------------------------------------------- pinned <-> device copies
+// Transfers between device memory and pinned host memory (hipHostMalloc: mapped into the
+// device's address space) run as this kernel, one launch per piece: the launch returns at
+// once, where a hipMemcpyAsync between them held the host thread for about as long as the
+// transfer (the runtime's own blit kernel), so the pieces went out one at a time.  16-byte
+// words when both ends are 16-byte aligned, else 4-byte words (every transfer here is of
+// floats or ints).
+__global__ void pin_copy16(uint4 *__restrict__ d, const uint4 *__restrict__ s, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+__global__ void pin_copy4(uint32_t *__restrict__ d, const uint32_t *__restrict__ s, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+
+bool pin_copy(void *dst, const void *src, size_t n, hipStream_t st, const char *who) {
+    if (!n) return true;
+    if (n % 4) return fail(who, hipErrorInvalidValue);
+    const bool w16 = !(((uintptr_t)dst | (uintptr_t)src | n) & 15);
+    const size_t words = w16 ? n / 16 : n / 4;
+    const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+    if (w16)
+        hipLaunchKernelGGL(pin_copy16, dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, words);
+    else
+        hipLaunchKernelGGL(pin_copy4, dim3(blocks), dim3(256), 0, st, (uint32_t *)dst, (const uint32_t *)src, words);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(who, e);
+    return true;
+}
+
+// ---------------------------------------------------------------- host copy helper
+// One helper thread shares the host side of read-backs and uploads: a cold copy by one
+// thread runs at ~20-26 GB/s on these hosts, by two at ~35-45 GB/s, which keeps up with
+// the ~45 GB/s transfers.  The calling thread hands it the odd pieces of a job and does
+// the even ones, then waits for it.  The helper starts on the first job and is joined at
+// shutdown.
+namespace {
+struct CopyHelper {
+    std::thread th;
+    std::mutex m;
+    std::condition_variable go, done;
+    void (*fn)(void *, int) = nullptr;   // the job: fn(ctx, piece) for the helper's pieces
+    void *ctx = nullptr;
+    int count = 0;
+    uint64_t posted = 0, finished = 0;
+    bool ok = true, stop = false;
+};
+CopyHelper *g_ch = nullptr;
+
+void helper_loop(CopyHelper *h) {
+    uint64_t seen = 0;
+    for (;;) {
+        void (*fn)(void *, int);
+        void *ctx;
+        int count;
+        {
+            std::unique_lock<std::mutex> lk(h->m);
+            h->go.wait(lk, [&] { return h->stop || h->posted != seen; });
+            if (h->stop) return;
+            seen = h->posted;
+            fn = h->fn, ctx = h->ctx, count = h->count;
+        }
+        for (int i = 1; i < count; i += 2) fn(ctx, i);
+        {
+            std::lock_guard<std::mutex> lk(h->m);
+            h->finished = seen;
+        }
+        h->done.notify_one();
+    }
+}
+
+// Runs fn(ctx, i) for i in [0, count): the helper the odd i, this thread the even ones.
+// Without a helper (thread start failed) this thread runs all of them.
+void split_pieces(void (*fn)(void *, int), void *ctx, int count) {
+    if (count > 1 && !g_ch) {
+        CopyHelper *h = new (std::nothrow) CopyHelper;
+        if (h) {
+            try {
+                h->th = std::thread(helper_loop, h);
+                g_ch = h;
+            } catch (...) {
+                delete h;
+            }
+        }
+    }
+    if (count < 2 || !g_ch) {
+        for (int i = 0; i < count; i++) fn(ctx, i);
+        return;
+    }
+    CopyHelper *h = g_ch;
+    uint64_t job;
+    {
+        std::lock_guard<std::mutex> lk(h->m);
+        h->fn = fn, h->ctx = ctx, h->count = count;
+        job = ++h->posted;
+    }
+    h->go.notify_one();
+    for (int i = 0; i < count; i += 2) fn(ctx, i);
+    std::unique_lock<std::mutex> lk(h->m);
+    h->done.wait(lk, [&] { return h->finished == job; });
+}
+
+void copy_helper_stop() {
+    if (!g_ch) return;
+    {
+        std::lock_guard<std::mutex> lk(g_ch->m);
+        g_ch->stop = true;
+    }
+    g_ch->go.notify_one();
+    g_ch->th.join();
+    delete g_ch;
+    g_ch = nullptr;
+}
+}  // namespace
+
 // ---------------------------------------------------------------- read-backs
 // A read-back into a caller's (pageable) buffer goes through pinned staging: the device
-// copies in up to 8 pieces, each with its event, and each piece is copied out on the host
-// as soon as it has arrived, so the host copy of one piece overlaps the transfer of the
-// next.  (Several host threads do not copy faster here: one thread already reaches the
-// host memory bandwidth the process gets, ~30 GB/s for 8 MiB blocks on the MI355X boxes.)
+// copies in up to 8 pieces (pin_copy), each with its event, and each piece is copied out on
+// the host as soon as it has arrived (this thread and the copy helper take turns), so the
+// host copies overlap the transfers of the later pieces.
 namespace {
 void *g_rb = nullptr;   // pinned staging of read_back
 size_t g_rb_cap = 0;
@@ -152,6 +272,7 @@ bool g_up_busy = false;
 }  // namespace
 
 void read_back_shutdown() {
+    copy_helper_stop();
     host_scratch_free(&g_rb, &g_rb_cap);
     piece_events_free(g_rb_pe);
     if (g_up_busy) (void)hipEventSynchronize(g_up_done);
@@ -163,11 +284,11 @@ void read_back_shutdown() {
 
 // ---------------------------------------------------------------- uploads
 // Caller (pageable) buffers to the device through pinned staging, laid out one after the
-// other: each 1 MiB piece is copied into the staging on the host and its transfer issued at
-// once, so the transfer of one piece overlaps the host copy of the next (a pageable
-// hipMemcpyAsync does them in turn).  The staging is write-combined: the host only writes
-// it and the device only reads it.  The next upload reuses it once the last transfer out of
-// it is done (an event); the caller's buffers are free again on return.
+// other: each 1 MiB piece is copied into the staging on the host (this thread and the copy
+// helper take turns) and its transfer (pin_copy) issued at once, so transfers overlap the
+// host copies (a pageable hipMemcpyAsync does them in turn).  The staging is write-combined:
+// the host only writes it and the device only reads it.  The next upload reuses it once the
+// last transfer out of it is done (an event); the caller's buffers are free again on return.
 bool upload(const Upload *u, int nu, hipStream_t st, const char *who) {
     constexpr size_t kPiece = (size_t)1 << 20;
     size_t total = 0;
@@ -187,16 +308,49 @@ bool upload(const Upload *u, int nu, hipStream_t st, const char *who) {
         }
         g_up_cap = total;
     }
-    size_t off = 0;
+    // the pieces of all transfers in one list, copied and issued by this thread and the helper
+    constexpr int kMaxPieces = 256;
+    struct Piece {
+        void *d;
+        const void *h;
+        uint8_t *s;
+        size_t len;
+    };
+    Piece pcs[kMaxPieces];
+    int np = 0;
+    size_t off = 0, piece = kPiece;
     for (int i = 0; i < nu; i++) {
-        for (size_t o = 0; o < u[i].n; o += kPiece) {
-            const size_t len = u[i].n - o < kPiece ? u[i].n - o : kPiece;
-            uint8_t *s = (uint8_t *)g_up + off + o;
-            memcpy(s, (const uint8_t *)u[i].h + o, len);
-            const hipError_t e = hipMemcpyAsync((uint8_t *)u[i].d + o, s, len, hipMemcpyHostToDevice, st);
-            if (e != hipSuccess) return fail(who, e);
-        }
+        const size_t np_i = (u[i].n + kPiece - 1) / kPiece;
+        if ((size_t)np + np_i > (size_t)kMaxPieces) piece = 0;   // too many: one plain pass below
+        for (size_t o = 0; piece && o < u[i].n; o += kPiece)
+            pcs[np++] = {(uint8_t *)u[i].d + o, (const uint8_t *)u[i].h + o, (uint8_t *)g_up + off + o,
+                         u[i].n - o < kPiece ? u[i].n - o : kPiece};
         off += (u[i].n + 4095) & ~(size_t)4095;
+    }
+    if (!piece) {   // more than kMaxPieces MiB in one upload: this thread alone
+        off = 0;
+        for (int i = 0; i < nu; i++) {
+            memcpy((uint8_t *)g_up + off, u[i].h, u[i].n);
+            __atomic_thread_fence(__ATOMIC_SEQ_CST);
+            if (!pin_copy(u[i].d, (uint8_t *)g_up + off, u[i].n, st, who)) return false;
+            off += (u[i].n + 4095) & ~(size_t)4095;
+        }
+    } else {
+        struct Ctx {
+            const Piece *p;
+            hipStream_t st;
+            std::atomic<int> bad;
+        } c{pcs, st, {0}};
+        split_pieces(
+            [](void *v, int i) {
+                Ctx &c = *(Ctx *)v;
+                const Piece &p = c.p[i];
+                memcpy(p.s, p.h, p.len);
+                __atomic_thread_fence(__ATOMIC_SEQ_CST);   // the write-combined stores out before the launch
+                if (!pin_copy(p.d, p.s, p.len, c.st, "upload")) c.bad = 1;
+            },
+            &c, np);
+        if (c.bad) return fail(who, hipErrorUnknown);
     }
     hipError_t e = g_up_done ? hipSuccess : hipEventCreateWithFlags(&g_up_done, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(g_up_done, st);
@@ -215,8 +369,8 @@ bool issue_pieces(PieceEvents &pe, void *hdst, const void *dsrc, size_t n, hipSt
     pe.count = n ? (int)((n + piece - 1) / piece) : 0;
     for (int i = 0; i < pe.count; i++) {
         const size_t o = (size_t)i * piece, len = n - o < piece ? n - o : piece;
-        hipError_t e = hipMemcpyAsync((uint8_t *)hdst + o, (const uint8_t *)dsrc + o, len, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess && !pe.ev[i]) e = hipEventCreateWithFlags(&pe.ev[i], hipEventDisableTiming);
+        if (!pin_copy((uint8_t *)hdst + o, (const uint8_t *)dsrc + o, len, st, "read-back issue")) return false;
+        hipError_t e = pe.ev[i] ? hipSuccess : hipEventCreateWithFlags(&pe.ev[i], hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventRecord(pe.ev[i], st);
         if (e != hipSuccess) return fail("read-back issue", e);
     }
@@ -224,12 +378,24 @@ bool issue_pieces(PieceEvents &pe, void *hdst, const void *dsrc, size_t n, hipSt
 }
 
 bool copy_out(PieceEvents &pe, void *dst, const void *hsrc, const char *who) {
-    for (int i = 0; i < pe.count; i++) {
-        const hipError_t e = hipEventSynchronize(pe.ev[i]);
-        if (e != hipSuccess) return fail(who, e);
-        const size_t o = (size_t)i * pe.piece, len = pe.n - o < pe.piece ? pe.n - o : pe.piece;
-        memcpy((uint8_t *)dst + o, (const uint8_t *)hsrc + o, len);
-    }
+    struct Ctx {
+        PieceEvents *pe;
+        uint8_t *dst;
+        const uint8_t *src;
+        std::atomic<int> bad;
+    } c{&pe, (uint8_t *)dst, (const uint8_t *)hsrc, {0}};
+    split_pieces(
+        [](void *p, int i) {
+            Ctx &c = *(Ctx *)p;
+            if (hipEventSynchronize(c.pe->ev[i]) != hipSuccess) {
+                c.bad = 1;
+                return;
+            }
+            const size_t o = (size_t)i * c.pe->piece, len = c.pe->n - o < c.pe->piece ? c.pe->n - o : c.pe->piece;
+            memcpy(c.dst + o, c.src + o, len);
+        },
+        &c, pe.count);
+    if (c.bad) return fail(who, hipErrorUnknown);
     return true;
 }
 
