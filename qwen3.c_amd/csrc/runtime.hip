@@ -188,6 +188,7 @@ struct CopyHelper {
 CopyHelper *g_ch = nullptr;
 
 void helper_loop(CopyHelper *h) {
+    (void)hipSetDevice(G.dev);   // the current device is per thread; its launches go to the library's device
     uint64_t seen = 0;
     for (;;) {
         void (*fn)(void *, int);
