@@ -36,6 +36,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <vector>
+
 namespace coli {
 
 // ---------------------------------------------------------------- block reductions
@@ -2664,6 +2666,39 @@ static int gqa_rows(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTe
 // device work done when a shape is outside these kernels (the caller then takes gqa_rows).
 enum { kSeqNo = -1 };
 static int g_gqa_seq = 1;   // 0: every S takes the token loop (coli_hip_gqa_seq)
+// The rotation rows [pos][rot / 2] of (cos, sin) per position, c/qwen.c:570-579 as the
+// decode block computes them (in double, rounded to float), kept across calls: they depend
+// only on (theta, rot, pos), so the GQA layers of a prompt and its later chunks share them.
+// Rows are added as positions are first used.  nullptr when out of host memory.
+static const float *rope_rows(float theta, int rot, int pos_end) {
+    static float c_theta = 0.f;
+    static int c_rot = 0, c_rows = 0;
+    static std::vector<float> c_inv, c_tab;
+    const int hr = rot / 2;
+    try {
+        if (c_theta != theta || c_rot != rot) {
+            c_theta = theta, c_rot = rot, c_rows = 0;
+            c_tab.clear();
+            c_inv.resize(hr);
+            for (int j = 0; j < hr; j++) c_inv[j] = (float)pow((double)theta, (double)(-2.0f * j / rot));
+        }
+        if (pos_end > c_rows) {
+            c_tab.resize((size_t)pos_end * hr * 2);
+            for (int s = c_rows; s < pos_end; s++)
+                for (int j = 0; j < hr; j++) {
+                    const float ang = (float)s * c_inv[j];
+                    c_tab[((size_t)s * hr + j) * 2] = (float)cos((double)ang);
+                    c_tab[((size_t)s * hr + j) * 2 + 1] = (float)sin((double)ang);
+                }
+            c_rows = pos_end;
+        }
+    } catch (...) {
+        c_theta = 0.f, c_rot = 0, c_rows = 0;
+        return nullptr;
+    }
+    return c_tab.data();
+}
+
 static int gqa_seq(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTensor *tk, ColiVkTensor *tv,
                    ColiVkTensor *to, float *out, int S, const GqaDims &d, int pos_base, int Dout) {
     const int H = d.H, KH = d.KH, hd = d.hd, hr = d.rot / 2;
@@ -2684,19 +2719,10 @@ static int gqa_seq(int layer, const float *x, int D, ColiVkTensor *tq, ColiVkTen
     float *rope = wbuf(W_ROPE, (size_t)S * hr * 2);
     if (!dx || !dout || !qraw || !kr || !qn || !ctx || !rope) return 0;
     float *vr = kr + (size_t)S * KH * hd;
-    float *tab = (float *)malloc((size_t)S * hr * 2 * 4);
+    const float *tab = rope_rows(d.theta, d.rot, pos_base + S);
     if (!tab) return 0;
-    for (int s = 0; s < S; s++)   // c/qwen.c:570-579 as the decode block: in double, rounded to float
-        for (int j = 0; j < hr; j++) {
-            const float inv = (float)pow((double)d.theta, (double)(-2.0f * j / d.rot));
-            const float ang = (float)(pos_base + s) * inv;
-            tab[((size_t)s * hr + j) * 2] = (float)cos((double)ang);
-            tab[((size_t)s * hr + j) * 2 + 1] = (float)sin((double)ang);
-        }
-    const Upload u[2] = {{dx, x, (size_t)S * D * 4}, {rope, tab, (size_t)S * hr * 8}};
-    const bool up = upload(u, 2, stream(), "gqa seq upload");
-    free(tab);
-    if (!up) return 0;
+    const Upload u[2] = {{dx, x, (size_t)S * D * 4}, {rope, tab + (size_t)pos_base * hr * 2, (size_t)S * hr * 8}};
+    if (!upload(u, 2, stream(), "gqa seq upload")) return 0;
     const ColiVkTensor *tp[3] = {tq, tk, tv};
     float *const yp[3] = {qraw, kr, vr};
     if (!gemm6(tp, yp, 3, dx, S, stream())) return 0;
