@@ -99,6 +99,39 @@ def issue_chunks_into(lib, tensors, xs, S, D, chs, ybuf):
     lib.expert_group_take_into(ybuf[:S * D])
 
 
+def prepare_chunks(lib, tensors, S, chs):
+    """The ctypes arguments of every call issue_chunks_into makes, built once: the engine
+    builds its handle arrays in C, so a timing of the library calls leaves this out."""
+    E = len(tensors) - 1
+    prep = []
+    for es, rows, rtok, _ in chs:
+        g, u, d, r = lib._group([tensors[e][0] for e in es], [tensors[e][1] for e in es],
+                                [tensors[e][2] for e in es], rows)
+        prep.append((g, u, d, r, len(es), np.ascontiguousarray(rtok, np.int32)))
+    shared = lib._group([tensors[E][0]], [tensors[E][1]], [tensors[E][2]], [S])
+    return prep, shared
+
+
+def issue_prepared(lib, prepared, xs, S, D, ybuf):
+    """issue_chunks_into over arguments from prepare_chunks: the same ABI calls in the same
+    order (bind, issue_id / take per chunk, the shared expert's issue / take)."""
+    import ctypes as C
+    L = lib.L
+    prep, (sg, su, sd, sr) = prepared
+    px, py = xs.ctypes.data_as(C.c_void_p), ybuf.ctypes.data_as(C.c_void_p)
+    if not L.coli_vk_eg_xs_bind(px, S, D):
+        raise RuntimeError("coli_vk_eg_xs_bind failed")
+    for g, u, d, r, n, ids in prep:
+        if not L.coli_vk_expert_group_issue_id(g, u, d, r, n, ids.ctypes.data_as(C.c_void_p)):
+            raise RuntimeError("coli_vk_expert_group_issue_id refused a chunk")
+        if not L.coli_vk_expert_group_take(py):
+            raise RuntimeError("coli_vk_expert_group_take failed")
+    if not L.coli_vk_expert_group_issue(sg, su, sd, sr, 1, px):
+        raise RuntimeError("coli_vk_expert_group_issue refused the shared expert")
+    if not L.coli_vk_expert_group_take(py):
+        raise RuntimeError("coli_vk_expert_group_take failed")
+
+
 def engine_moe_batch(lib, tensors, xs, S, D, K, tidx, tval, sh_gate):
     """out [S, D] of the routed experts and the shared expert (tensors[e] = (g, u, d) for
     e < E, tensors[E] the shared expert), through the ABI as the engine calls it."""
