@@ -65,6 +65,9 @@ struct Upload {
     size_t n;
 };
 bool upload(const Upload *u, int nu, hipStream_t st, const char *who);
+// n bytes (n % 4 == 0) between device memory and pinned host memory (host_scratch) as a
+// copy kernel on `st`: the launch returns at once (runtime.hip)
+bool pin_copy(void *dst, const void *src, size_t n, hipStream_t st, const char *who);
 // The pieces of a read-back already issued into pinned memory: record one event per piece
 // after issuing it, then copy_out waits for each in turn and copies it out.
 struct PieceEvents {

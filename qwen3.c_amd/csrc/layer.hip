@@ -3119,16 +3119,16 @@ static int *hist_dev() { return (int *)wbuf(W_HIST, hist_ints()); }
 
 COLI_API int coli_vk_stream_begin(const float *x, int D) {
     if (!ok() || !x || D < 1) return 0;
-    // the row goes through pinned staging with an async copy: the token's first launches
-    // queue behind it at once.  The staging is rewritten only with the stream idle (a live
-    // stream is drained first; a finished token was drained by its read-backs).
+    // the row goes through pinned staging and a copy kernel: the token's first launches
+    // queue behind it at once (a hipMemcpyAsync held the host ~15 us while the device sat
+    // idle).  The staging is rewritten only with the stream idle (a live stream is drained
+    // first; a finished token was drained by its read-backs).
     if (g_str.live && !sync_stream("stream begin")) return 0;
     if (!scratch((void **)&g_str.d_resid, &g_str.resid_cap, (size_t)D * 4) ||
         !host_scratch((void **)&g_str.h_x, &g_str.hx_cap, (size_t)D * 4))
         return 0;
     memcpy(g_str.h_x, x, (size_t)D * 4);
-    const hipError_t e = hipMemcpyAsync(g_str.d_resid, g_str.h_x, (size_t)D * 4, hipMemcpyHostToDevice, stream());
-    if (e != hipSuccess) return fail("stream begin", e) ? 1 : 0;
+    if (!pin_copy(g_str.d_resid, g_str.h_x, (size_t)D * 4, stream(), "stream begin")) return 0;
     g_str.D = D;
     g_str.live = 1;
     g_str.pending = 0;
@@ -3201,6 +3201,20 @@ static bool stream_moe_ok(const char *who) {
     return err_report(who, le, le != 0 ? 0 : moe_error_take());
 }
 
+// stream_end's read-back as one launch into pinned memory: the error words (when checked)
+// at the head, then the fused layers' id history from ints kHistHead .. n.
+__global__ void stream_out(int *h, const int *dh, int n, const unsigned long long *l, const unsigned long long *m0,
+                           const unsigned long long *m1, int chk) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i == 0 && chk) {
+        unsigned long long *hw = (unsigned long long *)h;
+        hw[0] = l ? __hip_atomic_load(l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        hw[1] = m0 ? __hip_atomic_load(m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+        hw[2] = m1 ? __hip_atomic_load(m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+    }
+    for (int j = kHistHead + i; j < n; j += gridDim.x * blockDim.x) h[j] = dh[j];
+}
+
 COLI_API int coli_vk_stream_end(float *x, int D) {
     if (!g_str.live || D != g_str.D) return 0;
     if (!ok()) {   // disabled by an earlier failure: every later call returns 0
@@ -3213,9 +3227,15 @@ COLI_API int coli_vk_stream_end(float *x, int D) {
     const bool chk = !err_clean();
     int *dh = hist_dev();
     if (!dh || !host_scratch((void **)&g_str.h_rb, &g_str.hrb_cap, hist_ints() * 4)) return 0;
-    if (chk && !err_gather_launch((unsigned long long *)dh)) return 0;
-    const size_t nb = g_str.pending ? (kHistHead + (size_t)g_str.hist_hi * kTopK) * 4 : chk ? 24 : 0;
-    if (nb && hipMemcpyAsync(g_str.h_rb, dh, nb, hipMemcpyDeviceToHost, stream()) != hipSuccess) return 0;
+    const int n = g_str.pending ? kHistHead + g_str.hist_hi * kTopK : 0;
+    if (chk || n) {
+        const unsigned long long *m0, *m1;
+        moe_error_words(&m0, &m1);
+        hipLaunchKernelGGL(stream_out, dim3(1), dim3(256), 0, stream(), g_str.h_rb, (const int *)dh, n,
+                           (const unsigned long long *)g_lt.err, m0, m1, chk ? 1 : 0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail("stream end read-back", e) ? 1 : 0;
+    }
     if (!sync_stream("stream end")) return 0;   // the drain and the read-back
     if (chk && !stream_err_ok("stream end", (const unsigned long long *)g_str.h_rb)) {
         g_str.live = 0;
@@ -3278,7 +3298,7 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
         if (chk && !err_gather_launch(sl + kArgSlots)) return 0;
         if (!host_scratch((void **)&g_str.h_am, &g_str.ham_cap, (kArgSlots + 3) * 8)) return 0;
         unsigned long long *hb = g_str.h_am;
-        if (hipMemcpyAsync(hb, sl, (kArgSlots + (chk ? 3 : 0)) * 8, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+        if (!pin_copy(hb, sl, (kArgSlots + (chk ? 3 : 0)) * 8, stream(), "stream_norm_argmax") ||
             !sync_stream("stream_norm_argmax"))
             return 0;
         if (chk && !stream_err_ok("stream_norm_argmax", hb + kArgSlots)) return 0;
