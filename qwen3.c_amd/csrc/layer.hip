@@ -2512,6 +2512,16 @@ struct StreamState {
     size_t hx_cap = 0;
 };
 static StreamState g_str;
+// stream_norm_argmax's work launched ahead by stream_end (see ahead_launch)
+struct AheadArgmax {
+    const ColiVkTensor *t = nullptr;   // the last stream_norm_argmax's tensor (NULL: none yet)
+    const uint8_t *w = nullptr;
+    int fmt = 0, I = 0, O = 0, gs = 0;
+    float eps = 0.f;
+    bool pending = false;              // launched by stream_end, not yet taken
+    uint32_t ep = 0;                   // its launch tag
+};
+static AheadArgmax g_ahead;
 
 float *stream_resid(int D) { return g_str.live && g_str.D == D ? g_str.d_resid : nullptr; }
 const float *stream_nrm_dev(int D) {
@@ -2560,6 +2570,7 @@ void layer_shutdown() {
     host_scratch_free((void **)&g_str.h_rb, &g_str.hrb_cap);
     host_scratch_free((void **)&g_str.h_am, &g_str.ham_cap);
     g_str = StreamState();
+    g_ahead = AheadArgmax();
 }
 
 }  // namespace coli
@@ -3118,6 +3129,7 @@ static size_t hist_ints() { return kHistHead + (size_t)kMaxLayers * kTopK; }
 static int *hist_dev() { return (int *)wbuf(W_HIST, hist_ints()); }
 
 COLI_API int coli_vk_stream_begin(const float *x, int D) {
+    g_ahead.pending = false;   // a new token: the lm_head launched ahead is not wanted
     if (!ok() || !x || D < 1) return 0;
     // the row goes through pinned staging and a copy kernel: the token's first launches
     // queue behind it at once (a hipMemcpyAsync held the host ~15 us while the device sat
@@ -3201,6 +3213,39 @@ static bool stream_moe_ok(const char *who) {
     return err_report(who, le, le != 0 ? 0 : moe_error_take());
 }
 
+// The lm_head launched ahead.  The engine follows stream_end(NULL) with stream_norm_argmax
+// on its lm_head (c/qwen.c:1282, 1437-1441).  stream_end issues that call's work (the final
+// norm in the GEMV's prologue, the argmax keys, their copy to pinned memory) before it
+// waits, with the arguments of the last stream_norm_argmax, so the device goes on from the
+// last layer into the lm_head while the host returns and calls again.  stream_norm_argmax
+// then only waits and decodes when its arguments are those; otherwise the keys are
+// dropped and it runs as usual.  The residual and the final norm weight cannot change in
+// between (stream_begin and coli_vk_final_norm_weight drop the launch); a tensor's weights
+// stay where they are (the arena frees nothing), and its handle, weights and shape are
+// compared.
+static bool ahead_match(const ColiVkTensor *t, int fmt, int I, int O, int gs, float eps) {
+    return g_ahead.t && t == g_ahead.t && tensor_live(t) && t->w == g_ahead.w && t->layout == kLayoutLanes &&
+           t->fmt == fmt && t->I == I && t->O == O && t->gs == gs && fmt == g_ahead.fmt && I == g_ahead.I &&
+           O == g_ahead.O && gs == g_ahead.gs && eps == g_ahead.eps;
+}
+// stream_end's launch of the next stream_norm_argmax (false only on a runtime error)
+static bool ahead_launch() {
+    g_ahead.pending = false;
+    const ColiVkTensor *t = g_ahead.t;
+    if (!t || !ahead_match(t, g_ahead.fmt, g_ahead.I, g_ahead.O, g_ahead.gs, g_ahead.eps) || !g_str.d_fnw ||
+        g_str.fn_D != t->I || g_str.D != t->I || t->O >= (1 << 24))
+        return true;
+    if (!host_scratch((void **)&g_str.h_am, &g_str.ham_cap, (kArgSlots + 3) * 8)) return false;
+    uint32_t ep;
+    unsigned long long *sl;
+    if (!gemv_argmax(t, g_str.d_resid, nullptr, stream(), &ep, &sl, g_str.d_fnw, g_ahead.eps) ||
+        !pin_copy(g_str.h_am, sl, kArgSlots * 8, stream(), "stream end (lm_head ahead)"))
+        return false;
+    g_ahead.pending = true;
+    g_ahead.ep = ep;
+    return true;
+}
+
 // stream_end's read-back as one launch into pinned memory: the error words (when checked)
 // at the head, then the fused layers' id history from ints kHistHead .. n.
 __global__ void stream_out(int *h, const int *dh, int n, const unsigned long long *l, const unsigned long long *m0,
@@ -3236,6 +3281,7 @@ COLI_API int coli_vk_stream_end(float *x, int D) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail("stream end read-back", e) ? 1 : 0;
     }
+    if (!x && !ahead_launch()) return 0;        // the residual stays on the device: the lm_head next
     if (!sync_stream("stream end")) return 0;   // the drain and the read-back
     if (chk && !stream_err_ok("stream end", (const unsigned long long *)g_str.h_rb)) {
         g_str.live = 0;
@@ -3275,6 +3321,7 @@ COLI_API int coli_vk_stream_copy_resid(float *x, int D) {
 
 // c/backend_vulkan.c:2692-2711
 COLI_API int coli_vk_final_norm_weight(const float *w, int D) {
+    g_ahead.pending = false;
     if (!ok() || !w || D < 1) return 0;
     if (!scratch((void **)&g_str.d_fnw, &g_str.fnw_cap, (size_t)D * 4)) return 0;
     if (!h2d(g_str.d_fnw, w, (size_t)D * 4, "final norm weight")) return 0;
@@ -3288,12 +3335,28 @@ COLI_API int coli_vk_stream_norm_argmax(ColiVkTensor **tensor, const void *weigh
                                         int I, int O, int gs, float eps, int *idx, float *val) {
     if (!ok() || !g_str.d_fnw || g_str.fn_D != I || !g_str.d_resid || g_str.D != I || O < 1 || !idx) return 0;
     if (!coli_vk_tensor_ensure(tensor, weights, scales, fmt, I, O, gs)) return 0;
+    const bool ahead = g_ahead.pending && ahead_match(*tensor, fmt, I, O, gs, eps) && err_clean();
+    g_ahead.pending = false;
+    if (ahead) {   // stream_end launched this call's work: wait for its keys
+        int i;
+        float v;
+        if (!sync_stream("stream_norm_argmax") || !argmax_decode_host(g_str.h_am, g_ahead.ep, &i, &v) || i < 0 ||
+            i >= O)
+            return 0;
+        *idx = i;
+        if (val) *val = v;
+        return 1;
+    }
     if ((*tensor)->layout == kLayoutLanes && O < (1 << 24)) {
         // one launch: the norm in the GEMV's x prologue, argmax keys, and the error words
         // gathered after the keys; the host decodes the keys from the one read-back
         uint32_t ep;
         unsigned long long *sl;
         if (!gemv_argmax(*tensor, g_str.d_resid, nullptr, stream(), &ep, &sl, g_str.d_fnw, eps)) return 0;
+        g_ahead = AheadArgmax();   // the arguments for stream_end's next launch ahead
+        g_ahead.t = *tensor;
+        g_ahead.w = (*tensor)->w;
+        g_ahead.fmt = fmt, g_ahead.I = I, g_ahead.O = O, g_ahead.gs = gs, g_ahead.eps = eps;
         const bool chk = !err_clean();
         if (chk && !err_gather_launch(sl + kArgSlots)) return 0;
         if (!host_scratch((void **)&g_str.h_am, &g_str.ham_cap, (kArgSlots + 3) * 8)) return 0;

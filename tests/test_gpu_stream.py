@@ -80,6 +80,61 @@ def test_stream_norm_argmax_cfg1(lib, orc_omp, gen):
         assert io2 == lo
 
 
+def test_stream_norm_argmax_ahead(lib, orc_omp, gen):
+    """stream_end(NULL) launches the next stream_norm_argmax's work ahead, with the last
+    call's arguments (the engine's order, c/qwen.c:1282, 1437-1441).  Tokens in that order
+    get the oracle's winners; so do calls with other arguments right after such a launch
+    (another tensor, another eps), a token begun again without its argmax, and a call after
+    the final norm weight changed."""
+    O, I, gs, eps = 65536, 2048, 128, 1e-6
+    q, sz = gen.fmt6(O, I, gs, 0xA1)
+    q2, sz2 = gen.fmt6(O, I, gs, 0xA2)
+    fnw = gen.normal(I, 0xA3, 0.1)
+    lib.final_norm_weight(fnw)
+    t, t2 = lib.tensor(q, sz, 6, I, O, gs), lib.tensor(q2, sz2, 6, I, O, gs)
+
+    def check(tag, resid, w, tq, tsz, e, idx, val):
+        y, io = _final(lib, gen, orc_omp, resid, w, tq, tsz, O, I, gs, e)
+        tol = 2e-4 * float(np.abs(y).max())
+        print(f"ahead {tag}: device {idx} ({val:.6f}), oracle {io} ({y[io]:.6f})", flush=True)
+        assert 0 <= idx < O and abs(val - float(y[idx])) <= tol, tag
+        if idx != io:
+            assert abs(float(y[idx]) - float(y[io])) <= tol, (tag, idx, io)
+
+    plan = [("first", t, q, sz, eps), ("same", t, q, sz, eps), ("same", t, q, sz, eps),
+            ("other tensor", t2, q2, sz2, eps), ("same", t2, q2, sz2, eps), ("other eps", t2, q2, sz2, 1e-5),
+            ("back", t, q, sz, eps), ("same", t, q, sz, eps)]
+    for k, (tag, tt, tq, tsz, e) in enumerate(plan):
+        resid = gen.normal(I, 0xA10 + k, 3.0)
+        lib.stream_begin(resid)
+        lib.stream_end(I, read=False)
+        idx, val = lib.stream_norm_argmax(tt, e)
+        check(tag, resid, fnw, tq, tsz, e, idx, val)
+    # a token begun again before its argmax: the launch ahead is dropped
+    lib.stream_begin(gen.normal(I, 0xA20, 3.0))
+    lib.stream_end(I, read=False)
+    resid = gen.normal(I, 0xA21, 3.0)
+    lib.stream_begin(resid)
+    lib.stream_end(I, read=False)
+    idx, val = lib.stream_norm_argmax(t, eps)
+    check("begun again", resid, fnw, q, sz, eps, idx, val)
+    # the final norm weight replaced between stream_end and the argmax
+    resid = gen.normal(I, 0xA22, 3.0)
+    lib.stream_begin(resid)
+    lib.stream_end(I, read=False)
+    fnw2 = gen.normal(I, 0xA23, 0.1)
+    lib.final_norm_weight(fnw2)
+    idx, val = lib.stream_norm_argmax(t, eps)
+    check("new norm weight", resid, fnw2, q, sz, eps, idx, val)
+    # the residual read back at stream_end: no launch ahead, the call runs as usual
+    resid = gen.normal(I, 0xA24, 3.0)
+    lib.stream_begin(resid)
+    got = lib.stream_end(I, read=True)
+    assert np.array_equal(got, resid)
+    idx, val = lib.stream_norm_argmax(t, eps)
+    check("resid read", resid, fnw2, q, sz, eps, idx, val)
+
+
 # ---------------------------------------------------------------- int8 router and GDN a/b
 SMALL = dict(gqa=dict(H=4, KH=2, hd=64, rot=16, gs=64), gdn=dict(KH=2, KD=64, VH=4, VD=32, K=4, gs=64))
 
