@@ -3223,6 +3223,9 @@ static bool stream_moe_ok(const char *who) {
 // between (stream_begin and coli_vk_final_norm_weight drop the launch); a tensor's weights
 // stay where they are (the arena frees nothing), and its handle, weights and shape are
 // compared.
+void coli::stream_tensor_freed(const ColiVkTensor *t) {
+    if (t && t == g_ahead.t) g_ahead = AheadArgmax();   // a launch in flight reads arena memory, never freed
+}
 static bool ahead_match(const ColiVkTensor *t, int fmt, int I, int O, int gs, float eps) {
     return g_ahead.t && t == g_ahead.t && tensor_live(t) && t->w == g_ahead.w && t->layout == kLayoutLanes &&
            t->fmt == fmt && t->I == I && t->O == O && t->gs == gs && fmt == g_ahead.fmt && I == g_ahead.I &&

@@ -634,6 +634,7 @@ COLI_API int coli_vk_tensor_ensure(ColiVkTensor **tensor, const void *weights, c
 // generation was already uncounted by the shutdown).
 COLI_API void coli_vk_tensor_free(ColiVkTensor *t) {
     if (!t) return;
+    stream_tensor_freed(t);
     if (t->gen == G.gen) {
         G.used_bytes -= t->bytes;
         G.tensor_count--;

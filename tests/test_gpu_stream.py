@@ -14,6 +14,8 @@ the oracle's; the argmax equal to the oracle's unless the two logits lie within 
 tolerance of each other (then the device's pick must be exact on the oracle's logits up to
 that tolerance).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -133,6 +135,16 @@ def test_stream_norm_argmax_ahead(lib, orc_omp, gen):
     assert np.array_equal(got, resid)
     idx, val = lib.stream_norm_argmax(t, eps)
     check("resid read", resid, fnw2, q, sz, eps, idx, val)
+    # the lm_head handle freed after a launch ahead (the library forgets it; the launch read
+    # arena memory, which is never reused), then a new handle of other weights
+    resid = gen.normal(I, 0xA25, 3.0)
+    lib.stream_begin(resid)
+    lib.stream_end(I, read=False)
+    lib.L.coli_vk_tensor_free(t.handle)
+    t.handle = ctypes.c_void_p(None)
+    t3 = lib.tensor(q2, sz2, 6, I, O, gs)
+    idx, val = lib.stream_norm_argmax(t3, eps)
+    check("freed handle", resid, fnw2, q2, sz2, eps, idx, val)
 
 
 # ---------------------------------------------------------------- int8 router and GDN a/b
