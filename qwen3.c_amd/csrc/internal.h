@@ -67,8 +67,8 @@ struct Upload {
 bool upload(const Upload *u, int nu, hipStream_t st, const char *who);
 // a tensor handle is about to be freed: the decode stream drops what it kept of it (layer.hip)
 void stream_tensor_freed(const ColiVkTensor *t);
-// n bytes (n % 4 == 0) between device memory and pinned host memory (host_scratch) as a
-// copy kernel on `st`: the launch returns at once (runtime.hip)
+// n bytes between device memory and pinned host memory (host_scratch) as a copy kernel on
+// `st`: the launch returns at once (runtime.hip)
 bool pin_copy(void *dst, const void *src, size_t n, hipStream_t st, const char *who);
 // The pieces of a read-back already issued into pinned memory: record one event per piece
 // after issuing it, then copy_out waits for each in turn and copies it out.

@@ -139,11 +139,11 @@ bool sync_stream(const char *who) {
 
 // ---------------------------------------------------------------- pinned <-> device copies
 // Transfers between device memory and pinned host memory (hipHostMalloc: mapped into the
-// device's address space) run as this kernel, one launch per piece: the launch returns at
+// device's address space) run as these kernels, one launch per piece: the launch returns at
 // once, where a hipMemcpyAsync between them held the host thread for about as long as the
 // transfer (the runtime's own blit kernel), so the pieces went out one at a time.  16-byte
-// words when both ends are 16-byte aligned, else 4-byte words (every transfer here is of
-// floats or ints).
+// words when both ends and the size are 16-byte aligned, else 4-byte words when they are
+// 4-byte aligned (every transfer here is of floats or ints), else bytes.
 __global__ void pin_copy16(uint4 *__restrict__ d, const uint4 *__restrict__ s, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         d[i] = s[i];
@@ -152,17 +152,22 @@ __global__ void pin_copy4(uint32_t *__restrict__ d, const uint32_t *__restrict__
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         d[i] = s[i];
 }
+__global__ void pin_copy1(uint8_t *__restrict__ d, const uint8_t *__restrict__ s, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
 
 bool pin_copy(void *dst, const void *src, size_t n, hipStream_t st, const char *who) {
     if (!n) return true;
-    if (n % 4) return fail(who, hipErrorInvalidValue);
-    const bool w16 = !(((uintptr_t)dst | (uintptr_t)src | n) & 15);
-    const size_t words = w16 ? n / 16 : n / 4;
+    const uintptr_t al = (uintptr_t)dst | (uintptr_t)src | n;
+    const size_t w = (al & 15) == 0 ? 16 : (al & 3) == 0 ? 4 : 1, words = n / w;
     const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
-    if (w16)
+    if (w == 16)
         hipLaunchKernelGGL(pin_copy16, dim3(blocks), dim3(256), 0, st, (uint4 *)dst, (const uint4 *)src, words);
-    else
+    else if (w == 4)
         hipLaunchKernelGGL(pin_copy4, dim3(blocks), dim3(256), 0, st, (uint32_t *)dst, (const uint32_t *)src, words);
+    else
+        hipLaunchKernelGGL(pin_copy1, dim3(blocks), dim3(256), 0, st, (uint8_t *)dst, (const uint8_t *)src, words);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(who, e);
     return true;
