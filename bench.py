@@ -677,7 +677,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the fmt=6 GEMV/MoE path runs on a single "
-              "MI355X; see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+              "MI355X); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch  # plumbing: device buffers and event timing (imported before the library)

@@ -69,3 +69,16 @@ def test_reference_engine_links():
                f"-L{os.path.dirname(LIB)}", "-lcoli_hip", "-lm"]
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 (or a WORLD_SIZE above 1) exits with status 2
+    and a message, before it touches a device."""
+    env = dict(os.environ, WORLD_SIZE="1")
+    r = subprocess.run(["python3", os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       env=env, timeout=120)
+    assert r.returncode == 2 and "one GPU only" in r.stderr
+    env["WORLD_SIZE"] = "2"
+    r = subprocess.run(["python3", os.path.join(ROOT, "bench.py")], capture_output=True, text=True, env=env,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU only" in r.stderr
