@@ -83,6 +83,22 @@ def test_moe_small(lib, orc, gen, torch_dev, small, K):
     assert lib.moe_error() == 0
 
 
+@pytest.mark.parametrize("D,I,E,gs", [(320, 192, 40, 64), (448, 384, 24, 64)])
+def test_moe_odd_geometry(lib, orc, gen, torch_dev, D, I, E, gs):
+    """Row widths that are not a power of two of lanes (D = 320 or 448: 5 or 7 lanes of a
+    gate/up row; I = 192 or 384: 3 or 6 lanes of a down row), so the tiles carry padding
+    lanes, against the oracle."""
+    import torch
+
+    L = Layer(lib, gen, 0x0DD0 + D, D, I, E, gs)
+    Table(lib, [L]).activate()
+    for K in (3, 8):
+        for t in range(3):
+            x = gen.normal(D, 0x0DE0 + 16 * K + t)
+            check(orc, L, K, x, run_moe(lib, torch, torch_dev, 0, L, K, x))
+    assert lib.moe_error() == 0
+
+
 def test_moe_accumulate(lib, orc, gen, torch_dev, small):
     """accumulate=1: out = resid + moe (the residual-stream form)."""
     import torch

@@ -48,6 +48,17 @@ def test_prefill_small(lib, orc, gen, torch_dev, S, K):
     check(orc, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S))
 
 
+@pytest.mark.parametrize("S,K", [(37, 6), (130, 8)])
+def test_prefill_odd_geometry(lib, orc, gen, torch_dev, S, K):
+    """Hidden and intermediate sizes of 3 groups (D = I = 384): supersteps of 4 groups with
+    one missing, and a token count that leaves partial 16- and 32-row tiles."""
+    import torch
+    L = Layer(lib, gen, 0x9F8, 384, 384, 24, 128)
+    Table(lib, [L]).activate()
+    xs = gen.normal(S * L.D, 0x9F9 + S)
+    check(orc, L, K, xs, S, run_prefill(lib, torch, torch_dev, L, K, xs, S))
+
+
 @pytest.mark.parametrize("S", [1, 64, 200])
 def test_prefill_router_int8(lib, orc, gen, torch_dev, S):
     """fmt 1 router: int8 rows, the per-row scale applied after the dot (c/qwen.c:230-238)."""
