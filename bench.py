@@ -117,7 +117,8 @@ def gemv_cfg0(lib, torch, dev, steps, warmup):
     overhead); back to back (launches over 64 weight copies, 303 MB, more than the 256 MB
     Infinity Cache, so the weights stream from HBM); and sustained as one multi-matvec
     launch: 64 distinct 4096 x 2048 matrices stored back to back in one 262144-row tensor,
-    each applied to the same x in one GEMV launch (BASELINE.md's multi-matvec form)."""
+    each applied to the same x in one GEMV launch (a multi-matvec persistent launch: one
+    4.7 MB matrix is shorter than a launch at peak bandwidth)."""
     O, K = 4096, 2048
     ncopy = 64
     ws = [lib.tensor_synth(6, K, O, GS, 0xC0 * 1000 + c, 0.02) for c in range(ncopy)]
