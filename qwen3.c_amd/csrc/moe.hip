@@ -34,7 +34,7 @@
 namespace coli {
 
 constexpr int kRRows = kWaves;            // router rows per tile (one per wave)
-constexpr int kGSteps = 2;                // gate/up row steps per tile
+constexpr int kGSteps = 1;                // gate/up row steps per tile
 constexpr int kRouteReps = 4;             // copies of the route block (readers spread over them)
 constexpr int kRouteStride = 32;          // words per copy: idx [K] | w [K + 1] | ... | prov [K], K <= 8
 constexpr int kProvOff = 24;              // the provisional ids' words within a copy
@@ -545,7 +545,7 @@ __device__ __forceinline__ void tile_dslot(const MoeArgs &a, HPrep &H, int slot,
     down_slot<TPR>(a.g, s_rec[0], H, r0, gather, [&](int r, float y) { tag_put(&ys[r], ep, y); });
 }
 
-constexpr int kCRows = 64;   // combine tile rows (one thread each)
+constexpr int kCRows = 256;  // combine tile rows (one thread each)
 __device__ __forceinline__ void tile_combine(const MoeArgs &a, int r0, float *s_w) {
     const int tid = threadIdx.x, K = a.K, NS = K + 1, D = a.g.D;
     const unsigned long long *route = route_of(a, blockIdx.x % kRouteReps);
